@@ -1,0 +1,318 @@
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+Metric: paged decode-attention HBM GB/s (% of the 8 TB/s peak)
+plus KV-append tokens/s, 1 GPU.
+
+Workload of `value` (one "step" = one decode pass over one batch): FP8 E4M3 KV
+paged decode, batch 64, every row at context 32768, 24 query / 4 KV heads,
+head_dim 256, page 16, split-K + combine — the north-star point. Inputs are
+synthetic (seeded random codes/scales/queries) and resident in HBM before the
+timed region. Algorithmic bytes per step = sum over rows of ctx * 2080.25 B
+(K+V codes 2*4*256, K+V scales 2*4*4, 1/16 of a 4 B block-table entry) plus
+the query rows (24*256*2 B each).
+
+Extra lines inside the same JSON object: BASELINE config 4 (log-uniform
+contexts) and config 3 (BF16 KV), and KV append at config 2 (128 rows) and at
+2^16 rows, each with kernel times from HIP events on the launch stream.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+BYTES_PER_TOKEN_FP8 = 2 * 4 * 256 + 2 * 4 * 4 + 4 / 16      # 2080.25
+BYTES_PER_TOKEN_BF16 = 2 * 4 * 256 * 2 + 4 / 16              # 4096.25
+APPEND_BYTES_PER_ROW_FP8 = 2 * 4 * 256 * 2 + 8 + 4 + 2 * 4 * 256 + 2 * 4 * 4   # 6188
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP-event timing on the stream the kernels are launched on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.s = torch.cuda.Event(enable_timing=True)
+        self.e = torch.cuda.Event(enable_timing=True)
+
+    def __enter__(self):
+        self.s.record()
+        return self
+
+    def __exit__(self, *a):
+        self.e.record()
+
+    def ms(self):
+        self.e.synchronize()
+        return self.s.elapsed_time(self.e)
+
+
+def decode_setup(torch, ops, lens, fp8, seed, dev):
+    rows = len(lens)
+    P, H, D, QH = 16, 4, 256, 24
+    rng = np.random.default_rng(seed)
+    need = [(int(n) + P - 1) // P for n in lens]
+    num_pages = sum(need)
+    stride = max(need)
+    perm = torch.from_numpy(rng.permutation(num_pages).astype(np.int32))
+    bt = torch.full((rows, stride), -1, dtype=torch.int32)
+    k = 0
+    for r, n in enumerate(need):
+        bt[r, :n] = perm[k:k + n]
+        k += n
+    g = ops.PoolGeometry(1, num_pages, P, H, D)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    if fp8:
+        kp = torch.randint(0, 126, (g.pool_elems,), generator=gen, device=dev,
+                           dtype=torch.int32).to(torch.uint8)
+        vp = torch.randint(0, 126, (g.pool_elems,), generator=gen, device=dev,
+                           dtype=torch.int32).to(torch.uint8)
+        ks = torch.rand(g.scale_elems, generator=gen, device=dev) * 0.02 + 1e-3
+        vs = torch.rand(g.scale_elems, generator=gen, device=dev) * 0.02 + 1e-3
+    else:
+        kp = torch.randn(g.pool_elems, generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+        vp = torch.randn(g.pool_elems, generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+        ks = vs = None
+    q = torch.randn((rows, QH * D), generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+    out = torch.empty((rows, QH * D), dtype=torch.bfloat16, device=dev)
+    slots = torch.arange(rows, dtype=torch.int32, device=dev)
+    pos = torch.tensor(np.asarray(lens) - 1, dtype=torch.int32, device=dev)
+    return dict(g=g, kp=kp, vp=vp, ks=ks, vs=vs, q=q, out=out, slots=slots, pos=pos,
+                bt=bt.to(dev), lens=np.asarray(lens), fp8=fp8, QH=QH)
+
+
+def choose_splits(lens, kv_heads=4, target_wgs=2048, min_pages=16):
+    """Pages per split so that rows*kv_heads*splits ~ target_wgs (>= 8 WGs per CU)."""
+    pages = np.ceil(np.asarray(lens) / 16).astype(int)
+    total = int(pages.sum()) * kv_heads
+    per = max(min_pages, int(math.ceil(total / target_wgs)))
+    splits = int(math.ceil(pages.max() / per))
+    return splits, per
+
+
+def run_decode(torch, ops, st, steps, warmup, dev, splits=None, pps=None):
+    """Returns (step_ms, split_kernel_ms, reduce_ms, bytes)."""
+    import ctypes as C
+    from phaseshift_amd import lib, check
+    g, lens = st["g"], st["lens"]
+    if splits is None:
+        splits, pps = choose_splits(lens)
+    rows = len(lens)
+    a = ops.attention_args(g, 0, st["q"], st["out"], st["slots"], st["pos"], st["bt"], st["QH"])
+    nbytes = ops.split_partials_bytes(rows, st["QH"], g.kv_heads, splits)
+    partials = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    L = lib()
+    s = torch.cuda.current_stream().cuda_stream
+    kp, vp = st["kp"].data_ptr(), st["vp"].data_ptr()
+
+    def split_launch():
+        if st["fp8"]:
+            check("split", L.psk_attention_paged_fp8_e4m3_split(
+                C.byref(a), kp, vp, st["ks"].data_ptr(), st["vs"].data_ptr(),
+                partials.data_ptr(), splits, pps, s))
+        else:
+            check("split", L.psk_attention_paged_bf16_split_ex(
+                C.byref(a), kp, vp, partials.data_ptr(), splits, pps, s))
+
+    def reduce_launch():
+        check("reduce", L.psk_attention_paged_split_reduce_ex(C.byref(a), partials.data_ptr(),
+                                                              splits, pps, s))
+
+    for _ in range(warmup):
+        split_launch()
+        reduce_launch()
+    torch.cuda.synchronize()
+    # step time: K back-to-back steps
+    t = Timer(torch)
+    with t:
+        for _ in range(steps):
+            split_launch()
+            reduce_launch()
+    step_ms = t.ms() / steps
+    # per-kernel durations: events bracketing each launch on the same stream
+    sk, rk = [], []
+    for _ in range(steps):
+        t1 = Timer(torch)
+        with t1:
+            split_launch()
+        t2 = Timer(torch)
+        with t2:
+            reduce_launch()
+        sk.append(t1.ms())
+        rk.append(t2.ms())
+    per_tok = BYTES_PER_TOKEN_FP8 if st["fp8"] else BYTES_PER_TOKEN_BF16
+    nbytes_alg = float(lens.sum()) * per_tok + rows * st["QH"] * 256 * 2
+    return step_ms, float(np.mean(sk)), float(np.mean(rk)), nbytes_alg, splits, pps
+
+
+def run_append(torch, ops, rows, steps, warmup, dev, seed=7):
+    H, D, P = 4, 256, 16
+    rng = np.random.default_rng(seed)
+    seqs = max(1, rows // P)
+    g = ops.PoolGeometry(1, seqs + 16, P, H, D)
+    bt = torch.from_numpy(rng.permutation(seqs + 16)[:seqs].astype(np.int32).reshape(seqs, 1)).to(dev)
+    slots = torch.from_numpy(np.repeat(np.arange(seqs), P)[:rows].astype(np.int32)).to(dev)
+    pos = torch.from_numpy(np.tile(np.arange(P), seqs)[:rows].astype(np.int32)).to(dev)
+    perm = torch.from_numpy(rng.permutation(rows)).to(dev)
+    slots, pos = slots[perm].contiguous(), pos[perm].contiguous()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    k = torch.randn((rows, H * D), generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+    v = torch.randn((rows, H * D), generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+    kp = torch.empty(g.pool_elems, dtype=torch.uint8, device=dev)
+    vp = torch.empty_like(kp)
+    ks = torch.empty(g.scale_elems, dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+
+    def launch():
+        ops.kv_append(g, 0, k, v, slots, pos, bt, kp, vp, ks, vs)
+
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(steps):
+        t = Timer(torch)
+        with t:
+            launch()
+        times.append(t.ms())
+    ms = float(np.mean(times))
+    return ms, rows * APPEND_BYTES_PER_ROW_FP8
+
+
+def cpu_baseline(lens_row, seconds_cap=30.0):
+    """Scalar C oracle (1 thread) on a bounded sample of the same workload:
+    FP8 decode of whole rows at context 32768, until ~10 s of CPU work."""
+    import oracle
+    P, H, D, QH = 16, 4, 256, 24
+    ctx = int(lens_row)
+    rng = np.random.default_rng(5)
+    need = (ctx + P - 1) // P
+    num_pages = need
+    bt = rng.permutation(num_pages).astype(np.uint32).reshape(1, need)
+    n = num_pages * P * H * D
+    kp = rng.integers(0, 126, n, dtype=np.uint8)
+    vp = rng.integers(0, 126, n, dtype=np.uint8)
+    ks = rng.uniform(1e-3, 2e-2, num_pages * P * H).astype(np.float32)
+    vs = rng.uniform(1e-3, 2e-2, num_pages * P * H).astype(np.float32)
+    geom = dict(layer=0, page_tokens=P, num_pages=num_pages, num_attention_layers=1,
+                kv_heads=H, head_dim=D, block_table_stride=need, max_sequences=1, q_heads=QH)
+    q = oracle.f32_to_bf16(rng.standard_normal((1, QH * D)).astype(np.float32))
+    done, t0 = 0, time.perf_counter()
+    while True:
+        oracle.paged_attention(geom, q, [0], [ctx - 1], bt, kp, vp, ks, vs, 1 / 16)
+        done += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or el > seconds_cap:
+            break
+    gbps = done * ctx * BYTES_PER_TOKEN_FP8 / el / 1e9
+    return dict(value=round(gbps, 4), unit="GB/s", cores=1, kind="port",
+                sample=f"{done} row(s) of FP8 decode at ctx {ctx}, 24q/4kv, hd256, scalar C "
+                       f"oracle (two-pass fp32 softmax), {el:.1f} s")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the KV path needs no collective; "
+              "sharding is by KV head / batch row, see DESIGN.md); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from phaseshift_amd import ops
+    dev = torch.device("cuda:0")
+    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append"}
+    extra = {}
+
+    # ---- main: north-star point, FP8 batch 64 @ 32k
+    st = decode_setup(torch, ops, [32768] * 64, True, 11, dev)
+    torch.cuda.synchronize()
+    step_ms, k_ms, r_ms, nbytes, splits, pps = run_decode(torch, ops, st, args.steps, args.warmup,
+                                                          dev)
+    value = nbytes / (step_ms * 1e-3) / 1e9
+    achieved = nbytes / (k_ms * 1e-3) / 1e9
+    del st
+    torch.cuda.empty_cache()
+
+    if "cfg4" in only:
+        rng = np.random.default_rng(404)
+        lens = np.exp(rng.uniform(np.log(4096), np.log(65536), 64)).astype(np.int64)
+        st = decode_setup(torch, ops, lens, True, 404, dev)
+        s_ms, k4, r4, nb4, sp4, pp4 = run_decode(torch, ops, st, args.steps, args.warmup, dev)
+        extra["cfg4_fp8_decode_loguniform"] = dict(
+            GBps=round(nb4 / (s_ms * 1e-3) / 1e9, 1), ms_per_step=round(s_ms, 4),
+            split_kernel_ms=round(k4, 4), reduce_ms=round(r4, 4), splits=sp4, pages_per_split=pp4,
+            frac_of_peak=round(nb4 / (s_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+        del st
+        torch.cuda.empty_cache()
+    if "cfg3" in only:
+        rng = np.random.default_rng(303)
+        lens = rng.integers(1024, 32769, 32)
+        st = decode_setup(torch, ops, lens, False, 303, dev)
+        s_ms, k3, r3, nb3, sp3, pp3 = run_decode(torch, ops, st, args.steps, args.warmup, dev)
+        extra["cfg3_bf16_decode"] = dict(
+            GBps=round(nb3 / (s_ms * 1e-3) / 1e9, 1), ms_per_step=round(s_ms, 4),
+            split_kernel_ms=round(k3, 4), reduce_ms=round(r3, 4), splits=sp3, pages_per_split=pp3,
+            frac_of_peak=round(nb3 / (s_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+        del st
+        torch.cuda.empty_cache()
+    if "append" in only:
+        ap = {}
+        for rows in (128, 1 << 16):
+            ms, nb = run_append(torch, ops, rows, args.steps, args.warmup, dev)
+            ap[f"rows_{rows}"] = dict(tokens_per_s=round(rows / (ms * 1e-3), 1),
+                                      kernel_ms=round(ms, 5),
+                                      GBps=round(nb / (ms * 1e-3) / 1e9, 1),
+                                      frac_of_peak=round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+        extra["kv_append_fp8"] = ap
+
+    cpu = None if args.no_cpu else cpu_baseline(32768)
+    line = {
+        "metric": "paged decode-attn HBM GB/s (% of 8 TB/s peak) + KV-append tokens/s, 1 GPU",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 KV, bf16 Q, fp32 accumulate",
+        "data": "synthetic (seeded random FP8 codes/scales and bf16 queries)",
+        "config": {"workload": "paged decode, FP8 E4M3 KV, batch 64, ctx 32768 each, 24 q / 4 kv "
+                               "heads, head_dim 256, page 16, split-K + combine",
+                   "splits": splits, "pages_per_split": pps, "frac_of_peak":
+                       round(value / HBM_PEAK_GBPS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "kernel": "paged_decode_kernel<1,256> (FP8 split)",
+                     "kernel_ms": round(k_ms, 5), "reduce_ms": round(r_ms, 5),
+                     "bytes_per_launch": nbytes},
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

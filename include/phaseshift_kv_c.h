@@ -1,0 +1,256 @@
+/*
+ * phaseshift_kv_c.h — C-ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * Plain C: pointers, sizes, POD structs. No HIP or torch types appear in any
+ * signature: a stream is passed as `void*` (a hipStream_t, NULL = default
+ * stream) and every entry point returns an `int` that holds a hipError_t value
+ * (0 = hipSuccess, 1 = hipErrorInvalidValue, 801 = hipErrorNotSupported).
+ *
+ * The argument structs are byte-for-byte the reference's launcher structs, so
+ * a caller that already fills those can pass their address here unchanged:
+ *   psk_kv_append_args      == ps::kernel::KvAppendCommonArgs
+ *       (reference include/phaseshift/models/qwen35/kernels/optimized/kv_append.h:12-41,
+ *        96 B, asserted :52-72)
+ *   psk_paged_attention_args == ps::kernel::PagedAttentionCommonArgs
+ *       (reference include/phaseshift/models/qwen35/kernels/optimized/attention/
+ *        paged_attention.h:42-78, 112 B, asserted :86-109)
+ *
+ * Semantics shared by every entry point (reference file:line in brackets):
+ *  - KV pool element index: layer*elems_per_layer + page*elems_per_page
+ *    + slot*elems_per_token + kv_head*head_dim + d
+ *    [state/paged_kv_pool.cpp:64-69, kernels/optimized/kv_append.hip:47-49].
+ *  - FP8 scale index: ((layer*num_pages + page)*page_tokens + slot)*kv_heads + kv_head
+ *    [kv_append.hip:230-231].
+ *  - Block table: uint32 [max_sequences][block_table_stride]; 0xFFFFFFFF = empty
+ *    [state/paged_types.h:12]. A page id >= num_pages is invalid.
+ *  - Row r attends to positions [0, row_positions[r]] inclusive
+ *    [kernels/optimized/attention/paged_decode.hip:86-90].
+ *  - Launchers allocate nothing, never synchronise, and only enqueue on `stream`.
+ *  - Bad geometry / null pointers -> hipErrorInvalidValue; a shape no kernel
+ *    here handles -> hipErrorNotSupported; else the launch status.
+ *  - Data errors found on the device are silent: a row whose slot is invalid
+ *    is skipped; a row that meets an invalid page leaves its output unwritten.
+ */
+#ifndef PHASESHIFT_KV_C_H
+#define PHASESHIFT_KV_C_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PSK_INVALID_PAGE_ID 0xFFFFFFFFu
+
+/* KVCacheDType values [state/kv_cache_types.h:9-14]. */
+#define PSK_KV_BF16 0u
+#define PSK_KV_FP8_E4M3 1u
+
+/* PagedAttentionOutputDType values [paged_attention.h:37-40]. */
+#define PSK_OUT_BF16 0u
+#define PSK_OUT_F32 1u
+
+/* Same layout as ps::kernel::KvAppendCommonArgs (96 B, align 8). */
+typedef struct psk_kv_append_args {
+    const void* k_input;               /* bf16 [rows][k_row_stride] */
+    const void* v_input;               /* bf16 [rows][v_row_stride] */
+    uint32_t k_row_stride;             /* elements */
+    uint32_t v_row_stride;
+    const uint32_t* row_sequence_slots;
+    const uint32_t* row_positions;
+    const uint32_t* block_tables;
+    uint32_t block_table_stride;
+    uint32_t max_sequences;
+    uint32_t rows;
+    uint32_t layer;
+    uint32_t page_tokens;
+    uint32_t num_pages;
+    uint32_t num_attention_layers;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t elems_per_token;
+    uint32_t elems_per_page;
+    uint32_t elems_per_layer;
+} psk_kv_append_args;
+
+/* Same layout as ps::kernel::PagedAttentionCommonArgs (112 B, align 8). */
+typedef struct psk_paged_attention_args {
+    const void* q;                     /* bf16 [rows][q_row_stride] */
+    void* output;                      /* bf16 or f32 [rows][output_row_stride] */
+    uint8_t output_dtype;              /* PSK_OUT_BF16 / PSK_OUT_F32 */
+    uint32_t q_row_stride;
+    uint32_t output_row_stride;
+    const uint32_t* row_sequence_slots;
+    const uint32_t* row_positions;
+    const uint32_t* block_tables;
+    uint32_t block_table_stride;
+    uint32_t max_sequences;
+    uint32_t rows;
+    uint32_t layer;
+    uint32_t page_tokens;
+    uint32_t num_pages;
+    uint32_t num_attention_layers;
+    uint32_t q_heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t elems_per_token;
+    uint32_t elems_per_page;
+    uint32_t elems_per_layer;
+    float scale;
+} psk_paged_attention_args;
+
+/* Gather of paged KV back to contiguous [token][kv_heads*head_dim] rows.
+ * Sequence i contributes tokens [0, seq_lengths) of slot seq_slots[i], written
+ * to output rows [seq_token_offsets[i], seq_token_offsets[i+1]). No reference
+ * counterpart: the reference reads pools back on the host in its tests
+ * [tests/kernels/optimized/test_kv_append.hip:147-191]. */
+typedef struct psk_kv_gather_args {
+    const uint32_t* block_tables;
+    const uint32_t* seq_slots;         /* [num_seqs] */
+    const uint32_t* seq_token_offsets; /* [num_seqs + 1], exclusive prefix sum */
+    uint32_t block_table_stride;
+    uint32_t max_sequences;
+    uint32_t num_seqs;
+    uint32_t total_tokens;             /* == seq_token_offsets[num_seqs] */
+    uint32_t layer;
+    uint32_t page_tokens;
+    uint32_t num_pages;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t elems_per_token;
+    uint32_t elems_per_page;
+    uint32_t elems_per_layer;
+} psk_kv_gather_args;
+
+/* One page-copy job: copy page `src_page` of the source pools to page
+ * `dst_page` of the destination pools, every layer, K and V (and scales). */
+typedef struct psk_page_copy_pair {
+    uint32_t dst_page;
+    uint32_t src_page;
+} psk_page_copy_pair;
+
+typedef struct psk_page_copy_args {
+    void* dst_k;
+    void* dst_v;
+    float* dst_k_scale;                /* FP8 only, else NULL */
+    float* dst_v_scale;
+    const void* src_k;
+    const void* src_v;
+    const float* src_k_scale;
+    const float* src_v_scale;
+    const psk_page_copy_pair* pairs;   /* device array [num_pairs] */
+    uint32_t num_pairs;
+    uint32_t num_layers;
+    uint32_t dst_num_pages;
+    uint32_t src_num_pages;
+    uint32_t page_tokens;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t kv_dtype;                 /* PSK_KV_BF16 / PSK_KV_FP8_E4M3 */
+} psk_page_copy_args;
+
+/* Row metadata descriptor: same layout as ps::runtime::DeviceRequestDescriptor
+ * (64 B) [include/phaseshift/runtime/batch/device_batch_context.h:30-49]. */
+typedef struct psk_request_descriptor {
+    uint32_t slot;                     /* RequestHandle.slot */
+    uint32_t generation;               /* RequestHandle.generation */
+    uint32_t row_begin;
+    uint32_t row_count;
+    uint32_t prefix_length;
+    uint32_t sequence_length;
+    uint32_t output_index;
+    uint8_t execution_class;           /* 0 DECODE 1 SPEC_VERIFY 2 PREFILL 3 SPEC_DRAFT */
+    uint8_t compute_logits;
+    uint8_t output_count;
+    uint8_t reserved0;
+    uint8_t sampling[32];              /* DeviceSamplingParams, opaque here */
+} psk_request_descriptor;
+
+/* ---- KV append [kernels/optimized/kv_append.h:78-97] ---------------------- */
+int psk_kv_append_bf16(const psk_kv_append_args* a, void* k_pool, void* v_pool, void* stream);
+int psk_kv_append_fp8_e4m3(const psk_kv_append_args* a, void* k_pool, void* v_pool,
+                           float* k_scale_pool, float* v_scale_pool, void* stream);
+
+/* ---- Paged attention [attention/paged_attention.h:140-201] ---------------- */
+int psk_attention_paged_bf16(const psk_paged_attention_args* a, const void* k_pool,
+                             const void* v_pool, void* stream);
+int psk_attention_paged_fp8_e4m3(const psk_paged_attention_args* a, const void* k_pool,
+                                 const void* v_pool, const float* k_scale_pool,
+                                 const float* v_scale_pool, void* stream);
+int psk_attention_paged_bf16_split(const psk_paged_attention_args* a, const void* k_pool,
+                                   const void* v_pool, float* partials, uint32_t splits,
+                                   void* stream);
+int psk_attention_paged_bf16_split_reduce(const psk_paged_attention_args* a,
+                                          const float* partials, uint32_t splits,
+                                          void* stream);
+/* Additive (no reference counterpart): FP8 split-K decode. pages_per_split = 0
+ * splits each row's pages evenly into `splits` parts (the reference BF16 rule,
+ * paged_decode.hip:315-320); > 0 gives every split that many pages, so rows of
+ * different lengths use different numbers of splits. Partials layout is the
+ * BF16 split layout: f32 [rows][kv_heads][splits][q_per_kv*(2+256)]. */
+int psk_attention_paged_fp8_e4m3_split(const psk_paged_attention_args* a, const void* k_pool,
+                                       const void* v_pool, const float* k_scale_pool,
+                                       const float* v_scale_pool, float* partials,
+                                       uint32_t splits, uint32_t pages_per_split,
+                                       void* stream);
+/* Additive: BF16 split with an explicit pages_per_split, and the matching reduce. */
+int psk_attention_paged_bf16_split_ex(const psk_paged_attention_args* a, const void* k_pool,
+                                      const void* v_pool, float* partials, uint32_t splits,
+                                      uint32_t pages_per_split, void* stream);
+int psk_attention_paged_split_reduce_ex(const psk_paged_attention_args* a,
+                                        const float* partials, uint32_t splits,
+                                        uint32_t pages_per_split, void* stream);
+/* Bytes of partials the split launchers need. */
+uint64_t psk_attention_split_partials_bytes(uint32_t rows, uint32_t q_heads,
+                                            uint32_t kv_heads, uint32_t splits);
+
+/* Multi-row tiles (speculative verify blocks, chunked prefill)
+ * [attention/paged_prefill.hip:115-459,586-850]: rows [32*t, 32*t+32) of a
+ * launch form one tile and must belong to one sequence with non-decreasing
+ * positions (the reference's own tile contract, paged_prefill.hip:152-164). */
+int psk_attention_paged_prefill_bf16(const psk_paged_attention_args* a, const void* k_pool,
+                                     const void* v_pool, void* stream);
+int psk_attention_paged_prefill_fp8_e4m3(const psk_paged_attention_args* a,
+                                         const void* k_pool, const void* v_pool,
+                                         const float* k_scale_pool,
+                                         const float* v_scale_pool, void* stream);
+
+/* ---- Page-level operations ------------------------------------------------- */
+/* elem_bytes: 2 (bf16 pool), 1 (fp8 codes) or 4 (fp32 scale pool, with
+ * elems_per_token = kv_heads, elems_per_page = page_tokens*kv_heads). */
+int psk_kv_gather(const psk_kv_gather_args* a, const void* pool, void* out,
+                  uint32_t elem_bytes, void* stream);
+/* Batched prefix-cache / copy-on-write page copy
+ * [state/paged_kv_pool.cpp:338-542] in one launch. */
+int psk_kv_copy_pages(const psk_page_copy_args* a, void* stream);
+/* Fill `count` uint32 words at `dst` with `value` (block-table truncation
+ * [state/sequence_slot_pool.cpp:192-232]) without hipMemsetAsync. */
+int psk_fill_u32(uint32_t* dst, uint32_t value, uint64_t count, void* stream);
+/* Row metadata [runtime/batch/device_batch_context.hip:69-90]: for request i,
+ * rows [row_begin, row_begin+row_count) get slot and prefix_length + t. */
+int psk_prepare_row_metadata(const psk_request_descriptor* requests, uint32_t num_requests,
+                             uint32_t actual_rows, uint32_t* row_sequence_slots,
+                             uint32_t* row_positions, void* stream);
+
+/* ---- Self-test hooks (diagnostics, no reference counterpart) --------------- */
+/* Runs the device E4M3 encoder of the append kernel on the floats whose bit
+ * patterns are start_bits .. start_bits+count-1 (count % 4 == 0); word i of
+ * out_words holds the codes of inputs 4i..4i+3 in bytes 0..3. */
+int psk_selftest_e4m3_encode_range(uint32_t start_bits, uint32_t count, uint32_t* out_words,
+                                   void* stream);
+/* Decodes all 256 E4M3 codes with the device decoder of the attention kernels. */
+int psk_selftest_e4m3_decode_all(float* out256, void* stream);
+
+/* ---- Library --------------------------------------------------------------- */
+const char* psk_version(void);
+/* gfx target the library was built for ("gfx950"). */
+const char* psk_build_arch(void);
+/* Name of the last error an entry point returned on this thread. */
+const char* psk_error_string(int err);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* PHASESHIFT_KV_C_H */

@@ -1,0 +1,141 @@
+"""phaseshift_amd — MI355X (gfx950) paged KV-cache hot path of PhaseShift qwen35.
+
+The product is the HIP library ``libphaseshift_kv.so`` behind the C-ABI of
+``include/phaseshift_kv_c.h``. This package loads it with ctypes and offers
+torch-tensor helpers (torch provides device memory and streams only). There is
+no fallback: if the library is missing, importing the ops raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libphaseshift_kv.so")
+
+PSK_INVALID_PAGE_ID = 0xFFFFFFFF
+KV_BF16, KV_FP8 = 0, 1
+OUT_BF16, OUT_F32 = 0, 1
+HIP_SUCCESS, HIP_INVALID_VALUE, HIP_NOT_SUPPORTED = 0, 1, 801
+
+
+class KvAppendArgs(C.Structure):
+    """psk_kv_append_args == ps::kernel::KvAppendCommonArgs (96 B)."""
+    _fields_ = [("k_input", C.c_void_p), ("v_input", C.c_void_p),
+                ("k_row_stride", C.c_uint32), ("v_row_stride", C.c_uint32),
+                ("row_sequence_slots", C.c_void_p), ("row_positions", C.c_void_p),
+                ("block_tables", C.c_void_p)] + [
+        (n, C.c_uint32) for n in (
+            "block_table_stride", "max_sequences", "rows", "layer", "page_tokens",
+            "num_pages", "num_attention_layers", "kv_heads", "head_dim",
+            "elems_per_token", "elems_per_page", "elems_per_layer")]
+
+
+class PagedAttentionArgs(C.Structure):
+    """psk_paged_attention_args == ps::kernel::PagedAttentionCommonArgs (112 B)."""
+    _fields_ = [("q", C.c_void_p), ("output", C.c_void_p), ("output_dtype", C.c_uint8),
+                ("q_row_stride", C.c_uint32), ("output_row_stride", C.c_uint32),
+                ("row_sequence_slots", C.c_void_p), ("row_positions", C.c_void_p),
+                ("block_tables", C.c_void_p)] + [
+        (n, C.c_uint32) for n in (
+            "block_table_stride", "max_sequences", "rows", "layer", "page_tokens",
+            "num_pages", "num_attention_layers", "q_heads", "kv_heads", "head_dim",
+            "elems_per_token", "elems_per_page", "elems_per_layer")] + [("scale", C.c_float)]
+
+
+class KvGatherArgs(C.Structure):
+    _fields_ = [("block_tables", C.c_void_p), ("seq_slots", C.c_void_p),
+                ("seq_token_offsets", C.c_void_p)] + [
+        (n, C.c_uint32) for n in (
+            "block_table_stride", "max_sequences", "num_seqs", "total_tokens", "layer",
+            "page_tokens", "num_pages", "kv_heads", "head_dim", "elems_per_token",
+            "elems_per_page", "elems_per_layer")]
+
+
+class PageCopyArgs(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "dst_k", "dst_v", "dst_k_scale", "dst_v_scale", "src_k", "src_v", "src_k_scale",
+        "src_v_scale", "pairs")] + [
+        (n, C.c_uint32) for n in (
+            "num_pairs", "num_layers", "dst_num_pages", "src_num_pages", "page_tokens",
+            "kv_heads", "head_dim", "kv_dtype")]
+
+
+class RequestDescriptor(C.Structure):
+    """psk_request_descriptor == ps::runtime::DeviceRequestDescriptor (64 B)."""
+    _fields_ = [("slot", C.c_uint32), ("generation", C.c_uint32), ("row_begin", C.c_uint32),
+                ("row_count", C.c_uint32), ("prefix_length", C.c_uint32),
+                ("sequence_length", C.c_uint32), ("output_index", C.c_uint32),
+                ("execution_class", C.c_uint8), ("compute_logits", C.c_uint8),
+                ("output_count", C.c_uint8), ("reserved0", C.c_uint8),
+                ("sampling", C.c_uint8 * 32)]
+
+
+assert C.sizeof(KvAppendArgs) == 96
+assert C.sizeof(PagedAttentionArgs) == 112
+assert PagedAttentionArgs.scale.offset == 108 and PagedAttentionArgs.output_dtype.offset == 16
+assert C.sizeof(RequestDescriptor) == 64
+
+_P = C.c_void_p
+_U32 = C.c_uint32
+# name -> argtypes (restype int unless listed in _RESTYPE)
+SIGNATURES = {
+    "psk_kv_append_bf16": [_P, _P, _P, _P],
+    "psk_kv_append_fp8_e4m3": [_P, _P, _P, _P, _P, _P],
+    "psk_attention_paged_bf16": [_P, _P, _P, _P],
+    "psk_attention_paged_fp8_e4m3": [_P, _P, _P, _P, _P, _P],
+    "psk_attention_paged_bf16_split": [_P, _P, _P, _P, _U32, _P],
+    "psk_attention_paged_bf16_split_reduce": [_P, _P, _U32, _P],
+    "psk_attention_paged_fp8_e4m3_split": [_P, _P, _P, _P, _P, _P, _U32, _U32, _P],
+    "psk_attention_paged_bf16_split_ex": [_P, _P, _P, _P, _U32, _U32, _P],
+    "psk_attention_paged_split_reduce_ex": [_P, _P, _U32, _U32, _P],
+    "psk_attention_split_partials_bytes": [_U32, _U32, _U32, _U32],
+    "psk_attention_paged_prefill_bf16": [_P, _P, _P, _P],
+    "psk_attention_paged_prefill_fp8_e4m3": [_P, _P, _P, _P, _P, _P],
+    "psk_kv_gather": [_P, _P, _P, _U32, _P],
+    "psk_kv_copy_pages": [_P, _P],
+    "psk_fill_u32": [_P, _U32, C.c_uint64, _P],
+    "psk_prepare_row_metadata": [_P, _U32, _U32, _P, _P, _P],
+    "psk_selftest_e4m3_encode_range": [_U32, _U32, _P, _P],
+    "psk_selftest_e4m3_decode_all": [_P, _P],
+    "psk_version": [],
+    "psk_build_arch": [],
+    "psk_error_string": [C.c_int],
+}
+_RESTYPE = {
+    "psk_attention_split_partials_bytes": C.c_uint64,
+    "psk_version": C.c_char_p,
+    "psk_build_arch": C.c_char_p,
+    "psk_error_string": C.c_char_p,
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded HIP library. Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m phaseshift_amd.build` "
+                "(no CPU fallback exists)")
+        L = C.CDLL(LIB_PATH)
+        for name, argt in SIGNATURES.items():
+            f = getattr(L, name)
+            f.argtypes = argt
+            f.restype = _RESTYPE.get(name, C.c_int)
+        _lib = L
+    return _lib
+
+
+class HipError(RuntimeError):
+    def __init__(self, fn: str, code: int):
+        name = lib().psk_error_string(code).decode()
+        super().__init__(f"{fn} returned {code} ({name})")
+        self.code = code
+
+
+def check(fn: str, code: int) -> None:
+    if code != HIP_SUCCESS:
+        raise HipError(fn, code)

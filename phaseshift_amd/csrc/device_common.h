@@ -1,0 +1,108 @@
+// Device helpers shared by the gfx950 kernels of the paged KV path.
+// Wave64 throughout: a wavefront is 64 lanes, cross-lane reductions use the
+// full width.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace psk {
+
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kFp8Max = 448.0f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+    return __uint_as_float(h << 16);
+}
+
+// Round-to-nearest-even f32 -> bf16 bits (NaN -> quiet NaN), as __float2bfloat16.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    bf16x2 v = __builtin_convertvector((f32x2){f, 0.0f}, bf16x2);
+    return __builtin_bit_cast(uint32_t, v) & 0xFFFFu;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+
+// Two FP8 E4M3 codes (bytes 0/1 or 2/3 of `w`) -> two bf16 (exact: every E4M3
+// value is a bf16 value). One v_cvt_scalef32_pk_bf16_fp8 with unit scale.
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w, bool hi) {
+    bf16x2 r = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
+                  : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// 8 FP8 codes in two dwords -> 8 bf16 as one MFMA operand.
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+    u32x4 r;
+    r[0] = fp8x2_to_bf16x2(w0, false);
+    r[1] = fp8x2_to_bf16x2(w0, true);
+    r[2] = fp8x2_to_bf16x2(w1, false);
+    r[3] = fp8x2_to_bf16x2(w1, true);
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// SATFINITE E4M3 encode of two floats into the low 16 bits of the result
+// (byte 0 = a, byte 1 = b): clamp finite values to [-448, 448], then the
+// hardware round-to-nearest-even conversion. This is what ROCm's
+// __hip_cvt_float_to_fp8(x, __HIP_SATFINITE, __HIP_E4M3) lowers to on gfx950,
+// the conversion the reference calls (kv_append.hip:144-146).
+__device__ __forceinline__ float sat_e4m3(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return ((u & 0x7F800000u) != 0x7F800000u) ? __builtin_amdgcn_fmed3f(x, kFp8Max, -kFp8Max)
+                                              : x;
+}
+__device__ __forceinline__ uint32_t e4m3_encode_pair(float a, float b, uint32_t old, bool hi) {
+    return hi ? __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(a), sat_e4m3(b), old, true)
+              : __builtin_amdgcn_cvt_pk_fp8_f32(sat_e4m3(a), sat_e4m3(b), old, false);
+}
+
+// x / s with the IEEE-correct result's E4M3 code, given r = 1/s correctly
+// rounded: q0 = x*r, rem = fma(-q0, s, x) (exact), q = fma(rem, r, q0).
+// Valid when s >= 2^-100 and |x| >= 2^-100; otherwise a true division is used.
+// The E4M3 code of the result was checked equal to the code of x/s for every
+// finite bf16 pair with |x| <= amax, s = amax/448 (tests/native/div_identity.c).
+__device__ __forceinline__ float div_by_scale(float x, float s, float r, bool fast_scale) {
+    if (fast_scale && __builtin_fabsf(x) >= 0x1p-100f) {
+        const float q0 = x * r;
+        const float rem = __builtin_fmaf(-q0, s, x);
+        return __builtin_fmaf(rem, r, q0);
+    }
+    return x / s;
+}
+
+template <int W>
+__device__ __forceinline__ float group_max(float x) {
+#pragma unroll
+    for (int o = W / 2; o >= 1; o >>= 1) x = __builtin_fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x = __builtin_fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+// Orders this wave's LDS writes before its later LDS reads by other lanes.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace psk

@@ -1,0 +1,325 @@
+// Page-level kernels of the paged KV path (gfx950, wave64):
+//   gather of paged KV to contiguous rows, batched prefix-cache page copy,
+//   u32 fill (block-table truncation), row metadata from request descriptors,
+//   the generic any-shape attention kernel, and the E4M3 encoder self-test.
+#include "device_common.h"
+
+#include <phaseshift_kv/paged_attention.h>
+
+#include <cfloat>
+
+namespace psk {
+namespace {
+
+// ----------------------------------------------------------------- gather
+// One wave per output token row; the row is elems_per_token*elem_bytes
+// contiguous bytes in the pool (slot layout [kv_heads][head_dim]), copied with
+// 16 B accesses when aligned.
+__global__ __launch_bounds__(256) void gather_kernel(const psk_kv_gather_args a, const uint8_t* pool,
+                                                     uint8_t* out, uint32_t eb, uint32_t vec16) {
+    const uint64_t wave = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    if (wave >= a.total_tokens) return;
+    const uint32_t t = (uint32_t)wave;
+    // sequence of token t: last i with seq_token_offsets[i] <= t
+    uint32_t lo = 0, hi = a.num_seqs;
+    while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (a.seq_token_offsets[mid] <= t) lo = mid; else hi = mid;
+    }
+    const uint32_t slot = a.seq_slots[lo];
+    if (slot >= a.max_sequences) return;
+    const uint32_t pos = t - a.seq_token_offsets[lo];
+    const uint32_t lb = pos / a.page_tokens;
+    if (lb >= a.block_table_stride) return;
+    const uint32_t page = a.block_tables[(uint64_t)slot * a.block_table_stride + lb];
+    if (page >= a.num_pages) return;
+    const uint64_t src_e = (uint64_t)a.layer * a.elems_per_layer + (uint64_t)page * a.elems_per_page +
+                           (uint64_t)(pos % a.page_tokens) * a.elems_per_token;
+    const uint64_t bytes = (uint64_t)a.elems_per_token * eb;
+    const uint8_t* s = pool + src_e * eb;
+    uint8_t* d = out + (uint64_t)t * bytes;
+    if (vec16) {
+        for (uint64_t o = (uint64_t)lane * 16u; o < bytes; o += 64u * 16u)
+            *reinterpret_cast<u32x4*>(d + o) = *reinterpret_cast<const u32x4*>(s + o);
+    } else {
+        for (uint64_t o = lane; o < bytes; o += 64u) d[o] = s[o];
+    }
+}
+
+// ------------------------------------------------------------- page copy
+// grid.x = pages-pairs * layers * 4 tensors (K, V, K-scale, V-scale); every
+// block copies one page body (or one page's scale rows) with 16 B accesses.
+__global__ __launch_bounds__(256) void copy_pages_kernel(const psk_page_copy_args a, uint32_t eb,
+                                                         uint32_t vec16) {
+    const uint32_t tensor = blockIdx.x & 3u;
+    const uint32_t rest = blockIdx.x >> 2;
+    const uint32_t layer = rest % a.num_layers;
+    const uint32_t pair = rest / a.num_layers;
+    if (pair >= a.num_pairs) return;
+    const uint32_t dst_page = a.pairs[pair].dst_page;
+    const uint32_t src_page = a.pairs[pair].src_page;
+    if (dst_page >= a.dst_num_pages || src_page >= a.src_num_pages) return;
+    const uint64_t page_elems = (uint64_t)a.page_tokens * a.kv_heads * a.head_dim;
+    const uint64_t page_scales = (uint64_t)a.page_tokens * a.kv_heads;
+    const uint8_t* s;
+    uint8_t* d;
+    uint64_t bytes;
+    if (tensor < 2u) {
+        bytes = page_elems * eb;
+        const uint64_t so = ((uint64_t)layer * a.src_num_pages + src_page) * bytes;
+        const uint64_t dof = ((uint64_t)layer * a.dst_num_pages + dst_page) * bytes;
+        s = static_cast<const uint8_t*>(tensor == 0u ? a.src_k : a.src_v) + so;
+        d = static_cast<uint8_t*>(tensor == 0u ? a.dst_k : a.dst_v) + dof;
+    } else {
+        if (a.kv_dtype != PSK_KV_FP8_E4M3) return;
+        bytes = page_scales * 4u;
+        const uint64_t so = ((uint64_t)layer * a.src_num_pages + src_page) * bytes;
+        const uint64_t dof = ((uint64_t)layer * a.dst_num_pages + dst_page) * bytes;
+        s = reinterpret_cast<const uint8_t*>(tensor == 2u ? a.src_k_scale : a.src_v_scale) + so;
+        d = reinterpret_cast<uint8_t*>(tensor == 2u ? a.dst_k_scale : a.dst_v_scale) + dof;
+    }
+    if (vec16 && (bytes % 16u) == 0u) {
+        for (uint64_t o = (uint64_t)threadIdx.x * 16u; o < bytes; o += 256u * 16u)
+            *reinterpret_cast<u32x4*>(d + o) = *reinterpret_cast<const u32x4*>(s + o);
+    } else {
+        for (uint64_t o = threadIdx.x; o < bytes; o += 256u) d[o] = s[o];
+    }
+}
+
+// ------------------------------------------------------------------ fill
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* dst, uint32_t value, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = value;
+}
+
+// --------------------------------------------------------- row metadata
+// Restates prepare_batch_descriptor_kernel (device_batch_context.hip:69-90)
+// for the two row arrays of the KV path; one thread per (request, row).
+__global__ __launch_bounds__(256) void row_metadata_kernel(const psk_request_descriptor* req,
+                                                           uint32_t num_requests, uint32_t actual_rows,
+                                                           uint32_t* slots, uint32_t* positions) {
+    const uint32_t r = blockIdx.y;
+    if (r >= num_requests) return;
+    const psk_request_descriptor d = req[r];
+    for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < d.row_count;
+         t += gridDim.x * blockDim.x) {
+        const uint32_t row = d.row_begin + t;
+        if (row >= actual_rows) continue;
+        slots[row] = d.slot;
+        positions[row] = d.prefix_length + t;
+    }
+}
+
+// -------------------------------------------------- generic attention
+// Any head_dim <= 256, any q_per_kv: one wave per (row, q_head), lanes over
+// dims (4 per lane), online softmax in fp32, the reference's per-(row, head)
+// formulation (paged_decode.hip:47-206, FP8 :970-1140).
+template <int KVB>
+__global__ __launch_bounds__(256) void generic_attention_kernel(const psk_paged_attention_args a,
+                                                                const uint8_t* kp, const uint8_t* vp,
+                                                                const float* ksc, const float* vsc) {
+    const uint64_t task = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    if (task >= (uint64_t)a.rows * a.q_heads) return;
+    const uint32_t row = (uint32_t)(task / a.q_heads);
+    const uint32_t qh = (uint32_t)(task % a.q_heads);
+    const uint32_t kvh = qh / (a.q_heads / a.kv_heads);
+    const uint32_t slot = a.row_sequence_slots[row];
+    if (slot >= a.max_sequences) return;
+    const uint64_t vis64 = (uint64_t)a.row_positions[row] + 1u;
+    if (vis64 > (uint64_t)a.block_table_stride * a.page_tokens) return;
+    const uint32_t visible = (uint32_t)vis64;
+    const uint32_t D = a.head_dim;
+    const uint32_t* bt = a.block_tables + (uint64_t)slot * a.block_table_stride;
+    const uint16_t* q = static_cast<const uint16_t*>(a.q) + (uint64_t)row * a.q_row_stride +
+                        (uint64_t)qh * D;
+    float qv[4], acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t d = lane + 64u * j;
+        qv[j] = d < D ? bf16_bits_to_f32(q[d]) : 0.0f;
+        acc[j] = 0.0f;
+    }
+    float m = -INFINITY, l = 0.0f;
+    const float sl = a.scale * kLog2e;
+    for (uint32_t t = 0; t < visible; ++t) {
+        const uint32_t page = bt[t / a.page_tokens];
+        if (page >= a.num_pages) return;   // output left unwritten
+        const uint64_t e = (uint64_t)a.layer * a.elems_per_layer + (uint64_t)page * a.elems_per_page +
+                           (uint64_t)(t % a.page_tokens) * a.elems_per_token + (uint64_t)kvh * D;
+        float kf[4], vf[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t d = lane + 64u * j;
+            if (d < D) {
+                if constexpr (KVB == 2) {
+                    kf[j] = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(kp)[e + d]);
+                    vf[j] = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(vp)[e + d]);
+                } else {
+                    kf[j] = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)kp[e + d], false)[0];
+                    vf[j] = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)vp[e + d], false)[0];
+                }
+            } else {
+                kf[j] = 0.0f;
+                vf[j] = 0.0f;
+            }
+        }
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dot += qv[j] * kf[j];
+        dot = wave_sum(dot);
+        float vw = 1.0f, f = sl;
+        if constexpr (KVB == 1) {
+            const uint64_t si = (((uint64_t)a.layer * a.num_pages + page) * a.page_tokens +
+                                 t % a.page_tokens) * a.kv_heads + kvh;
+            f *= ksc[si];
+            vw = vsc[si];
+        }
+        const float s = dot * f;
+        const float mn = __builtin_fmaxf(m, s);
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        const float w = __builtin_amdgcn_exp2f(s - mn);
+        l = l * alpha + w;
+        m = mn;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = acc[j] * alpha + (w * vw) * vf[j];
+    }
+    const uint64_t ob = (uint64_t)row * a.output_row_stride + (uint64_t)qh * D;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t d = lane + 64u * j;
+        if (d >= D) continue;
+        const float r = acc[j] / l;
+        if (a.output_dtype == PSK_OUT_F32)
+            static_cast<float*>(a.output)[ob + d] = r;
+        else
+            static_cast<uint16_t*>(a.output)[ob + d] = f32_to_bf16_bits(r);
+    }
+}
+
+// ------------------------------------------------- encoder self-test
+// Encodes the floats with bit patterns start .. start+count-1 through the same
+// e4m3_encode_pair the append kernel uses (pairs land in bytes 0-3 of a word
+// exactly as in kv_append_kernel).
+__global__ __launch_bounds__(256) void e4m3_selftest_kernel(uint32_t start, uint32_t count,
+                                                            uint32_t* out) {
+    const uint64_t w = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (w * 4u >= count) return;
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(start + (uint32_t)(w * 4u) + (uint32_t)i);
+    out[w] = e4m3_encode_pair(x[2], x[3], e4m3_encode_pair(x[0], x[1], 0u, false), true);
+}
+
+__global__ __launch_bounds__(256) void e4m3_decode_selftest_kernel(float* out) {
+    const uint32_t c = threadIdx.x;
+    const uint32_t bf = fp8x2_to_bf16x2(c, false) & 0xFFFFu;
+    out[c] = __uint_as_float(bf << 16);
+}
+
+}  // namespace
+
+hipError_t launch_attention_generic(const psk_paged_attention_args& c, int kvb, const void* k,
+                                    const void* v, const float* ks, const float* vs,
+                                    hipStream_t stream) {
+    const uint64_t waves = (uint64_t)c.rows * c.q_heads;
+    const uint64_t blocks = (waves + 3u) / 4u;
+    if (blocks == 0u || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    if (kvb == 2)
+        hipLaunchKernelGGL(generic_attention_kernel<2>, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                           c, static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v), ks, vs);
+    else
+        hipLaunchKernelGGL(generic_attention_kernel<1>, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                           c, static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v), ks, vs);
+    return hipGetLastError();
+}
+
+}  // namespace psk
+
+extern "C" int psk_kv_gather(const psk_kv_gather_args* a, const void* pool, void* out,
+                             uint32_t elem_bytes, void* stream) {
+    if (a == nullptr || pool == nullptr || out == nullptr) return hipErrorInvalidValue;
+    if (elem_bytes != 1u && elem_bytes != 2u && elem_bytes != 4u) return hipErrorInvalidValue;
+    if (a->total_tokens == 0u) return hipSuccess;
+    if (a->block_tables == nullptr || a->seq_slots == nullptr || a->seq_token_offsets == nullptr ||
+        a->num_seqs == 0u || a->page_tokens == 0u || a->elems_per_token == 0u)
+        return hipErrorInvalidValue;
+    const uint64_t row_bytes = (uint64_t)a->elems_per_token * elem_bytes;
+    const uint32_t vec16 = (row_bytes % 16u == 0u) && ((uint64_t)a->elems_per_page * elem_bytes % 16u == 0u) &&
+                           ((uint64_t)a->elems_per_layer * elem_bytes % 16u == 0u) &&
+                           (reinterpret_cast<uintptr_t>(pool) % 16u == 0u) &&
+                           (reinterpret_cast<uintptr_t>(out) % 16u == 0u);
+    const uint64_t blocks = ((uint64_t)a->total_tokens + 3u) / 4u;
+    hipLaunchKernelGGL(psk::gather_kernel, dim3((uint32_t)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), *a, static_cast<const uint8_t*>(pool),
+                       static_cast<uint8_t*>(out), elem_bytes, vec16);
+    return hipGetLastError();
+}
+
+extern "C" int psk_kv_copy_pages(const psk_page_copy_args* a, void* stream) {
+    if (a == nullptr) return hipErrorInvalidValue;
+    if (a->num_pairs == 0u) return hipSuccess;
+    if (a->pairs == nullptr || a->dst_k == nullptr || a->dst_v == nullptr || a->src_k == nullptr ||
+        a->src_v == nullptr || a->num_layers == 0u || a->page_tokens == 0u || a->kv_heads == 0u ||
+        a->head_dim == 0u)
+        return hipErrorInvalidValue;
+    if (a->kv_dtype != PSK_KV_BF16 && a->kv_dtype != PSK_KV_FP8_E4M3) return hipErrorInvalidValue;
+    if (a->kv_dtype == PSK_KV_FP8_E4M3 &&
+        (a->dst_k_scale == nullptr || a->dst_v_scale == nullptr || a->src_k_scale == nullptr ||
+         a->src_v_scale == nullptr))
+        return hipErrorInvalidValue;
+    const uint32_t eb = a->kv_dtype == PSK_KV_FP8_E4M3 ? 1u : 2u;
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16u == 0u; };
+    const uint32_t vec16 = al(a->dst_k) && al(a->dst_v) && al(a->src_k) && al(a->src_v) &&
+                           (a->kv_dtype != PSK_KV_FP8_E4M3 ||
+                            (al(a->dst_k_scale) && al(a->dst_v_scale) && al(a->src_k_scale) &&
+                             al(a->src_v_scale)));
+    const uint64_t blocks = (uint64_t)a->num_pairs * a->num_layers * 4u;
+    if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(psk::copy_pages_kernel, dim3((uint32_t)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), *a, eb, vec16);
+    return hipGetLastError();
+}
+
+extern "C" int psk_fill_u32(uint32_t* dst, uint32_t value, uint64_t count, void* stream) {
+    if (count == 0u) return hipSuccess;
+    if (dst == nullptr) return hipErrorInvalidValue;
+    uint64_t blocks = (count + 255u) / 256u;
+    if (blocks > 4096u) blocks = 4096u;
+    hipLaunchKernelGGL(psk::fill_u32_kernel, dim3((uint32_t)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), dst, value, count);
+    return hipGetLastError();
+}
+
+extern "C" int psk_prepare_row_metadata(const psk_request_descriptor* requests, uint32_t num_requests,
+                                        uint32_t actual_rows, uint32_t* row_sequence_slots,
+                                        uint32_t* row_positions, void* stream) {
+    if (num_requests == 0u) return hipSuccess;
+    if (requests == nullptr || row_sequence_slots == nullptr || row_positions == nullptr)
+        return hipErrorInvalidValue;
+    if (num_requests > 65535u) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(psk::row_metadata_kernel, dim3(8, num_requests), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), requests, num_requests, actual_rows,
+                       row_sequence_slots, row_positions);
+    return hipGetLastError();
+}
+
+// Self-test hooks: run the device E4M3 encoder / decoder on given inputs.
+extern "C" int psk_selftest_e4m3_encode_range(uint32_t start_bits, uint32_t count, uint32_t* out_words,
+                                              void* stream) {
+    if (out_words == nullptr || count % 4u != 0u) return hipErrorInvalidValue;
+    if (count == 0u) return hipSuccess;
+    const uint64_t words = count / 4u;
+    hipLaunchKernelGGL(psk::e4m3_selftest_kernel, dim3((uint32_t)((words + 255u) / 256u)), dim3(256),
+                       0, static_cast<hipStream_t>(stream), start_bits, count, out_words);
+    return hipGetLastError();
+}
+
+extern "C" int psk_selftest_e4m3_decode_all(float* out256, void* stream) {
+    if (out256 == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(psk::e4m3_decode_selftest_kernel, dim3(1), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), out256);
+    return hipGetLastError();
+}

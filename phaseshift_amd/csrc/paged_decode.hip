@@ -1,0 +1,641 @@
+// Paged-attention decode over GQA KV pages, BF16 or FP8 E4M3 KV, gfx950.
+//
+// Reference behaviour restated (file:line in the reference repository):
+//   visibility (pos + 1), row skip rules, invalid page  paged_decode.hip:79-97,123-128
+//   BF16 math  s = scale*q.k, online softmax, out = acc/sum   paged_decode.hip:135-205
+//   FP8 math   s = (q.dec(k))*k_scale*scale,
+//              acc += (p*v_scale)*dec(v)                     paged_decode.hip:1064-1090
+//   split rule per = ceil(pages/splits), partial (m, P, A)   paged_decode.hip:315-320,413-471
+//   combine g = max m_s, W_s = e^(m_s-g),
+//           out = sum W_s A_s / sum W_s P_s                  paged_decode.hip:474-555
+//   launcher validation                                      paged_decode.hip:228-259,787-817
+//
+// MI355X design. One workgroup = (row, kv_head, split), 4 waves. The whole GQA
+// group (q_per_kv <= 16 query heads) is the N=16 side of
+// v_mfma_f32_16x16x32_bf16, so each K/V byte is read from HBM once per
+// (row, kv_head) instead of once per query head:
+//   S^T[16 tokens x 16 heads] = K[16 x D] * Q^T[D x 16]   (D/32 MFMAs)
+//   O^T[16 dims x 16 heads]  += V^T[16 x 32 tokens] * P^T[32 tokens x 16 heads]
+// Each wave owns 32-token chunks (round robin), keeps its own online-softmax
+// state in log2 units, and the 4 waves merge through LDS at the end. K is read
+// straight into MFMA A-operand registers (lane = token, 16 B per load, every
+// 64 B token segment read whole by 4 lanes); V is transposed through a
+// per-wave LDS tile so that a lane holds 8 tokens of one dim. FP8 codes become
+// bf16 exactly (v_cvt_scalef32_pk_bf16_fp8); k_scale multiplies the score and
+// v_scale is folded into P before PV.
+#include "device_common.h"
+
+#include <phaseshift_kv/paged_attention.h>
+
+#include <cfloat>
+
+namespace psk {
+namespace {
+
+struct DecodeParams {
+    psk_paged_attention_args a;
+    const uint8_t* k_pool;
+    const uint8_t* v_pool;
+    const float* k_scale;
+    const float* v_scale;
+    float* partials;          // nullptr: write the output directly
+    uint32_t splits;
+    uint32_t pages_per_split; // 0: ceil(pages / splits) per row
+    float scale_log2;         // scale * log2(e)
+};
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kChunk = 32;       // tokens per wave iteration
+constexpr int kMaxQPerKV = 16;
+constexpr uint32_t kMaxSplits = 1024;
+using ps::kernel::kPagedAttentionHeadLimit;
+
+template <int KVB>
+constexpr int lds_pitch() { return KVB == 1 ? 40 : 80; }   // bytes per dim row of a V^T tile
+
+__device__ __forceinline__ uint32_t split_pages(uint32_t pc, uint32_t splits, uint32_t pps) {
+    return pps != 0u ? pps : (pc + splits - 1u) / splits;
+}
+
+// Loads 8 bf16 of a query head as an MFMA operand (zeros past the group).
+__device__ __forceinline__ bf16x8 load_q8(const uint16_t* q, bool ok) {
+    u32x4 r = {0u, 0u, 0u, 0u};
+    if (ok) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = (uint32_t)q[2 * i] | ((uint32_t)q[2 * i + 1] << 16);
+    }
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+template <int KVB, int D>
+__global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeParams p) {
+    constexpr int NL = D * KVB / 64;   // 16 B loads per lane per 16-token half
+    constexpr int NS = D / 32;         // MFMA K-steps of the score product
+    constexpr int NDB = D / 16;        // 16-dim blocks of the output
+    constexpr int PITCH = lds_pitch<KVB>();
+    static_assert(NL >= 1 && NS >= 1, "head_dim too small for this kernel");
+
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ uint32_t bad_shared;
+
+    const psk_paged_attention_args& a = p.a;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
+    const uint32_t n = lane & 15u;   // token (loads, S rows) or head (S cols, P, O)
+    const uint32_t g = lane >> 4;    // lane group
+
+    const uint32_t splits = p.splits;
+    const uint32_t split = blockIdx.x % splits;
+    const uint32_t rest = blockIdx.x / splits;
+    const uint32_t kv_head = rest % a.kv_heads;
+    const uint32_t row = rest / a.kv_heads;
+    if (row >= a.rows) return;
+
+    const uint32_t slot = a.row_sequence_slots[row];
+    if (slot >= a.max_sequences) return;
+    const uint64_t vis64 = (uint64_t)a.row_positions[row] + 1u;
+    if (vis64 > (uint64_t)a.block_table_stride * a.page_tokens) return;
+    const uint32_t visible = (uint32_t)vis64;
+    const uint32_t P = a.page_tokens;
+    const uint32_t pc = (visible + P - 1u) / P;
+    const uint32_t per = split_pages(pc, splits, p.pages_per_split);
+    const uint32_t pb = split * per;
+    if (pb >= pc) return;   // empty split: the reduce never reads it
+    const uint32_t pe = (split == splits - 1u) ? pc : min(pc, pb + per);
+    const uint32_t t_begin = pb * P;
+    const uint32_t t_end = min(pe * P, visible);
+    const uint32_t* bt = a.block_tables + (uint64_t)slot * a.block_table_stride;
+
+    const uint32_t qpk = a.q_heads / a.kv_heads;
+    if (tid == 0) bad_shared = 0u;
+    __syncthreads();
+
+    // Q fragments: lane (n, g) holds head n, the dims that lane group g covers
+    // in each K-step (the same dims the K loads below put in that lane).
+    bf16x8 qf[NS];
+    {
+        const bool hv = n < qpk;
+        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + (uint64_t)row * a.q_row_stride +
+                               (uint64_t)(kv_head * qpk + (hv ? n : 0u)) * D;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int d0 = KVB == 2 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
+            qf[s] = load_q8(qrow + d0, hv);
+        }
+    }
+
+    const uint64_t layer_base = (uint64_t)a.layer * a.elems_per_layer;
+    const uint64_t scale_layer = (uint64_t)a.layer * a.num_pages;
+    uint8_t* vt = lds + (size_t)wave * D * PITCH;
+
+    float m_run = -INFINITY;   // running max (log2 units), head n
+    float l_run = 0.0f;        // partial softmax sum of this lane's tokens
+    f32x4 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    bool bad = false;
+
+    for (uint32_t cbase = t_begin + wave * kChunk; cbase < t_end; cbase += kWaves * kChunk) {
+        // ---- loads: lane owns token n of each 16-token half
+        u32x4 kr[2][NL], vr[2][NL];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint32_t tau = cbase + hf * 16 + n;
+            bool ok = tau < t_end;
+            uint64_t elem = 0;
+            if (ok) {
+                const uint32_t page = bt[tau / P];
+                if (page >= a.num_pages) {
+                    bad = true;
+                    ok = false;
+                } else {
+                    elem = layer_base + (uint64_t)page * a.elems_per_page +
+                           (uint64_t)(tau % P) * a.elems_per_token + (uint64_t)kv_head * D;
+                }
+            }
+            const uint8_t* kb = p.k_pool + elem * KVB + g * 16;
+            const uint8_t* vb = p.v_pool + elem * KVB + g * 16;
+#pragma unroll
+            for (int i = 0; i < NL; ++i) {
+                if (ok) {
+                    kr[hf][i] = *reinterpret_cast<const u32x4*>(kb + i * 64);
+                    vr[hf][i] = *reinterpret_cast<const u32x4*>(vb + i * 64);
+                } else {
+                    kr[hf][i] = (u32x4){0u, 0u, 0u, 0u};
+                    vr[hf][i] = (u32x4){0u, 0u, 0u, 0u};
+                }
+            }
+        }
+
+        // ---- V^T into this wave's LDS tile: element (token slot k, dim d)
+        // at vt[d*PITCH + k*KVB], k = 8*(n/4) + n%4 + 4*hf.
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint32_t k = 8u * (n >> 2) + (n & 3u) + 4u * hf;
+#pragma unroll
+            for (int i = 0; i < NL; ++i) {
+                if constexpr (KVB == 1) {
+                    const uint32_t d0 = i * 64 + g * 16;
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        vt[(d0 + e) * PITCH + k] = (uint8_t)(vr[hf][i][e >> 2] >> (8 * (e & 3)));
+                } else {
+                    const uint32_t d0 = i * 32 + g * 8;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        *reinterpret_cast<uint16_t*>(vt + (d0 + e) * PITCH + 2 * k) =
+                            (uint16_t)(vr[hf][i][e >> 1] >> (16 * (e & 1)));
+                }
+            }
+        }
+
+        // ---- scores S^T (token x head) for both halves
+        f32x4 sc[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                bf16x8 kf;
+                if constexpr (KVB == 2) {
+                    kf = __builtin_bit_cast(bf16x8, kr[hf][s]);
+                } else {
+                    const u32x4 w = kr[hf][s >> 1];
+                    kf = (s & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
+            }
+            sc[hf] = acc;
+        }
+
+        // ---- lane (n, g) now holds head n, tokens cbase + 16*hf + 4*g + r
+        float s2[2][4], vsc[2][4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t tau = cbase + hf * 16 + 4 * g + r;
+                float f = p.scale_log2;
+                float vs = 1.0f;
+                bool ok = tau < t_end;
+                if constexpr (KVB == 1) {
+                    if (ok) {
+                        const uint32_t page = bt[tau / P];
+                        if (page < a.num_pages) {
+                            const uint64_t si =
+                                ((scale_layer + page) * P + tau % P) * a.kv_heads + kv_head;
+                            f *= p.k_scale[si];
+                            vs = p.v_scale[si];
+                        } else {
+                            ok = false;
+                        }
+                    }
+                }
+                s2[hf][r] = ok ? sc[hf][r] * f : -INFINITY;
+                vsc[hf][r] = vs;
+                mx = __builtin_fmaxf(mx, s2[hf][r]);
+            }
+        }
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = __builtin_fmaxf(m_run, mx);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float pv[2][4];
+        float psum = 0.0f;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
+                psum += e;
+                pv[hf][r] = e * vsc[hf][r];
+            }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        u32x4 pw;
+        pw[0] = pack_bf16x2(pv[0][0], pv[0][1]);
+        pw[1] = pack_bf16x2(pv[0][2], pv[0][3]);
+        pw[2] = pack_bf16x2(pv[1][0], pv[1][1]);
+        pw[3] = pack_bf16x2(pv[1][2], pv[1][3]);
+        const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
+
+        wave_lds_sync();
+        // ---- O^T += V^T * P^T, 16 dims per MFMA
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            const uint8_t* src = vt + (db * 16 + n) * PITCH + g * 8 * KVB;
+            bf16x8 vf;
+            if constexpr (KVB == 1) {
+                const u32x2 w = *reinterpret_cast<const u32x2*>(src);
+                vf = fp8x8_to_bf16x8(w[0], w[1]);
+            } else {
+                vf = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(src));
+            }
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[db] * alpha, 0, 0, 0);
+        }
+        wave_lds_sync();
+    }
+
+    // ---- merge the 4 waves: per wave m[16], l[16], O[qpk][D] in LDS
+    if (bad) bad_shared = 1u;
+    const float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+    const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
+    __syncthreads();
+    float* fm = reinterpret_cast<float*>(lds);
+    float* fl = fm + kWaves * 16;
+    float* fo = fl + kWaves * 16;   // [wave][qpk][D]
+    if (g == 0) {
+        fm[wave * 16 + n] = m_run;
+        fl[wave * 16 + n] = l_all;
+    }
+    if (n < qpk) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                fo[((size_t)wave * qpk + n) * D + db * 16 + 4 * g + r] = o[db][r];
+    }
+    __syncthreads();
+
+    const uint32_t q0 = kv_head * qpk;
+    float* part = nullptr;
+    if (p.partials != nullptr)
+        part = p.partials + ((uint64_t)(row * a.kv_heads + kv_head) * splits + split) *
+                                (uint64_t)(qpk * (2u + kPagedAttentionHeadLimit));
+    if (bad_shared != 0u) {
+        // An invalid page leaves this row's output unwritten; the NaN marks
+        // the split for the reduce, which then writes nothing either.
+        if (part != nullptr && tid < qpk) part[tid] = __builtin_nanf("");
+        return;
+    }
+    for (uint32_t idx = tid; idx < qpk * D; idx += kThreads) {
+        const uint32_t h = idx / D, d = idx % D;
+        float gm = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) gm = __builtin_fmaxf(gm, fm[w * 16 + h]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float wt = __builtin_amdgcn_exp2f(fm[w * 16 + h] - gm);
+            L += wt * fl[w * 16 + h];
+            O += wt * fo[((size_t)w * qpk + h) * D + d];
+        }
+        if (part == nullptr) {
+            const uint64_t oi = (uint64_t)row * a.output_row_stride + (uint64_t)(q0 + h) * D + d;
+            const float res = O / L;
+            if (a.output_dtype == PSK_OUT_F32)
+                static_cast<float*>(a.output)[oi] = res;
+            else
+                static_cast<uint16_t*>(a.output)[oi] = f32_to_bf16_bits(res);
+        } else {
+            if (d == 0) {
+                part[h] = gm * 0.69314718055994531f;   // back to natural-log units
+                part[qpk + h] = L;
+            }
+            part[2u * qpk + h * kPagedAttentionHeadLimit + d] = O;
+        }
+    }
+}
+
+// Combine of the split partials: WG = (row, kv_head), thread = dim.
+__global__ __launch_bounds__(kThreads) void split_reduce_kernel(const DecodeParams p) {
+    const psk_paged_attention_args& a = p.a;
+    const uint32_t kv_head = blockIdx.x % a.kv_heads;
+    const uint32_t row = blockIdx.x / a.kv_heads;
+    if (row >= a.rows) return;
+    const uint32_t slot = a.row_sequence_slots[row];
+    if (slot >= a.max_sequences) return;
+    const uint64_t vis64 = (uint64_t)a.row_positions[row] + 1u;
+    if (vis64 > (uint64_t)a.block_table_stride * a.page_tokens) return;
+    const uint32_t pc = ((uint32_t)vis64 + a.page_tokens - 1u) / a.page_tokens;
+    const uint32_t per = split_pages(pc, p.splits, p.pages_per_split);
+    const uint32_t n_used = min(p.splits, (pc + per - 1u) / per);
+    const uint32_t qpk = a.q_heads / a.kv_heads;
+    const uint64_t stride = (uint64_t)qpk * (2u + kPagedAttentionHeadLimit);
+    const float* base = p.partials + (uint64_t)(row * a.kv_heads + kv_head) * p.splits * stride;
+    const uint32_t D = a.head_dim;
+    for (uint32_t h = 0; h < qpk; ++h) {
+        float gm = -INFINITY;
+        bool bad = false;
+        for (uint32_t s = 0; s < n_used; ++s) {
+            const float m = base[s * stride + h];
+            bad |= __builtin_isnan(m);
+            gm = __builtin_fmaxf(gm, m);
+        }
+        if (bad) return;
+        float L = 0.0f;
+        for (uint32_t s = 0; s < n_used; ++s)
+            L += __expf(base[s * stride + h] - gm) * base[s * stride + qpk + h];
+        for (uint32_t d = threadIdx.x; d < D; d += kThreads) {
+            float O = 0.0f;
+            for (uint32_t s = 0; s < n_used; ++s)
+                O += __expf(base[s * stride + h] - gm) *
+                     base[s * stride + 2u * qpk + h * kPagedAttentionHeadLimit + d];
+            const uint64_t oi =
+                (uint64_t)row * a.output_row_stride + (uint64_t)(kv_head * qpk + h) * D + d;
+            const float res = O / L;
+            if (a.output_dtype == PSK_OUT_F32)
+                static_cast<float*>(a.output)[oi] = res;
+            else
+                static_cast<uint16_t*>(a.output)[oi] = f32_to_bf16_bits(res);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- host side
+hipError_t validate_common(const psk_paged_attention_args& c) {
+    if (c.rows == 0u || c.head_dim == 0u || c.head_dim > kPagedAttentionHeadLimit)
+        return hipErrorInvalidValue;
+    if (c.q_heads == 0u || c.kv_heads == 0u || c.q_heads % c.kv_heads != 0u)
+        return hipErrorInvalidValue;
+    if (c.page_tokens == 0u || c.block_table_stride == 0u || c.num_pages == 0u)
+        return hipErrorInvalidValue;
+    if (c.q == nullptr || c.output == nullptr || c.row_sequence_slots == nullptr ||
+        c.row_positions == nullptr || c.block_tables == nullptr)
+        return hipErrorInvalidValue;
+    if (c.output_dtype != PSK_OUT_BF16 && c.output_dtype != PSK_OUT_F32)
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+// Shapes the MFMA kernel covers: q_per_kv <= 16, head_dim in {32 (bf16 only),
+// 64, 128, 256}, every head slice 16 B aligned.
+bool mfma_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, const void* vp) {
+    const uint32_t qpk = c.q_heads / c.kv_heads;
+    if (qpk > (uint32_t)kMaxQPerKV) return false;
+    const uint32_t D = c.head_dim;
+    if (!(D == 64 || D == 128 || D == 256 || (D == 32 && kvb == 2))) return false;
+    const uint32_t align_elems = 16u / (uint32_t)kvb;
+    if (c.elems_per_token % align_elems || c.elems_per_page % align_elems ||
+        c.elems_per_layer % align_elems)
+        return false;
+    if (reinterpret_cast<uintptr_t>(kp) % 16u || reinterpret_cast<uintptr_t>(vp) % 16u)
+        return false;
+    return true;
+}
+
+template <int KVB, int D>
+hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+    const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
+    const size_t v_bytes = (size_t)kWaves * D * lds_pitch<KVB>();
+    const size_t m_bytes = (size_t)kWaves * 32 * sizeof(float) + (size_t)kWaves * qpk * D * sizeof(float);
+    const size_t lds_bytes = v_bytes > m_bytes ? v_bytes : m_bytes;
+    const uint64_t grid = (uint64_t)p.a.rows * p.a.kv_heads * p.splits;
+    if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    if (lds_bytes > 64u * 1024u) {
+        // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&paged_decode_kernel<KVB, D>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+        if (attr != hipSuccess) return attr;
+    }
+    hipLaunchKernelGGL((paged_decode_kernel<KVB, D>), dim3((uint32_t)grid), dim3(kThreads),
+                       lds_bytes, stream, p);
+    return hipGetLastError();
+}
+
+template <int KVB>
+hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
+    switch (p.a.head_dim) {
+        case 256: return launch_decode_t<KVB, 256>(p, stream);
+        case 128: return launch_decode_t<KVB, 128>(p, stream);
+        case 64: return launch_decode_t<KVB, 64>(p, stream);
+        case 32:
+            if constexpr (KVB == 2) return launch_decode_t<2, 32>(p, stream);
+            return hipErrorNotSupported;
+        default: return hipErrorNotSupported;
+    }
+}
+
+hipError_t launch_reduce(const DecodeParams& p, hipStream_t stream) {
+    const uint64_t grid = (uint64_t)p.a.rows * p.a.kv_heads;
+    if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(split_reduce_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream, p);
+    return hipGetLastError();
+}
+
+DecodeParams make(const psk_paged_attention_args& c, const void* k, const void* v, const float* ks,
+                  const float* vs, float* partials, uint32_t splits, uint32_t pps) {
+    DecodeParams p{};
+    p.a = c;
+    p.k_pool = static_cast<const uint8_t*>(k);
+    p.v_pool = static_cast<const uint8_t*>(v);
+    p.k_scale = ks;
+    p.v_scale = vs;
+    p.partials = partials;
+    p.splits = splits;
+    p.pages_per_split = pps;
+    p.scale_log2 = c.scale * kLog2e;
+    return p;
+}
+
+}  // namespace
+
+// Generic fallback for shapes outside mfma_shape_ok (defined in page_ops.hip).
+hipError_t launch_attention_generic(const psk_paged_attention_args& c, int kvb, const void* k,
+                                    const void* v, const float* ks, const float* vs,
+                                    hipStream_t stream);
+
+}  // namespace psk
+
+using psk::DecodeParams;
+
+extern "C" uint64_t psk_attention_split_partials_bytes(uint32_t rows, uint32_t q_heads,
+                                                       uint32_t kv_heads, uint32_t splits) {
+    if (kv_heads == 0u) return 0u;
+    return (uint64_t)rows * kv_heads * splits * (q_heads / kv_heads) *
+           (2u + ps::kernel::kPagedAttentionHeadLimit) * sizeof(float);
+}
+
+extern "C" int psk_attention_paged_bf16(const psk_paged_attention_args* a, const void* k_pool,
+                                        const void* v_pool, void* stream) {
+    if (a == nullptr || k_pool == nullptr || v_pool == nullptr) return hipErrorInvalidValue;
+    hipError_t e = psk::validate_common(*a);
+    if (e != hipSuccess) return e;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (!psk::mfma_shape_ok(*a, 2, k_pool, v_pool))
+        return psk::launch_attention_generic(*a, 2, k_pool, v_pool, nullptr, nullptr, st);
+    return psk::launch_decode<2>(psk::make(*a, k_pool, v_pool, nullptr, nullptr, nullptr, 1u, 0u), st);
+}
+
+extern "C" int psk_attention_paged_fp8_e4m3(const psk_paged_attention_args* a, const void* k_pool,
+                                            const void* v_pool, const float* k_scale_pool,
+                                            const float* v_scale_pool, void* stream) {
+    if (a == nullptr || k_pool == nullptr || v_pool == nullptr || k_scale_pool == nullptr ||
+        v_scale_pool == nullptr)
+        return hipErrorInvalidValue;
+    hipError_t e = psk::validate_common(*a);
+    if (e != hipSuccess) return e;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (!psk::mfma_shape_ok(*a, 1, k_pool, v_pool))
+        return psk::launch_attention_generic(*a, 1, k_pool, v_pool, k_scale_pool, v_scale_pool, st);
+    return psk::launch_decode<1>(
+        psk::make(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, nullptr, 1u, 0u), st);
+}
+
+static int split_common(const psk_paged_attention_args* a, const void* k_pool, const void* v_pool,
+                        float* partials, uint32_t splits) {
+    if (a == nullptr || k_pool == nullptr || v_pool == nullptr || partials == nullptr)
+        return hipErrorInvalidValue;
+    hipError_t e = psk::validate_common(*a);
+    if (e != hipSuccess) return e;
+    if (splits == 0u || splits > psk::kMaxSplits) return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+extern "C" int psk_attention_paged_bf16_split_ex(const psk_paged_attention_args* a,
+                                                 const void* k_pool, const void* v_pool,
+                                                 float* partials, uint32_t splits,
+                                                 uint32_t pages_per_split, void* stream) {
+    int e = split_common(a, k_pool, v_pool, partials, splits);
+    if (e != hipSuccess) return e;
+    if (!psk::mfma_shape_ok(*a, 2, k_pool, v_pool)) return hipErrorNotSupported;
+    return psk::launch_decode<2>(
+        psk::make(*a, k_pool, v_pool, nullptr, nullptr, partials, splits, pages_per_split),
+        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int psk_attention_paged_bf16_split(const psk_paged_attention_args* a, const void* k_pool,
+                                              const void* v_pool, float* partials, uint32_t splits,
+                                              void* stream) {
+    // The reference accepts 2, 4, 8 or 16 splits (paged_decode.hip:805-806).
+    if (splits != 2u && splits != 4u && splits != 8u && splits != 16u) return hipErrorInvalidValue;
+    return psk_attention_paged_bf16_split_ex(a, k_pool, v_pool, partials, splits, 0u, stream);
+}
+
+extern "C" int psk_attention_paged_fp8_e4m3_split(const psk_paged_attention_args* a,
+                                                  const void* k_pool, const void* v_pool,
+                                                  const float* k_scale_pool,
+                                                  const float* v_scale_pool, float* partials,
+                                                  uint32_t splits, uint32_t pages_per_split,
+                                                  void* stream) {
+    int e = split_common(a, k_pool, v_pool, partials, splits);
+    if (e != hipSuccess) return e;
+    if (k_scale_pool == nullptr || v_scale_pool == nullptr) return hipErrorInvalidValue;
+    if (!psk::mfma_shape_ok(*a, 1, k_pool, v_pool)) return hipErrorNotSupported;
+    return psk::launch_decode<1>(psk::make(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, partials,
+                                           splits, pages_per_split),
+                                 static_cast<hipStream_t>(stream));
+}
+
+extern "C" int psk_attention_paged_split_reduce_ex(const psk_paged_attention_args* a,
+                                                   const float* partials, uint32_t splits,
+                                                   uint32_t pages_per_split, void* stream) {
+    if (a == nullptr || partials == nullptr) return hipErrorInvalidValue;
+    if (a->rows == 0u || a->head_dim == 0u || a->head_dim > ps::kernel::kPagedAttentionHeadLimit)
+        return hipErrorInvalidValue;
+    if (a->q_heads == 0u || a->kv_heads == 0u || a->q_heads % a->kv_heads != 0u)
+        return hipErrorInvalidValue;
+    if (a->output == nullptr || a->row_sequence_slots == nullptr || a->row_positions == nullptr)
+        return hipErrorInvalidValue;
+    if (a->page_tokens == 0u || splits == 0u || splits > psk::kMaxSplits) return hipErrorInvalidValue;
+    return psk::launch_reduce(
+        psk::make(*a, nullptr, nullptr, nullptr, nullptr, const_cast<float*>(partials), splits,
+                  pages_per_split),
+        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int psk_attention_paged_bf16_split_reduce(const psk_paged_attention_args* a,
+                                                     const float* partials, uint32_t splits,
+                                                     void* stream) {
+    if (splits != 2u && splits != 4u && splits != 8u && splits != 16u) return hipErrorInvalidValue;
+    return psk_attention_paged_split_reduce_ex(a, partials, splits, 0u, stream);
+}
+
+// ------------------------------------------------- reference C++ signatures
+namespace ps::kernel {
+
+static const psk_paged_attention_args* C(const PagedAttentionCommonArgs& c) {
+    return reinterpret_cast<const psk_paged_attention_args*>(&c);
+}
+
+hipError_t launch_attention_paged_bf16(const PagedAttentionCommonArgs& common, const bf16_t* k_pool,
+                                       const bf16_t* v_pool, hipStream_t stream) {
+    return static_cast<hipError_t>(psk_attention_paged_bf16(C(common), k_pool, v_pool, stream));
+}
+
+hipError_t launch_attention_paged_fp8_e4m3(const PagedAttentionCommonArgs& common,
+                                           const ::ps::qwen35::fp8e4m3_storage_t* k_pool,
+                                           const ::ps::qwen35::fp8e4m3_storage_t* v_pool,
+                                           const float* k_scale_pool, const float* v_scale_pool,
+                                           hipStream_t stream) {
+    return static_cast<hipError_t>(psk_attention_paged_fp8_e4m3(C(common), k_pool, v_pool,
+                                                                k_scale_pool, v_scale_pool, stream));
+}
+
+hipError_t launch_attention_paged_bf16_split(const PagedAttentionCommonArgs& common,
+                                             const bf16_t* k_pool, const bf16_t* v_pool,
+                                             float* partials, uint32_t splits, hipStream_t stream) {
+    return static_cast<hipError_t>(
+        psk_attention_paged_bf16_split(C(common), k_pool, v_pool, partials, splits, stream));
+}
+
+hipError_t launch_attention_paged_bf16_split_reduce(const PagedAttentionCommonArgs& common,
+                                                    const float* partials, uint32_t splits,
+                                                    hipStream_t stream) {
+    return static_cast<hipError_t>(
+        psk_attention_paged_bf16_split_reduce(C(common), partials, splits, stream));
+}
+
+hipError_t launch_attention_paged_fp8_e4m3_split(
+    const PagedAttentionCommonArgs& common, const ::ps::qwen35::fp8e4m3_storage_t* k_pool,
+    const ::ps::qwen35::fp8e4m3_storage_t* v_pool, const float* k_scale_pool,
+    const float* v_scale_pool, float* partials, uint32_t splits, uint32_t pages_per_split,
+    hipStream_t stream) {
+    return static_cast<hipError_t>(psk_attention_paged_fp8_e4m3_split(
+        C(common), k_pool, v_pool, k_scale_pool, v_scale_pool, partials, splits, pages_per_split,
+        stream));
+}
+
+hipError_t launch_attention_paged_split_reduce_ex(const PagedAttentionCommonArgs& common,
+                                                  const float* partials, uint32_t splits,
+                                                  uint32_t pages_per_split, hipStream_t stream) {
+    return static_cast<hipError_t>(
+        psk_attention_paged_split_reduce_ex(C(common), partials, splits, pages_per_split, stream));
+}
+
+}  // namespace ps::kernel

@@ -1,0 +1,236 @@
+"""Torch-tensor front of the C-ABI: fills the argument structs from tensors and
+calls the HIP library on the current torch stream.
+
+The geometry and argument meaning are the reference's launcher contract
+(include/phaseshift/models/qwen35/kernels/optimized/kv_append.h:12-41,
+attention/paged_attention.h:42-78); errors surface as HipError carrying the
+hipError_t code the launcher returned (hipErrorInvalidValue on bad geometry or
+null pointers, hipErrorNotSupported on shapes no kernel handles).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import (KV_BF16, KV_FP8, OUT_BF16, OUT_F32, KvAppendArgs, KvGatherArgs, PageCopyArgs,
+               PagedAttentionArgs, RequestDescriptor, check, lib)
+
+
+@dataclass(frozen=True)
+class PoolGeometry:
+    """KV pool geometry: [layers][num_pages][page_tokens][kv_heads][head_dim]
+    (reference state/paged_kv_pool.cpp:64-75)."""
+    num_layers: int
+    num_pages: int
+    page_tokens: int
+    kv_heads: int
+    head_dim: int
+
+    @property
+    def elems_per_token(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    @property
+    def elems_per_page(self) -> int:
+        return self.page_tokens * self.elems_per_token
+
+    @property
+    def elems_per_layer(self) -> int:
+        return self.num_pages * self.elems_per_page
+
+    @property
+    def pool_elems(self) -> int:
+        return self.num_layers * self.elems_per_layer
+
+    @property
+    def scale_elems(self) -> int:
+        return self.num_layers * self.num_pages * self.page_tokens * self.kv_heads
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else stream
+
+
+def _check_u32(*ts):
+    for t in ts:
+        if t is not None and t.dtype not in (torch.int32, torch.uint32):
+            raise TypeError("row metadata and block tables must be 32-bit integer tensors")
+
+
+def append_args(geom: PoolGeometry, layer: int, k_in, v_in, slots, positions, block_tables,
+                max_sequences: int | None = None) -> KvAppendArgs:
+    _check_u32(slots, positions, block_tables)
+    a = KvAppendArgs()
+    a.k_input, a.v_input = _ptr(k_in), _ptr(v_in)
+    a.k_row_stride, a.v_row_stride = k_in.stride(0), v_in.stride(0)
+    a.row_sequence_slots, a.row_positions = _ptr(slots), _ptr(positions)
+    a.block_tables = _ptr(block_tables)
+    a.block_table_stride = block_tables.shape[1]
+    a.max_sequences = block_tables.shape[0] if max_sequences is None else max_sequences
+    a.rows = k_in.shape[0]
+    a.layer = layer
+    a.page_tokens, a.num_pages = geom.page_tokens, geom.num_pages
+    a.num_attention_layers = geom.num_layers
+    a.kv_heads, a.head_dim = geom.kv_heads, geom.head_dim
+    a.elems_per_token, a.elems_per_page = geom.elems_per_token, geom.elems_per_page
+    a.elems_per_layer = geom.elems_per_layer
+    return a
+
+
+def kv_append(geom: PoolGeometry, layer: int, k_in, v_in, slots, positions, block_tables,
+              k_pool, v_pool, k_scale=None, v_scale=None, stream=None,
+              max_sequences: int | None = None) -> None:
+    """launch_kv_append_bf16 / launch_kv_append_fp8_e4m3 (kv_append.h:78-97)."""
+    a = append_args(geom, layer, k_in, v_in, slots, positions, block_tables, max_sequences)
+    s = _stream(stream)
+    if k_pool.dtype == torch.uint8:
+        check("psk_kv_append_fp8_e4m3", lib().psk_kv_append_fp8_e4m3(
+            C.byref(a), _ptr(k_pool), _ptr(v_pool), _ptr(k_scale), _ptr(v_scale), s))
+    else:
+        check("psk_kv_append_bf16", lib().psk_kv_append_bf16(
+            C.byref(a), _ptr(k_pool), _ptr(v_pool), s))
+
+
+def attention_args(geom: PoolGeometry, layer: int, q, out, slots, positions, block_tables,
+                   q_heads: int, scale: float | None = None,
+                   max_sequences: int | None = None) -> PagedAttentionArgs:
+    _check_u32(slots, positions, block_tables)
+    a = PagedAttentionArgs()
+    a.q, a.output = _ptr(q), _ptr(out)
+    a.output_dtype = OUT_F32 if out.dtype == torch.float32 else OUT_BF16
+    a.q_row_stride, a.output_row_stride = q.stride(0), out.stride(0)
+    a.row_sequence_slots, a.row_positions = _ptr(slots), _ptr(positions)
+    a.block_tables = _ptr(block_tables)
+    a.block_table_stride = block_tables.shape[1]
+    a.max_sequences = block_tables.shape[0] if max_sequences is None else max_sequences
+    a.rows = q.shape[0]
+    a.layer = layer
+    a.page_tokens, a.num_pages = geom.page_tokens, geom.num_pages
+    a.num_attention_layers = geom.num_layers
+    a.q_heads, a.kv_heads, a.head_dim = q_heads, geom.kv_heads, geom.head_dim
+    a.elems_per_token, a.elems_per_page = geom.elems_per_token, geom.elems_per_page
+    a.elems_per_layer = geom.elems_per_layer
+    a.scale = 1.0 / math.sqrt(geom.head_dim) if scale is None else scale
+    return a
+
+
+def split_partials_bytes(rows: int, q_heads: int, kv_heads: int, splits: int) -> int:
+    return int(lib().psk_attention_split_partials_bytes(rows, q_heads, kv_heads, splits))
+
+
+def paged_attention(geom: PoolGeometry, layer: int, q, out, slots, positions, block_tables,
+                    k_pool, v_pool, q_heads: int, k_scale=None, v_scale=None,
+                    scale: float | None = None, splits: int = 1, pages_per_split: int = 0,
+                    partials=None, stream=None, max_sequences: int | None = None,
+                    kind: str = "decode") -> None:
+    """Paged attention. splits == 1: launch_attention_paged_{bf16,fp8_e4m3};
+    splits > 1: the split kernel into `partials`, then the combine.
+    kind == "prefill": launch_attention_paged_prefill_* (multi-row tiles)."""
+    a = attention_args(geom, layer, q, out, slots, positions, block_tables, q_heads, scale,
+                       max_sequences)
+    s = _stream(stream)
+    L = lib()
+    fp8 = k_pool.dtype == torch.uint8
+    if kind == "prefill":
+        if fp8:
+            check("prefill_fp8", L.psk_attention_paged_prefill_fp8_e4m3(
+                C.byref(a), _ptr(k_pool), _ptr(v_pool), _ptr(k_scale), _ptr(v_scale), s))
+        else:
+            check("prefill_bf16", L.psk_attention_paged_prefill_bf16(
+                C.byref(a), _ptr(k_pool), _ptr(v_pool), s))
+        return
+    if splits <= 1:
+        if fp8:
+            check("psk_attention_paged_fp8_e4m3", L.psk_attention_paged_fp8_e4m3(
+                C.byref(a), _ptr(k_pool), _ptr(v_pool), _ptr(k_scale), _ptr(v_scale), s))
+        else:
+            check("psk_attention_paged_bf16", L.psk_attention_paged_bf16(
+                C.byref(a), _ptr(k_pool), _ptr(v_pool), s))
+        return
+    need = split_partials_bytes(q.shape[0], q_heads, geom.kv_heads, splits)
+    if partials is None or partials.numel() * partials.element_size() < need:
+        raise ValueError(f"partials workspace must hold {need} bytes")
+    if fp8:
+        check("psk_attention_paged_fp8_e4m3_split", L.psk_attention_paged_fp8_e4m3_split(
+            C.byref(a), _ptr(k_pool), _ptr(v_pool), _ptr(k_scale), _ptr(v_scale),
+            _ptr(partials), splits, pages_per_split, s))
+    else:
+        check("psk_attention_paged_bf16_split_ex", L.psk_attention_paged_bf16_split_ex(
+            C.byref(a), _ptr(k_pool), _ptr(v_pool), _ptr(partials), splits, pages_per_split, s))
+    check("psk_attention_paged_split_reduce_ex", L.psk_attention_paged_split_reduce_ex(
+        C.byref(a), _ptr(partials), splits, pages_per_split, s))
+
+
+def kv_gather(geom: PoolGeometry, layer: int, pool, block_tables, seq_slots, seq_offsets,
+              out, elem_bytes: int | None = None, elems_per_token: int | None = None,
+              elems_per_page: int | None = None, max_sequences: int | None = None,
+              stream=None) -> None:
+    """psk_kv_gather: paged pool -> out[token][elems_per_token]."""
+    _check_u32(block_tables, seq_slots, seq_offsets)
+    a = KvGatherArgs()
+    a.block_tables, a.seq_slots, a.seq_token_offsets = (
+        _ptr(block_tables), _ptr(seq_slots), _ptr(seq_offsets))
+    a.block_table_stride = block_tables.shape[1]
+    a.max_sequences = block_tables.shape[0] if max_sequences is None else max_sequences
+    a.num_seqs = seq_slots.shape[0]
+    a.total_tokens = out.shape[0]
+    a.layer = layer
+    a.page_tokens, a.num_pages = geom.page_tokens, geom.num_pages
+    a.kv_heads, a.head_dim = geom.kv_heads, geom.head_dim
+    ept = elems_per_token or geom.elems_per_token
+    epp = elems_per_page or geom.page_tokens * ept
+    a.elems_per_token, a.elems_per_page = ept, epp
+    a.elems_per_layer = epp * geom.num_pages
+    eb = elem_bytes or pool.element_size()
+    check("psk_kv_gather", lib().psk_kv_gather(C.byref(a), _ptr(pool), _ptr(out), eb,
+                                               _stream(stream)))
+
+
+def copy_pages(geom: PoolGeometry, dst: dict, src: dict, pairs, src_num_pages: int | None = None,
+               stream=None) -> None:
+    """psk_kv_copy_pages: pairs is an int32 device tensor [n, 2] of (dst_page, src_page)."""
+    a = PageCopyArgs()
+    a.dst_k, a.dst_v = _ptr(dst["k"]), _ptr(dst["v"])
+    a.dst_k_scale, a.dst_v_scale = _ptr(dst.get("k_scale")), _ptr(dst.get("v_scale"))
+    a.src_k, a.src_v = _ptr(src["k"]), _ptr(src["v"])
+    a.src_k_scale, a.src_v_scale = _ptr(src.get("k_scale")), _ptr(src.get("v_scale"))
+    a.pairs = _ptr(pairs)
+    a.num_pairs = pairs.shape[0]
+    a.num_layers = geom.num_layers
+    a.dst_num_pages = geom.num_pages
+    a.src_num_pages = geom.num_pages if src_num_pages is None else src_num_pages
+    a.page_tokens, a.kv_heads, a.head_dim = geom.page_tokens, geom.kv_heads, geom.head_dim
+    a.kv_dtype = KV_FP8 if dst["k"].dtype == torch.uint8 else KV_BF16
+    check("psk_kv_copy_pages", lib().psk_kv_copy_pages(C.byref(a), _stream(stream)))
+
+
+def fill_u32(dst, value: int, stream=None) -> None:
+    check("psk_fill_u32", lib().psk_fill_u32(_ptr(dst), value & 0xFFFFFFFF, dst.numel(),
+                                             _stream(stream)))
+
+
+def prepare_row_metadata(requests_dev, num_requests: int, actual_rows: int, slots, positions,
+                         stream=None) -> None:
+    """requests_dev: uint8 device tensor holding num_requests RequestDescriptor (64 B each)."""
+    check("psk_prepare_row_metadata", lib().psk_prepare_row_metadata(
+        _ptr(requests_dev), num_requests, actual_rows, _ptr(slots), _ptr(positions),
+        _stream(stream)))
+
+
+def pack_requests(descs: list[dict]) -> bytes:
+    arr = (RequestDescriptor * len(descs))()
+    for i, d in enumerate(descs):
+        for k, v in d.items():
+            setattr(arr[i], k, v)
+        if "output_index" not in d:
+            arr[i].output_index = 0xFFFFFFFF
+    return bytes(arr)

@@ -1,0 +1,118 @@
+"""Seeded synthetic cases of the paged KV path (numpy, host side).
+
+Shapes follow the BASELINE configs and the reference's own test cases
+(tests/kernels/optimized/test_kv_append.hip:562-637,
+tests/kernels/optimized/test_paged_attention.hip:585-743).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+import oracle
+
+INVALID = 0xFFFFFFFF
+
+
+def bf16_normal(rng, shape, outlier_frac=0.0, outlier_mult=20.0):
+    x = rng.standard_normal(shape, dtype=np.float32)
+    if outlier_frac:
+        m = rng.random(shape) < outlier_frac
+        x = np.where(m, x * outlier_mult, x).astype(np.float32)
+    return oracle.f32_to_bf16(x)
+
+
+@dataclass
+class Layout:
+    num_layers: int
+    num_pages: int
+    page_tokens: int
+    kv_heads: int
+    head_dim: int
+    block_tables: np.ndarray   # uint32 [max_sequences][stride]
+    slots: np.ndarray = field(default=None)
+    positions: np.ndarray = field(default=None)
+
+    @property
+    def geom(self) -> dict:
+        return dict(layer=0, page_tokens=self.page_tokens, num_pages=self.num_pages,
+                    num_attention_layers=self.num_layers, kv_heads=self.kv_heads,
+                    head_dim=self.head_dim, block_table_stride=self.block_tables.shape[1],
+                    max_sequences=self.block_tables.shape[0])
+
+    @property
+    def pool_elems(self) -> int:
+        return self.num_layers * self.num_pages * self.page_tokens * self.kv_heads * self.head_dim
+
+    @property
+    def scale_elems(self) -> int:
+        return self.num_layers * self.num_pages * self.page_tokens * self.kv_heads
+
+
+def paged_layout(rng, seq_lens, page_tokens, kv_heads, head_dim, num_layers=1, spare_pages=0,
+                 stride=None) -> Layout:
+    """Pages of every sequence drawn from one seeded permutation of the pool."""
+    need = [(int(n) + page_tokens - 1) // page_tokens for n in seq_lens]
+    num_pages = sum(need) + spare_pages
+    stride = stride or max(max(need), 1)
+    perm = rng.permutation(num_pages).astype(np.uint32)
+    bt = np.full((len(seq_lens), stride), INVALID, np.uint32)
+    k = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = perm[k:k + n]
+        k += n
+    return Layout(num_layers, num_pages, page_tokens, kv_heads, head_dim, bt)
+
+
+def random_fp8_codes(rng, n):
+    c = rng.integers(0, 256, n, dtype=np.uint8)
+    return np.where((c & 0x7F) == 0x7F, c ^ 0x01, c).astype(np.uint8)
+
+
+def to_dev(a, device="cuda"):
+    """numpy -> torch device tensor, bit-preserving (u32 -> i32, u16 -> i16)."""
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    elif a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to(device)
+
+
+def to_host(t, dtype=None):
+    """torch tensor -> numpy with the bit pattern kept (i32 -> u32, i16 -> u16)."""
+    import torch
+    a = t.detach().cpu()
+    if a.dtype == torch.int32:
+        return a.numpy().view(np.uint32)
+    if a.dtype in (torch.int16, torch.bfloat16):
+        return a.view(torch.int16).numpy().view(np.uint16)
+    return a.numpy()
+
+
+def oracle_attention_parallel(geom, q, slots, positions, block_tables, kp, vp, ks=None, vs=None,
+                              scale=None, output_dtype="f32", out=None, workers=8):
+    """oracle.paged_attention over row chunks in threads (ctypes drops the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+    rows = q.shape[0]
+    H, D = geom["q_heads"], geom["head_dim"]
+    if out is None:
+        out = np.zeros((rows, H * D), np.float32 if output_dtype == "f32" else np.uint16)
+    slots = np.asarray(slots, np.uint32)
+    positions = np.asarray(positions, np.uint32)
+    bounds = np.linspace(0, rows, min(workers, rows) + 1).astype(int)
+
+    def job(i):
+        a, b = bounds[i], bounds[i + 1]
+        if a == b:
+            return
+        o = np.ascontiguousarray(out[a:b])
+        oracle.paged_attention(geom, q[a:b], slots[a:b], positions[a:b], block_tables, kp, vp,
+                               ks, vs, scale, output_dtype, out=o)
+        out[a:b] = o
+
+    with ThreadPoolExecutor(len(bounds) - 1) as ex:
+        list(ex.map(job, range(len(bounds) - 1)))
+    return out

@@ -1,0 +1,140 @@
+"""Pins the oracle's E4M3 and bf16 codecs.
+
+Evidence, each independent of the oracle's own formulas:
+  * the OCP E4M3 known-answer list of the reference's codec test
+    (tests/unit/test_ocp_e4m3_codec.cpp:54-103);
+  * exhaustive equality with the reference's own e4m3.cpp / f32_to_bf16_rne,
+    compiled from the reference sources into oracle/_ref (skipped when absent);
+  * ROCm's hip_fp8.h SATFINITE converter (tests/golden, gen_fp8_golden.cpp);
+  * torch's float32 -> bfloat16 cast (round to nearest even).
+"""
+import math
+import os
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def enc(x):
+    return int(oracle.e4m3_encode(np.array([x], np.float32))[0])
+
+
+def test_e4m3_decode_all_256_closed_form():
+    codes = np.arange(256, dtype=np.uint8)
+    got = oracle.e4m3_decode(codes)
+    for c in range(256):
+        s = -1.0 if c & 0x80 else 1.0
+        e, m = (c >> 3) & 15, c & 7
+        if (c & 0x7F) == 0x7F:
+            assert math.isnan(got[c])
+            continue
+        want = s * (math.ldexp(m, -9) if e == 0 else math.ldexp(8 + m, e - 10))
+        assert got[c] == np.float32(want), c
+    assert got[0x38] == 1.0 and got[0x08] == 2.0 ** -6 and got[0x7E] == 448.0
+    assert got[0x80] == 0.0 and math.copysign(1, got[0x80]) < 0
+
+
+def test_e4m3_known_answers():
+    # test_ocp_e4m3_codec.cpp:74-91
+    kat = [(0.0, 0x00), (-0.0, 0x80), (448.0, 0x7E), (-448.0, 0xFE),
+           (float(np.nextafter(np.float32(448), np.float32(1e30))), 0x7E),
+           (-float(np.nextafter(np.float32(448), np.float32(1e30))), 0xFE),
+           (math.inf, 0x7E), (-math.inf, 0xFE), (math.nan, 0x7F),
+           (2.0 ** -9, 0x01), (7 * 2.0 ** -9, 0x07), (2.0 ** -11, 0x00), (2.0 ** -10, 0x00),
+           (1.5 * 2.0 ** -9, 0x02), (1e-30, 0x00), (1.0625, 0x38), (1.1875, 0x3A),
+           (0.0302734375, 0x10)]
+    for x, c in kat:
+        assert enc(x) == c, (x, hex(enc(x)), hex(c))
+
+
+def test_e4m3_roundtrip_every_finite_code():
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    assert np.array_equal(oracle.e4m3_encode(oracle.e4m3_decode(codes)), codes)
+
+
+def test_e4m3_random_idempotent():
+    # test_ocp_e4m3_codec.cpp:93-103 (distribution U(-1000, 1000))
+    rng = np.random.default_rng(20260826)
+    x = rng.uniform(-1000, 1000, 200000).astype(np.float32)
+    c = oracle.e4m3_encode(x)
+    d = oracle.e4m3_decode(c)
+    assert np.array_equal(oracle.e4m3_encode(d), c)
+    nz = (np.abs(x) > 1e-7) & (d != 0)
+    assert np.array_equal(np.signbit(d[nz]), np.signbit(x[nz]))
+
+
+def test_e4m3_matches_rocm_hip_fp8_converter():
+    x = np.fromfile(os.path.join(GOLDEN, "e4m3_rocm_inputs.f32"), np.float32)
+    c = np.fromfile(os.path.join(GOLDEN, "e4m3_rocm_codes.u8"), np.uint8)
+    got = oracle.e4m3_encode(x)
+    # ROCm's host (software) path returns nonzero codes for |x| in about
+    # [2^-75, 2^-69]; the exact OCP result there is 0 (the reference's own
+    # e4m3.cpp agrees with the oracle on every float, see the exhaustive test).
+    # The device path the reference runs is the hardware converter, checked
+    # exhaustively against the oracle by the GPU self-test.
+    tiny = np.abs(x) < 2.0 ** -60
+    assert np.array_equal(got[~tiny], c[~tiny])
+    assert np.all(got[tiny] & 0x7F == 0)
+    assert (~tiny).sum() > 90000
+
+
+@pytest.mark.skipif(oracle.ref_lib() is None, reason="oracle/_ref not built (no reference tree)")
+def test_e4m3_encode_exhaustive_vs_reference_codec():
+    R, L = oracle.ref_lib(), oracle.lib()
+    R.ref_e4m3_encode_range(0, 1, np.zeros(1, np.uint8))   # builds its static table once
+    CH = 1 << 26
+
+    def job(i):
+        a = np.empty(CH, np.uint8)
+        b = np.empty(CH, np.uint8)
+        L.or_e4m3_encode_range(i * CH, CH, a)
+        R.ref_e4m3_encode_range(i * CH, CH, b)
+        return int(np.count_nonzero(a != b))
+
+    with ThreadPoolExecutor(8) as ex:
+        bad = sum(ex.map(job, range(1 << 6)))
+    assert bad == 0
+
+
+@pytest.mark.skipif(oracle.ref_lib() is None, reason="oracle/_ref not built (no reference tree)")
+def test_e4m3_decode_vs_reference_codec():
+    ref = np.empty(256, np.float32)
+    oracle.ref_lib().ref_e4m3_decode_all(ref)
+    got = oracle.e4m3_decode(np.arange(256, dtype=np.uint8))
+    assert np.array_equal(np.isnan(ref), np.isnan(got))
+    fin = ~np.isnan(ref)
+    assert np.array_equal(ref[fin].view(np.uint32), got[fin].view(np.uint32))
+
+
+def test_bf16_rne_vs_torch_cast():
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2 ** 32, 4_000_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.f32_to_bf16(x), want)
+    # ties: exactly halfway values round to even
+    t = np.array([0x3F808000, 0x3F818000, 0xBF808000], np.uint32).view(np.float32)
+    assert list(oracle.f32_to_bf16(t)) == [0x3F80, 0x3F82, 0xBF80]
+    assert oracle.f32_to_bf16(np.array([np.nan], np.float32))[0] == 0x7FC0
+
+
+@pytest.mark.skipif(oracle.ref_lib() is None, reason="oracle/_ref not built (no reference tree)")
+def test_bf16_rne_exhaustive_vs_reference():
+    R = oracle.ref_lib()
+    CH = 1 << 26
+
+    def job(i):
+        a = np.empty(CH, np.uint16)
+        R.ref_f32_to_bf16_range(i * CH, CH, a)
+        x = (np.arange(CH, dtype=np.uint64) + i * CH).astype(np.uint32).view(np.float32)
+        return int(np.count_nonzero(oracle.f32_to_bf16(x) != a))
+
+    with ThreadPoolExecutor(8) as ex:
+        assert sum(ex.map(job, range(64))) == 0

@@ -1,0 +1,220 @@
+"""Pins the oracle's append, gather, attention, combine and page copy.
+
+Append: ROCm-converter golden fixture (bit-exact codes and scales), the
+byte-copy closed form, the reference's skip rules. Attention: closed forms
+(single visible token -> V; equal keys -> mean of V), invariance under page
+permutation, a float64 numpy softmax, and split-combine == unsplit."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.kvcase import INVALID, bf16_normal, paged_layout, random_fp8_codes
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def test_fp8_append_matches_rocm_golden():
+    R, H, D = 128, 4, 256
+    for t in "kv":
+        xin = np.fromfile(f"{GOLDEN}/fp8_append_{t}_in.bf16", np.uint16).reshape(R, H * D)
+        codes = np.fromfile(f"{GOLDEN}/fp8_append_{t}_codes.u8", np.uint8).reshape(R, H, D)
+        sc = np.fromfile(f"{GOLDEN}/fp8_append_{t}_scale.f32", np.float32).reshape(R, H)
+        geom = dict(layer=0, page_tokens=16, num_pages=R, num_attention_layers=1, kv_heads=H,
+                    head_dim=D, block_table_stride=1, max_sequences=R)
+        kp = np.zeros(R * 16 * H * D, np.uint8)
+        vp = kp.copy()
+        ks = np.zeros(R * 16 * H, np.float32)
+        vs = ks.copy()
+        bt = np.arange(R, dtype=np.uint32).reshape(R, 1)
+        pos = np.arange(R, dtype=np.uint32) % 16   # every slot of a page
+        oracle.kv_append(geom, xin, xin, np.arange(R), pos, bt, kp, vp, ks, vs)
+        kp = kp.reshape(R, 16, H, D)[np.arange(R), pos]
+        ks = ks.reshape(R, 16, H)[np.arange(R), pos]
+        assert np.array_equal(kp, codes)
+        assert np.array_equal(ks.view(np.uint32), sc.view(np.uint32))
+        assert np.all(ks[5, 2] == 1.0)   # all-zero head -> scale 1.0
+
+
+def test_bf16_append_is_a_byte_copy_and_skips_bad_rows():
+    rng = np.random.default_rng(7)
+    lens = [7, 33, 64, 100]
+    lay = paged_layout(rng, lens, 16, 2, 128, spare_pages=64 - 15)
+    rows = sum(lens)
+    slots = np.repeat(np.arange(4), lens).astype(np.uint32)
+    pos = np.concatenate([np.arange(n) for n in lens]).astype(np.uint32)
+    k = bf16_normal(rng, (rows, 256))
+    v = bf16_normal(rng, (rows, 256))
+    kp = np.full(lay.pool_elems, 0x3F3F, np.uint16)
+    vp = kp.copy()
+    # corrupt three rows: bad slot, position past the table, invalid page
+    slots_b, pos_b = slots.copy(), pos.copy()
+    bt = lay.block_tables.copy()
+    slots_b[3] = 99
+    pos_b[40] = 16 * bt.shape[1] + 1
+    bt[2, 1] = INVALID   # rows of seq 2 at positions 16..31
+    oracle.kv_append(lay.geom, k, v, slots_b, pos_b, bt, kp, vp)
+    kp4 = kp.reshape(64, 16, 2, 128)
+    expect_written = np.zeros(64 * 16, bool)
+    for r in range(rows):
+        s, p = slots_b[r], pos_b[r]
+        if s >= 4 or p // 16 >= bt.shape[1] or bt[s, p // 16] >= 64:
+            continue
+        page, off = bt[s, p // 16], p % 16
+        assert np.array_equal(kp4[page, off].reshape(-1), k[r])
+        expect_written[page * 16 + off] = True
+    untouched = kp.reshape(64 * 16, 256)[~expect_written]
+    assert np.all(untouched == 0x3F3F)   # sentinel bytes untouched
+
+
+def test_gather_inverts_append():
+    rng = np.random.default_rng(3)
+    lens = [7, 33, 64, 100]
+    lay = paged_layout(rng, lens, 16, 2, 128, spare_pages=64 - 15)
+    rows = sum(lens)
+    slots = np.repeat(np.arange(4), lens)
+    pos = np.concatenate([np.arange(n) for n in lens])
+    k = bf16_normal(rng, (rows, 256))
+    kp = np.zeros(lay.pool_elems, np.uint16)
+    vp = kp.copy()
+    oracle.kv_append(lay.geom, k, k, slots, pos, lay.block_tables, kp, vp)
+    out = oracle.kv_gather(lay.geom, kp, lay.block_tables, np.arange(4), lens)
+    assert np.array_equal(out, k)
+
+
+def _attn_case(rng, lens, qh, kvh, D, P, fp8):
+    lay = paged_layout(rng, lens, P, kvh, D, spare_pages=3)
+    if fp8:
+        kp = random_fp8_codes(rng, lay.pool_elems)
+        vp = random_fp8_codes(rng, lay.pool_elems)
+        ks = rng.uniform(0.001, 0.02, lay.scale_elems).astype(np.float32)
+        vs = rng.uniform(0.001, 0.02, lay.scale_elems).astype(np.float32)
+    else:
+        kp = bf16_normal(rng, lay.pool_elems)
+        vp = bf16_normal(rng, lay.pool_elems)
+        ks = vs = None
+    q = bf16_normal(rng, (len(lens), qh * D))
+    g = dict(lay.geom, q_heads=qh)
+    return lay, g, q, kp, vp, ks, vs
+
+
+def _numpy_attention(lay, g, q, kp, vp, ks, vs, slots, pos, scale):
+    """float64 restatement: gather K/V per row, softmax, weighted sum."""
+    qh, kvh, D, P = g["q_heads"], g["kv_heads"], g["head_dim"], g["page_tokens"]
+    fp8 = kp.dtype == np.uint8
+    K = (oracle.e4m3_decode(kp) if fp8 else oracle.bf16_to_f32(kp)).astype(np.float64)
+    V = (oracle.e4m3_decode(vp) if fp8 else oracle.bf16_to_f32(vp)).astype(np.float64)
+    K = K.reshape(lay.num_pages, P, kvh, D)
+    V = V.reshape(lay.num_pages, P, kvh, D)
+    if fp8:
+        K = K * ks.reshape(lay.num_pages, P, kvh, 1)
+        V = V * vs.reshape(lay.num_pages, P, kvh, 1)
+    out = np.zeros((len(slots), qh * D))
+    Q = oracle.bf16_to_f32(q).astype(np.float64).reshape(len(slots), qh, D)
+    for r, (s, p) in enumerate(zip(slots, pos)):
+        t = np.arange(p + 1)
+        pages = lay.block_tables[s, t // P]
+        for h in range(qh):
+            kv = h // (qh // kvh)
+            kk = K[pages, t % P, kv]
+            vv = V[pages, t % P, kv]
+            sc = kk @ Q[r, h] * scale
+            w = np.exp(sc - sc.max())
+            out[r, h * D:(h + 1) * D] = (w[:, None] * vv).sum(0) / w.sum()
+    return out
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("qh,kvh,D,P", [(8, 4, 64, 16), (4, 4, 128, 16), (24, 4, 256, 16),
+                                        (8, 2, 32, 8)])
+def test_attention_vs_float64(fp8, qh, kvh, D, P):
+    rng = np.random.default_rng(qh * 1000 + D)
+    lens = [1, 17, 90, 300]
+    lay, g, q, kp, vp, ks, vs = _attn_case(rng, lens, qh, kvh, D, P, fp8)
+    slots = np.arange(4)
+    pos = np.array(lens) - 1
+    scale = 1.0 / np.sqrt(D)
+    got = oracle.paged_attention(g, q, slots, pos, lay.block_tables, kp, vp, ks, vs, scale)
+    want = _numpy_attention(lay, g, q, kp, vp, ks, vs, slots, pos, scale)
+    assert np.max(np.abs(got - want)) < 1e-4
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(11)
+    lay, g, q, kp, vp, ks, vs = _attn_case(rng, [1, 50], 6, 1, 64, 16, False)
+    got = oracle.paged_attention(g, q, [0, 1], [0, 49], lay.block_tables, kp, vp, scale=0.125)
+    # one visible token: output == V of that token, every head of the group
+    page0 = lay.block_tables[0, 0]
+    v0 = oracle.bf16_to_f32(vp.reshape(lay.num_pages, 16, 1, 64)[page0, 0, 0])
+    assert np.allclose(got[0].reshape(6, 64), v0[None], atol=0, rtol=0)
+    # equal keys: softmax uniform -> mean of V
+    kp2 = kp.reshape(lay.num_pages, 16, 1, 64).copy()
+    kp2[:] = kp2[lay.block_tables[1, 0], 0]
+    got2 = oracle.paged_attention(g, q, [1], [49], lay.block_tables, kp2.reshape(-1), vp,
+                                  scale=0.125)
+    t = np.arange(50)
+    vv = oracle.bf16_to_f32(vp.reshape(lay.num_pages, 16, 1, 64)[lay.block_tables[1, t // 16],
+                                                                  t % 16, 0])
+    assert np.allclose(got2[0].reshape(6, 64), vv.mean(0)[None], atol=1e-5)
+
+
+def test_attention_invalid_rows_left_unwritten():
+    rng = np.random.default_rng(5)
+    lay, g, q, kp, vp, ks, vs = _attn_case(rng, [40, 40, 40], 8, 4, 64, 16, False)
+    bt = lay.block_tables.copy()
+    bt[1, 1] = INVALID
+    out = np.full((3, 8 * 64), 7.0, np.float32)
+    oracle.paged_attention(g, q, [0, 1, 9], [39, 39, 39], bt, kp, vp, out=out)
+    assert np.all(out[1] == 7.0) and np.all(out[2] == 7.0) and not np.all(out[0] == 7.0)
+
+
+def test_split_combine_equals_unsplit():
+    """Partials built per split by restricting visibility, combined by
+    or_split_reduce, equal the unsplit result (paged_decode.hip:474-555)."""
+    rng = np.random.default_rng(9)
+    qh, kvh, D, P = 8, 2, 64, 16
+    lay, g, q, kp, vp, ks, vs = _attn_case(rng, [200, 37], qh, kvh, D, P, False)
+    qpk = qh // kvh
+    splits = 4
+    full = oracle.paged_attention(g, q, [0, 1], [199, 36], lay.block_tables, kp, vp)
+    K = oracle.bf16_to_f32(kp).reshape(lay.num_pages, P, kvh, D).astype(np.float32)
+    V = oracle.bf16_to_f32(vp).reshape(lay.num_pages, P, kvh, D).astype(np.float32)
+    Q = oracle.bf16_to_f32(q).reshape(2, qh, D)
+    part = np.zeros((2, kvh, splits, qpk * 258), np.float32)
+    n_used = []
+    for r, n in enumerate([200, 37]):
+        pc = (n + P - 1) // P
+        per = (pc + splits - 1) // splits
+        n_used.append((pc + per - 1) // per)
+        for s in range(splits):
+            t = np.arange(s * per * P, min((s + 1) * per * P, n))
+            for kv in range(kvh):
+                for j in range(qpk):
+                    if len(t) == 0:
+                        continue
+                    pg = lay.block_tables[r, t // P]
+                    sc = K[pg, t % P, kv] @ Q[r, kv * qpk + j] / np.sqrt(D)
+                    m = sc.max()
+                    w = np.exp(sc - m)
+                    part[r, kv, s, j] = m
+                    part[r, kv, s, qpk + j] = w.sum()
+                    part[r, kv, s, 2 * qpk + j * 256: 2 * qpk + j * 256 + D] = w @ V[pg, t % P, kv]
+    got = oracle.split_reduce(g, part, splits, n_used, [0, 1], 2)
+    assert np.max(np.abs(got - full)) < 1e-5
+
+
+def test_copy_page_copies_every_layer_and_scales():
+    rng = np.random.default_rng(2)
+    L, NP, P, H, D = 3, 5, 16, 4, 256
+    src = {k: random_fp8_codes(rng, L * NP * P * H * D) for k in "kv"}
+    src.update({k + "_scale": rng.random(L * NP * P * H).astype(np.float32) for k in "kv"})
+    dst = {k: np.zeros_like(v) for k, v in src.items()}
+    oracle.copy_page(dst, src, 4, 1, dict(layers=L, dst_num_pages=NP, src_num_pages=NP,
+                                          page_tokens=P, kv_heads=H, head_dim=D))
+    for k in "kv":
+        a = dst[k].reshape(L, NP, -1)
+        b = src[k].reshape(L, NP, -1)
+        assert np.array_equal(a[:, 4], b[:, 1]) and not a[:, :4].any()
+        a = dst[k + "_scale"].reshape(L, NP, -1)
+        assert np.array_equal(a[:, 4], src[k + "_scale"].reshape(L, NP, -1)[:, 1])
