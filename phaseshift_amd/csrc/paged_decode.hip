@@ -46,13 +46,9 @@ struct DecodeParams {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kChunk = 32;       // tokens per wave iteration
 constexpr int kMaxQPerKV = 16;
 constexpr uint32_t kMaxSplits = 1024;
 using ps::kernel::kPagedAttentionHeadLimit;
-
-template <int KVB>
-constexpr int lds_pitch() { return KVB == 1 ? 40 : 80; }   // bytes per dim row of a V^T tile
 
 __device__ __forceinline__ uint32_t split_pages(uint32_t pc, uint32_t splits, uint32_t pps) {
     return pps != 0u ? pps : (pc + splits - 1u) / splits;
@@ -68,12 +64,36 @@ __device__ __forceinline__ bf16x8 load_q8(const uint16_t* q, bool ok) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
+template <int KVB>
+constexpr int chunk_halves() { return KVB == 1 ? 2 : 1; }   // 16-token halves per chunk
+
 template <int KVB, int D>
+constexpr int v_row_bytes() { return D * KVB + 16; }   // padded LDS row of one V token
+
+typedef __attribute__((ext_vector_type(2))) int i32x2;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// gfx950 transposing LDS reads. Within each 16-lane block, the 16 lanes name
+// 16 rows of 8 bytes: ds_read_b64_tr_b8 gives lane i byte i%8 of rows
+// 2j + i/8 (j = 0..7); ds_read_b64_tr_b16 gives lane i element i%4 of rows
+// 4j + i/4 (j = 0..3).
+__device__ __forceinline__ i32x2 lds_read_tr8(const uint8_t* p) {
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(p));
+}
+__device__ __forceinline__ i16x4 lds_read_tr16(const uint8_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+}
+
+template <int KVB, int D, bool kAl16>
 __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeParams p) {
+    constexpr int H = chunk_halves<KVB>();
+    constexpr int CT = 16 * H;         // tokens per wave iteration
     constexpr int NL = D * KVB / 64;   // 16 B loads per lane per 16-token half
     constexpr int NS = D / 32;         // MFMA K-steps of the score product
     constexpr int NDB = D / 16;        // 16-dim blocks of the output
-    constexpr int PITCH = lds_pitch<KVB>();
+    constexpr int VROW = v_row_bytes<KVB, D>();
     static_assert(NL >= 1 && NS >= 1, "head_dim too small for this kernel");
 
     extern __shared__ __align__(16) uint8_t lds[];
@@ -107,6 +127,9 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
     const uint32_t t_begin = pb * P;
     const uint32_t t_end = min(pe * P, visible);
     const uint32_t* bt = a.block_tables + (uint64_t)slot * a.block_table_stride;
+    // With page_tokens a multiple of 16, every 16-token half of a chunk lies in
+    // one page (chunks start page-aligned), so one table lookup serves it.
+    constexpr bool al16 = kAl16;   // launcher guarantees (P & 15) == 0
 
     const uint32_t qpk = a.q_heads / a.kv_heads;
     if (tid == 0) bad_shared = 0u;
@@ -128,73 +151,103 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
 
     const uint64_t layer_base = (uint64_t)a.layer * a.elems_per_layer;
     const uint64_t scale_layer = (uint64_t)a.layer * a.num_pages;
-    uint8_t* vt = lds + (size_t)wave * D * PITCH;
+    uint8_t* vt = lds + (size_t)wave * CT * VROW;
+    bool bad = false;
+
+    // Page id of half hf of the chunk at cb (al16 geometry), or invalid when the
+    // half starts past the split's range.
+    auto half_page = [&](uint32_t cb, int hf) -> uint32_t {
+        const uint32_t hb = cb + hf * 16;
+        return (al16 && hb < t_end) ? bt[hb / P] : 0xFFFFFFFFu;
+    };
+
+    // Issues the K/V loads of the chunk at `cb`: lane owns token n of each
+    // half, and (FP8) that token's k/v scales.
+    auto load_chunk = [&](uint32_t cb, const uint32_t (&pgs)[H], u32x4 (&kr)[H][NL],
+                          u32x4 (&vr)[H][NL], float (&ksl)[H], float (&vsl)[H]) {
+#pragma unroll
+        for (int hf = 0; hf < H; ++hf) {
+            const uint32_t tau = cb + hf * 16 + n;
+            bool ok = tau < t_end;
+            const uint32_t page = al16 ? pgs[hf] : (ok ? bt[tau / P] : 0xFFFFFFFFu);
+            if (ok && page >= a.num_pages) {
+                bad = true;
+                ok = false;
+            }
+            const uint32_t off = tau % P;
+            const uint64_t elem = ok ? layer_base + (uint64_t)page * a.elems_per_page +
+                                           (uint64_t)off * a.elems_per_token + (uint64_t)kv_head * D
+                                     : 0;
+            const uint8_t* kb = p.k_pool + elem * KVB + g * 16;
+            const uint8_t* vb = p.v_pool + elem * KVB + g * 16;
+#pragma unroll
+            for (int i = 0; i < NL; ++i) {
+                kr[hf][i] = ok ? *reinterpret_cast<const u32x4*>(kb + i * 64) : (u32x4){0u, 0u, 0u, 0u};
+                vr[hf][i] = ok ? *reinterpret_cast<const u32x4*>(vb + i * 64) : (u32x4){0u, 0u, 0u, 0u};
+            }
+            if constexpr (KVB == 1) {
+                const uint64_t si = ok ? ((scale_layer + page) * P + off) * a.kv_heads + kv_head : 0;
+                ksl[hf] = ok ? p.k_scale[si] : 0.0f;
+                vsl[hf] = ok ? p.v_scale[si] : 0.0f;
+            } else {
+                ksl[hf] = 1.0f;
+                vsl[hf] = 1.0f;
+            }
+        }
+    };
 
     float m_run = -INFINITY;   // running max (log2 units), head n
     float l_run = 0.0f;        // partial softmax sum of this lane's tokens
     f32x4 o[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    bool bad = false;
 
-    for (uint32_t cbase = t_begin + wave * kChunk; cbase < t_end; cbase += kWaves * kChunk) {
-        // ---- loads: lane owns token n of each 16-token half
-        u32x4 kr[2][NL], vr[2][NL];
+    constexpr uint32_t kStep = kWaves * CT;   // a wave's stride between chunks
+    u32x4 kr[H][NL], vr[H][NL];
+    float ksl[H], vsl[H];
+    uint32_t pg_next[H];
+    uint32_t cbase = t_begin + wave * CT;
+    {
+        uint32_t pg0[H];
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const uint32_t tau = cbase + hf * 16 + n;
-            bool ok = tau < t_end;
-            uint64_t elem = 0;
-            if (ok) {
-                const uint32_t page = bt[tau / P];
-                if (page >= a.num_pages) {
-                    bad = true;
-                    ok = false;
-                } else {
-                    elem = layer_base + (uint64_t)page * a.elems_per_page +
-                           (uint64_t)(tau % P) * a.elems_per_token + (uint64_t)kv_head * D;
-                }
-            }
-            const uint8_t* kb = p.k_pool + elem * KVB + g * 16;
-            const uint8_t* vb = p.v_pool + elem * KVB + g * 16;
-#pragma unroll
-            for (int i = 0; i < NL; ++i) {
-                if (ok) {
-                    kr[hf][i] = *reinterpret_cast<const u32x4*>(kb + i * 64);
-                    vr[hf][i] = *reinterpret_cast<const u32x4*>(vb + i * 64);
-                } else {
-                    kr[hf][i] = (u32x4){0u, 0u, 0u, 0u};
-                    vr[hf][i] = (u32x4){0u, 0u, 0u, 0u};
-                }
-            }
+        for (int hf = 0; hf < H; ++hf) {
+            pg0[hf] = half_page(cbase, hf);
+            pg_next[hf] = half_page(cbase + kStep, hf);
         }
+        if (cbase < t_end) load_chunk(cbase, pg0, kr, vr, ksl, vsl);
+    }
 
-        // ---- V^T into this wave's LDS tile: element (token slot k, dim d)
-        // at vt[d*PITCH + k*KVB], k = 8*(n/4) + n%4 + 4*hf.
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const uint32_t k = 8u * (n >> 2) + (n & 3u) + 4u * hf;
-#pragma unroll
-            for (int i = 0; i < NL; ++i) {
-                if constexpr (KVB == 1) {
-                    const uint32_t d0 = i * 64 + g * 16;
-#pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        vt[(d0 + e) * PITCH + k] = (uint8_t)(vr[hf][i][e >> 2] >> (8 * (e & 3)));
-                } else {
-                    const uint32_t d0 = i * 32 + g * 8;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        *reinterpret_cast<uint16_t*>(vt + (d0 + e) * PITCH + 2 * k) =
-                            (uint16_t)(vr[hf][i][e >> 1] >> (16 * (e & 1)));
-                }
-            }
-        }
+    // tr-read address of this lane inside the V tile (dim offset added per block)
+    uint32_t tr_off;
+    if constexpr (KVB == 1) {
+        const uint32_t j = n >> 1;
+        const uint32_t tok = j < 4u ? 4u * g + j : 16u + 4u * g + (j - 4u);
+        tr_off = tok * VROW + 8u * (n & 1u);
+    } else {
+        tr_off = (4u * g + (n >> 2)) * VROW + 8u * (n & 3u);
+    }
 
-        // ---- scores S^T (token x head) for both halves
-        f32x4 sc[2];
+    for (; cbase < t_end; cbase += kStep) {
+        // ---- V of this chunk into the wave's LDS tile, natural layout
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
+        for (int hf = 0; hf < H; ++hf)
+#pragma unroll
+            for (int i = 0; i < NL; ++i)
+                *reinterpret_cast<u32x4*>(vt + (hf * 16 + n) * VROW + i * 64 + g * 16) = vr[hf][i];
+
+        // ---- page ids two chunks ahead, then the next chunk's loads
+        const uint32_t nbase = cbase + kStep;
+        uint32_t pg_after[H];
+#pragma unroll
+        for (int hf = 0; hf < H; ++hf) pg_after[hf] = half_page(nbase + kStep, hf);
+        u32x4 kn[H][NL];
+        float ksn[H], vsn[H];
+        if (nbase < t_end) load_chunk(nbase, pg_next, kn, vr, ksn, vsn);
+
+        // ---- scores S^T (token x head)
+        f32x4 sc[H];
+#pragma unroll
+        for (int hf = 0; hf < H; ++hf) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
@@ -210,44 +263,34 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
             sc[hf] = acc;
         }
 
-        // ---- lane (n, g) now holds head n, tokens cbase + 16*hf + 4*g + r
-        float s2[2][4], vsc[2][4];
+        // ---- online softmax (log2 units) for head n; the scales of the tokens
+        // this lane holds (4*g + r) come from the lanes that loaded them.
+        float s2[H][4], vsc[H][4];
         float mx = -INFINITY;
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
+        for (int hf = 0; hf < H; ++hf)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const uint32_t tau = cbase + hf * 16 + 4 * g + r;
-                float f = p.scale_log2;
-                float vs = 1.0f;
-                bool ok = tau < t_end;
+                const uint32_t src = 4u * g + (uint32_t)r;
+                const bool ok = cbase + hf * 16 + src < t_end;
+                float f = p.scale_log2, vs = 1.0f;
                 if constexpr (KVB == 1) {
-                    if (ok) {
-                        const uint32_t page = bt[tau / P];
-                        if (page < a.num_pages) {
-                            const uint64_t si =
-                                ((scale_layer + page) * P + tau % P) * a.kv_heads + kv_head;
-                            f *= p.k_scale[si];
-                            vs = p.v_scale[si];
-                        } else {
-                            ok = false;
-                        }
-                    }
+                    f *= __shfl(ksl[hf], (int)src, 64);
+                    vs = __shfl(vsl[hf], (int)src, 64);
                 }
                 s2[hf][r] = ok ? sc[hf][r] * f : -INFINITY;
                 vsc[hf][r] = vs;
                 mx = __builtin_fmaxf(mx, s2[hf][r]);
             }
-        }
         mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m_new = __builtin_fmaxf(m_run, mx);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float pv[2][4];
+        float pv[H][4];
         float psum = 0.0f;
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+        for (int hf = 0; hf < H; ++hf)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
@@ -256,28 +299,48 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
             }
         l_run = l_run * alpha + psum;
         m_run = m_new;
-        u32x4 pw;
-        pw[0] = pack_bf16x2(pv[0][0], pv[0][1]);
-        pw[1] = pack_bf16x2(pv[0][2], pv[0][3]);
-        pw[2] = pack_bf16x2(pv[1][0], pv[1][1]);
-        pw[3] = pack_bf16x2(pv[1][2], pv[1][3]);
-        const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
+        // O is rescaled only when some head's running max moved.
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+        }
 
         wave_lds_sync();
-        // ---- O^T += V^T * P^T, 16 dims per MFMA
+        // ---- O^T += V^T * P^T
+        if constexpr (KVB == 1) {
+            u32x4 pw;
+            pw[0] = pack_bf16x2(pv[0][0], pv[0][1]);
+            pw[1] = pack_bf16x2(pv[0][2], pv[0][3]);
+            pw[2] = pack_bf16x2(pv[1][0], pv[1][1]);
+            pw[3] = pack_bf16x2(pv[1][2], pv[1][3]);
+            const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-            const uint8_t* src = vt + (db * 16 + n) * PITCH + g * 8 * KVB;
-            bf16x8 vf;
-            if constexpr (KVB == 1) {
-                const u32x2 w = *reinterpret_cast<const u32x2*>(src);
-                vf = fp8x8_to_bf16x8(w[0], w[1]);
-            } else {
-                vf = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(src));
+            for (int db = 0; db < NDB; ++db) {
+                const i32x2 w = lds_read_tr8(vt + tr_off + 16 * db);
+                const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[db], 0, 0, 0);
             }
-            o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[db] * alpha, 0, 0, 0);
+        } else {
+            u32x2 pw;
+            pw[0] = pack_bf16x2(pv[0][0], pv[0][1]);
+            pw[1] = pack_bf16x2(pv[0][2], pv[0][3]);
+            const i16x4 pf = __builtin_bit_cast(i16x4, pw);
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const i16x4 vf = lds_read_tr16(vt + tr_off + 32 * db);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf, o[db], 0, 0, 0);
+            }
         }
         wave_lds_sync();
+
+#pragma unroll
+        for (int hf = 0; hf < H; ++hf) {
+            pg_next[hf] = pg_after[hf];
+            ksl[hf] = ksn[hf];
+            vsl[hf] = vsn[hf];
+#pragma unroll
+            for (int i = 0; i < NL; ++i) kr[hf][i] = kn[hf][i];
+        }
     }
 
     // ---- merge the 4 waves: per wave m[16], l[16], O[qpk][D] in LDS
@@ -418,10 +481,10 @@ bool mfma_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
     return true;
 }
 
-template <int KVB, int D>
-hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+template <int KVB, int D, bool kAl16>
+hipError_t launch_decode_t2(const DecodeParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
-    const size_t v_bytes = (size_t)kWaves * D * lds_pitch<KVB>();
+    const size_t v_bytes = (size_t)kWaves * 16 * chunk_halves<KVB>() * v_row_bytes<KVB, D>();
     const size_t m_bytes = (size_t)kWaves * 32 * sizeof(float) + (size_t)kWaves * qpk * D * sizeof(float);
     const size_t lds_bytes = v_bytes > m_bytes ? v_bytes : m_bytes;
     const uint64_t grid = (uint64_t)p.a.rows * p.a.kv_heads * p.splits;
@@ -429,13 +492,19 @@ hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_decode_kernel<KVB, D>),
+            reinterpret_cast<const void*>(&paged_decode_kernel<KVB, D, kAl16>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((paged_decode_kernel<KVB, D>), dim3((uint32_t)grid), dim3(kThreads),
+    hipLaunchKernelGGL((paged_decode_kernel<KVB, D, kAl16>), dim3((uint32_t)grid), dim3(kThreads),
                        lds_bytes, stream, p);
     return hipGetLastError();
+}
+
+template <int KVB, int D>
+hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+    return (p.a.page_tokens & 15u) == 0u ? launch_decode_t2<KVB, D, true>(p, stream)
+                                         : launch_decode_t2<KVB, D, false>(p, stream);
 }
 
 template <int KVB>

@@ -133,7 +133,8 @@ def test_config4_fp8_split_decode(dev):
     a = run_gpu(lay, 24, q, slots, pos, bt, kp, vp, ks, vs, splits=16)
     b = run_gpu(lay, 24, q, slots, pos, bt, kp, vp, ks, vs, splits=64, pages_per_split=64)
     c = run_gpu(lay, 24, q, slots, pos, bt, kp, vp, ks, vs, splits=1)
-    assert np.max(np.abs(a - c)) < 1e-3 and np.max(np.abs(b - c)) < 1e-3
+    # P is rounded to bf16 before PV, so split layouts differ by ~2^-9 relative
+    assert np.max(np.abs(a - c)) < 1e-2 and np.max(np.abs(b - c)) < 1e-2
     pick = np.sort(np.concatenate([np.argsort(lens)[-4:], rng.choice(64, 12, replace=False)]))
     want = oracle_out(lay, 24, q[pick], slots[pick], pos[pick], bt, kp, vp, ks, vs)
     assert np.max(np.abs(a[pick] - want)) < 5e-2
