@@ -32,21 +32,6 @@ struct AppendParams {
     uint32_t vec_ok;           // 16 B loads / vector stores legal
 };
 
-__device__ __forceinline__ bool resolve_row(const psk_kv_append_args& a, uint32_t row,
-                                            uint64_t& base, uint32_t& page, uint32_t& off) {
-    const uint32_t slot = a.row_sequence_slots[row];
-    if (slot >= a.max_sequences) return false;
-    const uint32_t pos = a.row_positions[row];
-    const uint32_t lb = pos / a.page_tokens;
-    off = pos % a.page_tokens;
-    if (lb >= a.block_table_stride) return false;
-    page = a.block_tables[(uint64_t)slot * a.block_table_stride + lb];
-    if (page >= a.num_pages) return false;
-    base = (uint64_t)a.layer * a.elems_per_layer + (uint64_t)page * a.elems_per_page +
-           (uint64_t)off * a.elems_per_token;
-    return true;
-}
-
 // Loads chunk `c` (elements 8c..8c+7) of a head slice as 8 floats; elements
 // past head_dim read as 0.
 __device__ __forceinline__ void load_chunk(const uint16_t* src, uint32_t c, uint32_t D, bool vec,
@@ -66,80 +51,196 @@ __device__ __forceinline__ void load_chunk(const uint16_t* src, uint32_t c, uint
     }
 }
 
+// Quantizes 8 values of one head slice and packs the E4M3 codes (byte i =
+// element i): x / scale as the reference computes it (IEEE quotient, then the
+// SATFINITE RNE conversion).
+__device__ __forceinline__ u32x2 encode8(const float (&x)[8], float scale, float rcp, bool fast) {
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = div_by_scale(x[i], scale, rcp, fast);
+    u32x2 c;
+    c[0] = e4m3_encode_pair(q[2], q[3], e4m3_encode_pair(q[0], q[1], 0u, false), true);
+    c[1] = e4m3_encode_pair(q[6], q[7], e4m3_encode_pair(q[4], q[5], 0u, false), true);
+    return c;
+}
+
+__device__ __forceinline__ float head_scale(float amax) {
+    return amax == 0.0f ? 1.0f : amax / kFp8Max;
+}
+
+__device__ __forceinline__ bool fast_div_ok(float scale) {
+    return scale >= 0x1p-100f && scale <= 0x1.fffffep+127f;
+}
+
+// Fast path: head_dim % 8 == 0, head_dim <= 8 * L, every access aligned. A
+// wave runs kUnroll groups of 64/L tasks. All input loads of the kUnroll
+// groups are issued first, then the kUnroll slot/position loads, then the
+// kUnroll block-table loads, so the HBM reads overlap the lookup chain
+// (reference skip rules: kv_append.hip:31-55).
+constexpr int kUnroll = 4;
+
 template <bool kFp8>
-__global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
+__global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams p) {
     const psk_kv_append_args& a = p.a;
     const uint32_t L = p.lanes_per_head;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave_global = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const uint32_t tasks_per_wave = 64u >> p.log2_lanes;
-    const uint64_t task = (uint64_t)wave_global * tasks_per_wave + (lane >> p.log2_lanes);
     const uint32_t sub = lane & (L - 1u);
-    const uint64_t total = (uint64_t)a.rows * a.kv_heads;
-    const bool live = task < total;
+    const uint32_t total = a.rows * a.kv_heads;   // launcher checks < 2^32
+    const uint32_t D = a.head_dim;
+    const bool has_chunk = sub < p.chunks;
+    const uint32_t e0 = sub * 8u;
 
-    uint32_t row = 0, head = 0, page = 0, off = 0;
-    uint64_t base = 0;
-    bool valid = false;
-    if (live) {
-        row = (uint32_t)(task / a.kv_heads);
-        head = (uint32_t)(task % a.kv_heads);
-        valid = resolve_row(a, row, base, page, off);
+    uint32_t row[kUnroll], head[kUnroll];
+    bool live[kUnroll];
+    u32x4 kw[kUnroll], vw[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t task = (wave_global * kUnroll + u) * tasks_per_wave + (lane >> p.log2_lanes);
+        live[u] = task < total;
+        const uint32_t t = live[u] ? task : 0u;
+        row[u] = t / a.kv_heads;
+        head[u] = t - row[u] * a.kv_heads;
+        // lanes without a chunk read the slice start (always in bounds) and
+        // drop the value, so the loads need no branch
+        const uint32_t e = has_chunk ? e0 : 0u;
+        const uint16_t* ks = static_cast<const uint16_t*>(a.k_input) +
+                             (uint64_t)row[u] * a.k_row_stride + head[u] * D + e;
+        const uint16_t* vs = static_cast<const uint16_t*>(a.v_input) +
+                             (uint64_t)row[u] * a.v_row_stride + head[u] * D + e;
+        kw[u] = *reinterpret_cast<const u32x4*>(ks);
+        vw[u] = *reinterpret_cast<const u32x4*>(vs);
     }
+    uint32_t slot[kUnroll], pos[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        slot[u] = a.row_sequence_slots[row[u]];
+        pos[u] = a.row_positions[row[u]];
+    }
+    uint32_t page[kUnroll], off[kUnroll];
+    bool valid[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const uint32_t lb = pos[u] / a.page_tokens;
+        off[u] = pos[u] - lb * a.page_tokens;
+        const bool ok = live[u] && slot[u] < a.max_sequences && lb < a.block_table_stride;
+        page[u] = a.block_tables[ok ? (uint64_t)slot[u] * a.block_table_stride + lb : 0u];
+        valid[u] = ok;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        if (!has_chunk) kw[u] = vw[u] = (u32x4){0u, 0u, 0u, 0u};
+        valid[u] = valid[u] && page[u] < a.num_pages;
+        const uint64_t dst = (uint64_t)a.layer * a.elems_per_layer +
+                             (uint64_t)page[u] * a.elems_per_page +
+                             (uint64_t)off[u] * a.elems_per_token + head[u] * D + e0;
+        if constexpr (!kFp8) {
+            if (valid[u] && has_chunk) {
+                *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.k_pool) + dst) = kw[u];
+                *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.v_pool) + dst) = vw[u];
+            }
+        } else {
+            float kx[8], vx[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                kx[2 * i] = __uint_as_float(kw[u][i] << 16);
+                kx[2 * i + 1] = __uint_as_float(kw[u][i] & 0xFFFF0000u);
+                vx[2 * i] = __uint_as_float(vw[u][i] << 16);
+                vx[2 * i + 1] = __uint_as_float(vw[u][i] & 0xFFFF0000u);
+            }
+            // per-head absmax over the L lanes; fmaxf ignores NaN as the
+            // reference's fmaxf(k_max, fabsf(kf)) does
+            float km = 0.0f, vm = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                km = __builtin_fmaxf(km, __builtin_fabsf(kx[i]));
+                vm = __builtin_fmaxf(vm, __builtin_fabsf(vx[i]));
+            }
+            for (uint32_t o = L >> 1; o >= 1u; o >>= 1) {
+                km = __builtin_fmaxf(km, __shfl_xor(km, (int)o, 64));
+                vm = __builtin_fmaxf(vm, __shfl_xor(vm, (int)o, 64));
+            }
+            if (!valid[u]) continue;
+            const float k_scale = head_scale(km), v_scale = head_scale(vm);
+            if (sub == 0u) {
+                const uint64_t si =
+                    (((uint64_t)a.layer * a.num_pages + page[u]) * a.page_tokens + off[u]) *
+                        a.kv_heads + head[u];
+                p.k_scale[si] = k_scale;
+                p.v_scale[si] = v_scale;
+            }
+            if (has_chunk) {
+                const u32x2 kc = encode8(kx, k_scale, 1.0f / k_scale, fast_div_ok(k_scale));
+                const u32x2 vc = encode8(vx, v_scale, 1.0f / v_scale, fast_div_ok(v_scale));
+                *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(p.k_pool) + dst) = kc;
+                *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(p.v_pool) + dst) = vc;
+            }
+        }
+    }
+}
+
+// General shapes (any head_dim, unaligned slices): one task group per wave,
+// lanes loop over 8-element chunks, element-wise accesses at the edges.
+template <bool kFp8>
+__global__ __launch_bounds__(256) void kv_append_generic_kernel(const AppendParams p) {
+    const psk_kv_append_args& a = p.a;
+    const uint32_t L = p.lanes_per_head;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint64_t wave_global = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint64_t task = wave_global * (64u >> p.log2_lanes) + (lane >> p.log2_lanes);
+    const uint32_t sub = lane & (L - 1u);
+    const bool live = task < (uint64_t)a.rows * a.kv_heads;
+    const uint32_t row = live ? (uint32_t)(task / a.kv_heads) : 0u;
+    const uint32_t head = live ? (uint32_t)(task % a.kv_heads) : 0u;
     const uint32_t D = a.head_dim;
     const bool vec = p.vec_ok != 0u;
+    bool valid = false;
+    uint32_t page = 0, off = 0;
+    if (live) {
+        const uint32_t slot = a.row_sequence_slots[row];
+        const uint32_t pos = a.row_positions[row];
+        const uint32_t lb = pos / a.page_tokens;
+        off = pos % a.page_tokens;
+        if (slot < a.max_sequences && lb < a.block_table_stride) {
+            page = a.block_tables[(uint64_t)slot * a.block_table_stride + lb];
+            valid = page < a.num_pages;
+        }
+    }
     const uint16_t* ks = static_cast<const uint16_t*>(a.k_input) + (uint64_t)row * a.k_row_stride +
                          (uint64_t)head * D;
     const uint16_t* vs = static_cast<const uint16_t*>(a.v_input) + (uint64_t)row * a.v_row_stride +
                          (uint64_t)head * D;
-    const uint64_t dst = base + (uint64_t)head * D;
-
+    const uint64_t dst = (uint64_t)a.layer * a.elems_per_layer + (uint64_t)page * a.elems_per_page +
+                         (uint64_t)off * a.elems_per_token + (uint64_t)head * D;
     if constexpr (!kFp8) {
         if (!valid) return;
         uint16_t* kd = static_cast<uint16_t*>(p.k_pool) + dst;
         uint16_t* vd = static_cast<uint16_t*>(p.v_pool) + dst;
-        for (uint32_t c = sub; c < p.chunks; c += L) {
-            const uint32_t e0 = c * 8u;
-            if (vec) {
-                const u32x4 kw = *reinterpret_cast<const u32x4*>(ks + e0);
-                const u32x4 vw = *reinterpret_cast<const u32x4*>(vs + e0);
-                *reinterpret_cast<u32x4*>(kd + e0) = kw;
-                *reinterpret_cast<u32x4*>(vd + e0) = vw;
-            } else {
-                for (uint32_t i = 0; i < 8u && e0 + i < D; ++i) {
-                    kd[e0 + i] = ks[e0 + i];
-                    vd[e0 + i] = vs[e0 + i];
-                }
+        for (uint32_t c = sub; c < p.chunks; c += L)
+            for (uint32_t i = c * 8u; i < c * 8u + 8u && i < D; ++i) {
+                kd[i] = ks[i];
+                vd[i] = vs[i];
             }
-        }
     } else {
-        // Pass 1: per-head absmax over the L lanes of the task. fmaxf ignores
-        // NaN, as the reference's fmaxf(k_max, fabsf(kf)) does.
-        float kx[8], vx[8];
         float km = 0.0f, vm = 0.0f;
+        float kx[8], vx[8];
         if (valid) {
             for (uint32_t c = sub; c < p.chunks; c += L) {
                 load_chunk(ks, c, D, vec, kx);
                 load_chunk(vs, c, D, vec, vx);
-#pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     km = __builtin_fmaxf(km, __builtin_fabsf(kx[i]));
                     vm = __builtin_fmaxf(vm, __builtin_fabsf(vx[i]));
                 }
             }
         }
-        // Reduce within the L-lane group (groups are aligned lane ranges).
         for (uint32_t o = L >> 1; o >= 1u; o >>= 1) {
             km = __builtin_fmaxf(km, __shfl_xor(km, (int)o, 64));
             vm = __builtin_fmaxf(vm, __shfl_xor(vm, (int)o, 64));
         }
         if (!valid) return;
-        const float k_scale = km == 0.0f ? 1.0f : km / kFp8Max;
-        const float v_scale = vm == 0.0f ? 1.0f : vm / kFp8Max;
-        const float k_rcp = 1.0f / k_scale;
-        const float v_rcp = 1.0f / v_scale;
-        const bool k_fast = k_scale >= 0x1p-100f && k_scale <= 0x1.fffffep+127f;
-        const bool v_fast = v_scale >= 0x1p-100f && v_scale <= 0x1.fffffep+127f;
+        const float k_scale = head_scale(km), v_scale = head_scale(vm);
         if (sub == 0u) {
             const uint64_t si =
                 (((uint64_t)a.layer * a.num_pages + page) * a.page_tokens + off) * a.kv_heads + head;
@@ -148,34 +249,14 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
         }
         uint8_t* kd = static_cast<uint8_t*>(p.k_pool) + dst;
         uint8_t* vd = static_cast<uint8_t*>(p.v_pool) + dst;
-        // Pass 2: quantize. With one chunk per lane the values are still in
-        // registers; otherwise they are reloaded (cache hits).
-        const bool single = p.chunks <= L;
         for (uint32_t c = sub; c < p.chunks; c += L) {
-            if (!single) {
-                load_chunk(ks, c, D, vec, kx);
-                load_chunk(vs, c, D, vec, vx);
-            }
-            float kq[8], vq[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                kq[i] = div_by_scale(kx[i], k_scale, k_rcp, k_fast);
-                vq[i] = div_by_scale(vx[i], v_scale, v_rcp, v_fast);
-            }
-            u32x2 kc, vc;
-            kc[0] = e4m3_encode_pair(kq[2], kq[3], e4m3_encode_pair(kq[0], kq[1], 0u, false), true);
-            kc[1] = e4m3_encode_pair(kq[6], kq[7], e4m3_encode_pair(kq[4], kq[5], 0u, false), true);
-            vc[0] = e4m3_encode_pair(vq[2], vq[3], e4m3_encode_pair(vq[0], vq[1], 0u, false), true);
-            vc[1] = e4m3_encode_pair(vq[6], vq[7], e4m3_encode_pair(vq[4], vq[5], 0u, false), true);
-            const uint32_t e0 = c * 8u;
-            if (vec) {
-                *reinterpret_cast<u32x2*>(kd + e0) = kc;
-                *reinterpret_cast<u32x2*>(vd + e0) = vc;
-            } else {
-                for (uint32_t i = 0; i < 8u && e0 + i < D; ++i) {
-                    kd[e0 + i] = (uint8_t)(kc[i >> 2] >> (8u * (i & 3u)));
-                    vd[e0 + i] = (uint8_t)(vc[i >> 2] >> (8u * (i & 3u)));
-                }
+            load_chunk(ks, c, D, vec, kx);
+            load_chunk(vs, c, D, vec, vx);
+            const u32x2 kc = encode8(kx, k_scale, 1.0f / k_scale, fast_div_ok(k_scale));
+            const u32x2 vc = encode8(vx, v_scale, 1.0f / v_scale, fast_div_ok(v_scale));
+            for (uint32_t i = 0; i < 8u && c * 8u + i < D; ++i) {
+                kd[c * 8u + i] = (uint8_t)(kc[i >> 2] >> (8u * (i & 3u)));
+                vd[c * 8u + i] = (uint8_t)(vc[i >> 2] >> (8u * (i & 3u)));
             }
         }
     }
@@ -229,10 +310,16 @@ template <bool kFp8>
 hipError_t launch(const AppendParams& p, hipStream_t stream) {
     const uint64_t tasks = (uint64_t)p.a.rows * p.a.kv_heads;
     const uint64_t tasks_per_wave = 64u >> p.log2_lanes;
-    const uint64_t waves = (tasks + tasks_per_wave - 1) / tasks_per_wave;
+    const uint64_t groups = (tasks + tasks_per_wave - 1) / tasks_per_wave;
+    const bool fast = p.vec_ok != 0u && p.chunks <= p.lanes_per_head && tasks < 0xFFFFFFFFull;
+    const uint64_t waves = fast ? (groups + kUnroll - 1) / kUnroll : groups;
     const uint64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(kv_append_kernel<kFp8>, dim3((uint32_t)blocks), dim3(256), 0, stream, p);
+    if (fast)
+        hipLaunchKernelGGL(kv_append_fast_kernel<kFp8>, dim3((uint32_t)blocks), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(kv_append_generic_kernel<kFp8>, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                           p);
     return hipGetLastError();
 }
 

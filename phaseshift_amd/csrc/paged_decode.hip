@@ -404,11 +404,17 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
     }
 }
 
-// Combine of the split partials: WG = (row, kv_head), thread = dim.
+// Combine of the split partials: WG = (row, kv_head, query head of the
+// group), thread = dim. Split weights W_s = e^(m_s - g) are computed once into
+// LDS; every thread then sums W_s * A_s[d] with loads coalesced over d.
 __global__ __launch_bounds__(kThreads) void split_reduce_kernel(const DecodeParams p) {
+    __shared__ float w_lds[kMaxSplits];
+    __shared__ float red[2 * kWaves];
     const psk_paged_attention_args& a = p.a;
-    const uint32_t kv_head = blockIdx.x % a.kv_heads;
-    const uint32_t row = blockIdx.x / a.kv_heads;
+    const uint32_t qpk = a.q_heads / a.kv_heads;
+    const uint32_t h = blockIdx.x % qpk;
+    const uint32_t kv_head = (blockIdx.x / qpk) % a.kv_heads;
+    const uint32_t row = blockIdx.x / (qpk * a.kv_heads);
     if (row >= a.rows) return;
     const uint32_t slot = a.row_sequence_slots[row];
     if (slot >= a.max_sequences) return;
@@ -417,35 +423,50 @@ __global__ __launch_bounds__(kThreads) void split_reduce_kernel(const DecodePara
     const uint32_t pc = ((uint32_t)vis64 + a.page_tokens - 1u) / a.page_tokens;
     const uint32_t per = split_pages(pc, p.splits, p.pages_per_split);
     const uint32_t n_used = min(p.splits, (pc + per - 1u) / per);
-    const uint32_t qpk = a.q_heads / a.kv_heads;
     const uint64_t stride = (uint64_t)qpk * (2u + kPagedAttentionHeadLimit);
     const float* base = p.partials + (uint64_t)(row * a.kv_heads + kv_head) * p.splits * stride;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+
+    // g = max m_s (NaN marks a split that met an invalid page)
+    float gm = -INFINITY;
+    bool bad = false;
+    for (uint32_t s = tid; s < n_used; s += kThreads) {
+        const float m = base[s * stride + h];
+        bad |= __builtin_isnan(m);
+        gm = __builtin_fmaxf(gm, m);
+    }
+    gm = wave_max(gm);
+    const bool bad_w = __any(bad);
+    if (lane == 0) {
+        red[wave] = gm;
+        red[kWaves + wave] = bad_w ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+    gm = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    if (red[kWaves] + red[kWaves + 1] + red[kWaves + 2] + red[kWaves + 3] != 0.0f) return;
+    __syncthreads();
+    float lsum = 0.0f;
+    for (uint32_t s = tid; s < n_used; s += kThreads) {
+        const float w = __expf(base[s * stride + h] - gm);
+        w_lds[s] = w;
+        lsum += w * base[s * stride + qpk + h];
+    }
+    lsum = wave_sum(lsum);
+    if (lane == 0) red[wave] = lsum;
+    __syncthreads();
+    const float L = red[0] + red[1] + red[2] + red[3];
     const uint32_t D = a.head_dim;
-    for (uint32_t h = 0; h < qpk; ++h) {
-        float gm = -INFINITY;
-        bool bad = false;
-        for (uint32_t s = 0; s < n_used; ++s) {
-            const float m = base[s * stride + h];
-            bad |= __builtin_isnan(m);
-            gm = __builtin_fmaxf(gm, m);
-        }
-        if (bad) return;
-        float L = 0.0f;
-        for (uint32_t s = 0; s < n_used; ++s)
-            L += __expf(base[s * stride + h] - gm) * base[s * stride + qpk + h];
-        for (uint32_t d = threadIdx.x; d < D; d += kThreads) {
-            float O = 0.0f;
-            for (uint32_t s = 0; s < n_used; ++s)
-                O += __expf(base[s * stride + h] - gm) *
-                     base[s * stride + 2u * qpk + h * kPagedAttentionHeadLimit + d];
-            const uint64_t oi =
-                (uint64_t)row * a.output_row_stride + (uint64_t)(kv_head * qpk + h) * D + d;
-            const float res = O / L;
-            if (a.output_dtype == PSK_OUT_F32)
-                static_cast<float*>(a.output)[oi] = res;
-            else
-                static_cast<uint16_t*>(a.output)[oi] = f32_to_bf16_bits(res);
-        }
+    const float* A = base + 2u * qpk + h * kPagedAttentionHeadLimit;
+    for (uint32_t d = tid; d < D; d += kThreads) {
+        float O = 0.0f;
+        for (uint32_t s = 0; s < n_used; ++s) O += w_lds[s] * A[s * stride + d];
+        const uint64_t oi =
+            (uint64_t)row * a.output_row_stride + (uint64_t)(kv_head * qpk + h) * D + d;
+        const float res = O / L;
+        if (a.output_dtype == PSK_OUT_F32)
+            static_cast<float*>(a.output)[oi] = res;
+        else
+            static_cast<uint16_t*>(a.output)[oi] = f32_to_bf16_bits(res);
     }
 }
 
@@ -521,7 +542,7 @@ hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
 }
 
 hipError_t launch_reduce(const DecodeParams& p, hipStream_t stream) {
-    const uint64_t grid = (uint64_t)p.a.rows * p.a.kv_heads;
+    const uint64_t grid = (uint64_t)p.a.rows * p.a.q_heads;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
     hipLaunchKernelGGL(split_reduce_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, stream, p);
     return hipGetLastError();
