@@ -151,20 +151,19 @@ def run_decode(torch, ops, st, steps, warmup, dev, splits=None, pps=None):
             split_launch()
             reduce_launch()
     step_ms = t.ms() / steps
-    # per-kernel durations: events bracketing each launch on the same stream
-    sk, rk = [], []
-    for _ in range(steps):
-        t1 = Timer(torch)
-        with t1:
+    # per-kernel durations: HIP events on the launch stream around `steps`
+    # back-to-back launches of that kernel alone (amortizes the event gaps)
+    t1 = Timer(torch)
+    with t1:
+        for _ in range(steps):
             split_launch()
-        t2 = Timer(torch)
-        with t2:
+    t2 = Timer(torch)
+    with t2:
+        for _ in range(steps):
             reduce_launch()
-        sk.append(t1.ms())
-        rk.append(t2.ms())
     per_tok = BYTES_PER_TOKEN_FP8 if st["fp8"] else BYTES_PER_TOKEN_BF16
     nbytes_alg = float(lens.sum()) * per_tok + rows * st["QH"] * 256 * 2
-    return step_ms, float(np.mean(sk)), float(np.mean(rk)), nbytes_alg, splits, pps
+    return step_ms, t1.ms() / steps, t2.ms() / steps, nbytes_alg, splits, pps
 
 
 def run_append(torch, ops, rows, steps, warmup, dev, seed=7):
@@ -192,13 +191,11 @@ def run_append(torch, ops, rows, steps, warmup, dev, seed=7):
     for _ in range(warmup):
         launch()
     torch.cuda.synchronize()
-    times = []
-    for _ in range(steps):
-        t = Timer(torch)
-        with t:
+    t = Timer(torch)
+    with t:
+        for _ in range(steps):
             launch()
-        times.append(t.ms())
-    ms = float(np.mean(times))
+    ms = t.ms() / steps
     return ms, rows * APPEND_BYTES_PER_ROW_FP8
 
 

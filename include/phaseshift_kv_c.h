@@ -216,6 +216,15 @@ int psk_attention_paged_prefill_fp8_e4m3(const psk_paged_attention_args* a,
                                          const float* k_scale_pool,
                                          const float* v_scale_pool, void* stream);
 
+/* Additive: split-K over the same tiles; the combine is
+ * psk_attention_paged_split_reduce_ex with the same splits / pages_per_split
+ * (pages_per_split > 0 is required: the rows of a tile differ in length). */
+int psk_attention_paged_tile_split(const psk_paged_attention_args* a, uint32_t kv_dtype,
+                                   const void* k_pool, const void* v_pool,
+                                   const float* k_scale_pool, const float* v_scale_pool,
+                                   float* partials, uint32_t splits, uint32_t pages_per_split,
+                                   void* stream);
+
 /* ---- Page-level operations ------------------------------------------------- */
 /* elem_bytes: 2 (bf16 pool), 1 (fp8 codes) or 4 (fp32 scale pool, with
  * elems_per_token = kv_heads, elems_per_page = page_tokens*kv_heads). */
@@ -232,6 +241,104 @@ int psk_fill_u32(uint32_t* dst, uint32_t value, uint64_t count, void* stream);
 int psk_prepare_row_metadata(const psk_request_descriptor* requests, uint32_t num_requests,
                              uint32_t actual_rows, uint32_t* row_sequence_slots,
                              uint32_t* row_positions, void* stream);
+
+/* ---- Host KV state (opaque handles) ----------------------------------------
+ * Status codes of these entry points: 0 ok, else one of PSK_ERR_* (message in
+ * psk_last_error_message()). Reference: state/paged_kv_pool.cpp,
+ * state/sequence_slot_pool.cpp, state/paged_sequence_state.cpp. */
+#define PSK_ERR_INVALID_ARGUMENT 1001
+#define PSK_ERR_OUT_OF_RANGE 1002
+#define PSK_ERR_INVALID_STATE 1003
+#define PSK_ERR_INSUFFICIENT_MEMORY 1004
+#define PSK_ERR_HIP 1005
+
+typedef struct psk_kv_pool psk_kv_pool;
+typedef struct psk_slot_pool psk_slot_pool;
+typedef struct psk_sequence psk_sequence;
+
+typedef struct psk_pool_info_t {
+    void* k_pool;
+    void* v_pool;
+    float* k_scale_pool;
+    float* v_scale_pool;
+    uint32_t num_pages;
+    uint32_t page_tokens;
+    uint32_t num_layers;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t kv_dtype;
+    uint32_t free_pages;
+    uint32_t used_pages;
+    uint64_t reserved_bytes;
+} psk_pool_info_t;
+
+typedef struct psk_sequence_info_t {
+    uint32_t slot;
+    uint32_t generation;
+    uint32_t position;
+    uint32_t max_seq_len;
+    uint32_t num_blocks;
+    uint32_t poisoned;
+} psk_sequence_info_t;
+
+const char* psk_last_error_message(void);
+/* PagedKVPool::create (paged_kv_pool.cpp:27-194); kv_dtype PSK_KV_*. */
+int psk_pool_create(psk_kv_pool** out, uint32_t num_pages, uint32_t page_tokens,
+                    uint32_t num_layers, uint32_t kv_heads, uint32_t head_dim, uint32_t kv_dtype);
+void psk_pool_destroy(psk_kv_pool* pool);
+int psk_pool_info(const psk_kv_pool* pool, psk_pool_info_t* out);
+int psk_pool_allocate(psk_kv_pool* pool, uint32_t* page);
+int psk_pool_release(psk_kv_pool* pool, uint32_t page);
+/* copy_page_from for n (dst, src) pairs, host arrays (paged_kv_pool.cpp:338-542). */
+int psk_pool_copy_pages(psk_kv_pool* dst, const psk_kv_pool* src, const uint32_t* dst_pages,
+                        const uint32_t* src_pages, uint32_t n, void* stream);
+/* SequenceSlotPool (sequence_slot_pool.cpp): device tables [max_sequences][max_blocks]. */
+int psk_slot_pool_create(psk_slot_pool** out, uint32_t max_sequences, uint32_t max_blocks,
+                         void* stream);
+void psk_slot_pool_destroy(psk_slot_pool* slots);
+uint32_t* psk_slot_pool_block_tables(const psk_slot_pool* slots);
+/* PagedSequenceState and its reserve / rollback / commit
+ * (paged_sequence_state.cpp:111-271). */
+int psk_sequence_create(psk_sequence** out, psk_slot_pool* slots, psk_kv_pool* pool,
+                        uint32_t max_seq_len, void* stream);
+int psk_sequence_release(psk_sequence* seq, void* stream);
+int psk_sequence_reserve(psk_sequence* seq, uint32_t token_count, void* stream);
+int psk_sequence_rollback(psk_sequence* seq, uint32_t old_block_count, void* stream);
+int psk_sequence_commit(psk_sequence* seq, uint32_t tokens);
+int psk_sequence_info(const psk_sequence* seq, psk_sequence_info_t* out);
+uint32_t psk_sequence_block_table(const psk_sequence* seq, uint32_t* out, uint32_t cap);
+
+/* ---- Step planner (paged_attention_dispatch.hip:437-894) -------------------
+ * Plans and launches the PAGED_ATTENTION binding of one mixed step: decode
+ * region (rows before the first PREFILL request) with split-K when
+ * max_visible_tokens >= 2048 and partials fit, PREFILL requests of >= 128 rows
+ * on the tile launcher. stream == (void*)~0 plans without launching. */
+#define PSK_MAX_PLANNED 16
+typedef struct psk_step_request {
+    uint32_t row_begin;
+    uint32_t row_count;
+    uint8_t execution_class;           /* 0 DECODE 1 SPEC_VERIFY 2 PREFILL 3 SPEC_DRAFT */
+    uint8_t reserved[3];
+} psk_step_request;
+
+typedef struct psk_planned_kernel {
+    uint32_t kind;                     /* 0 decode (split when splits > 1), 1 tile */
+    uint32_t row_begin;
+    uint32_t rows;
+    uint32_t splits;
+    uint32_t pages_per_split;
+} psk_planned_kernel;
+
+typedef struct psk_step_plan_t {
+    uint32_t count;
+    psk_planned_kernel kernels[PSK_MAX_PLANNED];
+} psk_step_plan_t;
+
+int psk_paged_attention_step(const psk_paged_attention_args* common, uint32_t kv_dtype,
+                             const void* k_pool, const void* v_pool, const float* k_scale_pool,
+                             const float* v_scale_pool, const psk_step_request* requests,
+                             uint32_t num_requests, uint32_t max_visible_tokens, float* partials,
+                             uint64_t partial_bytes, psk_step_plan_t* plan_out, void* stream);
 
 /* ---- Self-test hooks (diagnostics, no reference counterpart) --------------- */
 /* Runs the device E4M3 encoder of the append kernel on the floats whose bit

@@ -61,6 +61,37 @@ class PageCopyArgs(C.Structure):
             "kv_heads", "head_dim", "kv_dtype")]
 
 
+class PoolInfo(C.Structure):
+    _fields_ = [("k_pool", C.c_void_p), ("v_pool", C.c_void_p), ("k_scale_pool", C.c_void_p),
+                ("v_scale_pool", C.c_void_p)] + [
+        (n, C.c_uint32) for n in ("num_pages", "page_tokens", "num_layers", "kv_heads", "head_dim",
+                                  "kv_dtype", "free_pages", "used_pages")] + [
+        ("reserved_bytes", C.c_uint64)]
+
+
+class SequenceInfo(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("slot", "generation", "position", "max_seq_len",
+                                          "num_blocks", "poisoned")]
+
+
+class StepRequest(C.Structure):
+    _fields_ = [("row_begin", C.c_uint32), ("row_count", C.c_uint32),
+                ("execution_class", C.c_uint8), ("reserved", C.c_uint8 * 3)]
+
+
+class PlannedKernel(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("kind", "row_begin", "rows", "splits", "pages_per_split")]
+
+
+class StepPlan(C.Structure):
+    _fields_ = [("count", C.c_uint32), ("kernels", PlannedKernel * 16)]
+
+
+PSK_ERR = {1001: "invalid_argument", 1002: "out_of_range", 1003: "invalid_state",
+           1004: "insufficient_memory", 1005: "hip_error"}
+PLAN_ONLY = C.c_void_p(~0 & 0xFFFFFFFFFFFFFFFF)
+
+
 class RequestDescriptor(C.Structure):
     """psk_request_descriptor == ps::runtime::DeviceRequestDescriptor (64 B)."""
     _fields_ = [("slot", C.c_uint32), ("generation", C.c_uint32), ("row_begin", C.c_uint32),
@@ -92,10 +123,29 @@ SIGNATURES = {
     "psk_attention_split_partials_bytes": [_U32, _U32, _U32, _U32],
     "psk_attention_paged_prefill_bf16": [_P, _P, _P, _P],
     "psk_attention_paged_prefill_fp8_e4m3": [_P, _P, _P, _P, _P, _P],
+    "psk_attention_paged_tile_split": [_P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _P],
     "psk_kv_gather": [_P, _P, _P, _U32, _P],
     "psk_kv_copy_pages": [_P, _P],
     "psk_fill_u32": [_P, _U32, C.c_uint64, _P],
     "psk_prepare_row_metadata": [_P, _U32, _U32, _P, _P, _P],
+    "psk_last_error_message": [],
+    "psk_pool_create": [_P, _U32, _U32, _U32, _U32, _U32, _U32],
+    "psk_pool_destroy": [_P],
+    "psk_pool_info": [_P, _P],
+    "psk_pool_allocate": [_P, _P],
+    "psk_pool_release": [_P, _U32],
+    "psk_pool_copy_pages": [_P, _P, _P, _P, _U32, _P],
+    "psk_slot_pool_create": [_P, _U32, _U32, _P],
+    "psk_slot_pool_destroy": [_P],
+    "psk_slot_pool_block_tables": [_P],
+    "psk_sequence_create": [_P, _P, _P, _U32, _P],
+    "psk_sequence_release": [_P, _P],
+    "psk_sequence_reserve": [_P, _U32, _P],
+    "psk_sequence_rollback": [_P, _U32, _P],
+    "psk_sequence_commit": [_P, _U32],
+    "psk_sequence_info": [_P, _P],
+    "psk_sequence_block_table": [_P, _P, _U32],
+    "psk_paged_attention_step": [_P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _P, C.c_uint64, _P, _P],
     "psk_selftest_e4m3_encode_range": [_U32, _U32, _P, _P],
     "psk_selftest_e4m3_decode_all": [_P, _P],
     "psk_version": [],
@@ -103,6 +153,11 @@ SIGNATURES = {
     "psk_error_string": [C.c_int],
 }
 _RESTYPE = {
+    "psk_last_error_message": C.c_char_p,
+    "psk_pool_destroy": None,
+    "psk_slot_pool_destroy": None,
+    "psk_slot_pool_block_tables": C.c_void_p,
+    "psk_sequence_block_table": C.c_uint32,
     "psk_attention_split_partials_bytes": C.c_uint64,
     "psk_version": C.c_char_p,
     "psk_build_arch": C.c_char_p,
@@ -112,7 +167,24 @@ _RESTYPE = {
 _lib = None
 
 
-def lib() -> C.CDLL:
+class _Lib:
+    """The C-ABI with a ctypes prototype on every entry point. Only functions
+    listed in SIGNATURES are reachable: a call without a prototype would pass
+    64-bit device pointers as 32-bit ints."""
+
+    def __init__(self, cdll: C.CDLL):
+        self._cdll = cdll
+        for name, argt in SIGNATURES.items():
+            f = getattr(cdll, name)
+            f.argtypes = argt
+            f.restype = _RESTYPE.get(name, C.c_int)
+            setattr(self, name, f)
+
+    def __getattr__(self, name):
+        raise AttributeError(f"{name} has no ctypes prototype in phaseshift_amd.SIGNATURES")
+
+
+def lib() -> _Lib:
     """The loaded HIP library. Raises if it has not been built."""
     global _lib
     if _lib is None:
@@ -120,12 +192,7 @@ def lib() -> C.CDLL:
             raise ImportError(
                 f"{LIB_PATH} is missing: build it with `python -m phaseshift_amd.build` "
                 "(no CPU fallback exists)")
-        L = C.CDLL(LIB_PATH)
-        for name, argt in SIGNATURES.items():
-            f = getattr(L, name)
-            f.argtypes = argt
-            f.restype = _RESTYPE.get(name, C.c_int)
-        _lib = L
+        _lib = _Lib(C.CDLL(LIB_PATH))
     return _lib
 
 
@@ -139,3 +206,18 @@ class HipError(RuntimeError):
 def check(fn: str, code: int) -> None:
     if code != HIP_SUCCESS:
         raise HipError(fn, code)
+
+
+class StateError(RuntimeError):
+    """A PSK_ERR_* status of the host-state entry points (reference Status codes)."""
+
+    def __init__(self, fn: str, code: int):
+        msg = lib().psk_last_error_message().decode()
+        super().__init__(f"{fn}: {PSK_ERR.get(code, code)}: {msg}")
+        self.code = code
+        self.kind = PSK_ERR.get(code, "hip_error")
+
+
+def check_state(fn: str, code: int) -> None:
+    if code != 0:
+        raise StateError(fn, code)

@@ -3,24 +3,6 @@
 #include <phaseshift_kv_c.h>
 #include <hip/hip_runtime.h>
 
-// Tile launchers (speculative-verify blocks, chunked prefill). Every row of a
-// tile attends to its own positions [0, pos], which is the reference's causal
-// rule inside a tile (paged_prefill.hip:342-352); each row is computed by the
-// decode kernel, so the tile contract (one sequence per 32 rows,
-// paged_prefill.hip:152-164) is accepted but not required.
-extern "C" int psk_attention_paged_prefill_bf16(const psk_paged_attention_args* a,
-                                                const void* k_pool, const void* v_pool,
-                                                void* stream) {
-    return psk_attention_paged_bf16(a, k_pool, v_pool, stream);
-}
-
-extern "C" int psk_attention_paged_prefill_fp8_e4m3(const psk_paged_attention_args* a,
-                                                    const void* k_pool, const void* v_pool,
-                                                    const float* k_scale_pool,
-                                                    const float* v_scale_pool, void* stream) {
-    return psk_attention_paged_fp8_e4m3(a, k_pool, v_pool, k_scale_pool, v_scale_pool, stream);
-}
-
 extern "C" const char* psk_version(void) { return "phaseshift-kv-mi355x 0.1.0"; }
 
 extern "C" const char* psk_build_arch(void) { return "gfx950"; }

@@ -1,0 +1,217 @@
+// C-ABI over the host KV state and the step planner (opaque handles).
+#include <phaseshift_kv/dispatch.h>
+#include <phaseshift_kv/kv_state.h>
+#include <phaseshift_kv_c.h>
+
+#include <cstring>
+#include <new>
+#include <string>
+
+using namespace ps;
+using namespace ps::qwen35;
+
+struct psk_kv_pool {
+    PagedKVPool pool;
+};
+struct psk_slot_pool {
+    SequenceSlotPool slots;
+};
+struct psk_sequence {
+    PagedSequenceState seq;
+};
+
+namespace {
+thread_local std::string g_last_error;
+
+int to_code(const Status& st) {
+    if (st.ok()) return 0;
+    g_last_error = st.message;
+    switch (st.code) {
+        case Status::Code::InvalidArgument: return PSK_ERR_INVALID_ARGUMENT;
+        case Status::Code::OutOfRange: return PSK_ERR_OUT_OF_RANGE;
+        case Status::Code::InvalidState: return PSK_ERR_INVALID_STATE;
+        case Status::Code::InsufficientMemory: return PSK_ERR_INSUFFICIENT_MEMORY;
+        default: return PSK_ERR_HIP;
+    }
+}
+hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+}  // namespace
+
+extern "C" const char* psk_last_error_message(void) { return g_last_error.c_str(); }
+
+extern "C" int psk_pool_create(psk_kv_pool** out, uint32_t num_pages, uint32_t page_tokens,
+                               uint32_t num_layers, uint32_t kv_heads, uint32_t head_dim,
+                               uint32_t kv_dtype) {
+    if (out == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    auto* h = new (std::nothrow) psk_kv_pool();
+    if (h == nullptr) return PSK_ERR_INSUFFICIENT_MEMORY;
+    const Status st = PagedKVPool::create(
+        h->pool, num_pages, page_tokens, num_layers, kv_heads, head_dim,
+        kv_dtype == PSK_KV_FP8_E4M3 ? KVCacheDType::FP8_E4M3
+                                    : (kv_dtype == PSK_KV_BF16 ? KVCacheDType::BF16
+                                                               : KVCacheDType::PSQ4_W32));
+    if (!st.ok()) {
+        delete h;
+        return to_code(st);
+    }
+    *out = h;
+    return 0;
+}
+
+extern "C" void psk_pool_destroy(psk_kv_pool* p) { delete p; }
+
+extern "C" int psk_pool_info(const psk_kv_pool* p, psk_pool_info_t* out) {
+    if (p == nullptr || out == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    const auto& q = p->pool;
+    out->k_pool = q.k_pool();
+    out->v_pool = q.v_pool();
+    out->k_scale_pool = q.k_scale_pool();
+    out->v_scale_pool = q.v_scale_pool();
+    out->num_pages = q.num_pages();
+    out->page_tokens = q.page_tokens();
+    out->num_layers = q.num_attention_layers();
+    out->kv_heads = q.kv_heads();
+    out->head_dim = q.head_dim();
+    out->kv_dtype = q.dtype() == KVCacheDType::FP8_E4M3 ? PSK_KV_FP8_E4M3 : PSK_KV_BF16;
+    out->free_pages = q.num_free_pages();
+    out->used_pages = q.used_count();
+    out->reserved_bytes = q.reserved_bytes();
+    return 0;
+}
+
+extern "C" int psk_pool_allocate(psk_kv_pool* p, uint32_t* page) {
+    if (p == nullptr || page == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(p->pool.allocate(*page));
+}
+
+extern "C" int psk_pool_release(psk_kv_pool* p, uint32_t page) {
+    if (p == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(p->pool.release(page));
+}
+
+extern "C" int psk_pool_copy_pages(psk_kv_pool* dst, const psk_kv_pool* src, const uint32_t* dst_pages,
+                                   const uint32_t* src_pages, uint32_t n, void* stream) {
+    if (dst == nullptr || src == nullptr || (n > 0 && (dst_pages == nullptr || src_pages == nullptr)))
+        return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(dst->pool.copy_pages_from(std::vector<PageId>(dst_pages, dst_pages + n), src->pool,
+                                             std::vector<PageId>(src_pages, src_pages + n), S(stream)));
+}
+
+extern "C" int psk_slot_pool_create(psk_slot_pool** out, uint32_t max_sequences, uint32_t max_blocks,
+                                    void* stream) {
+    if (out == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    auto* h = new (std::nothrow) psk_slot_pool();
+    if (h == nullptr) return PSK_ERR_INSUFFICIENT_MEMORY;
+    const Status st = SequenceSlotPool::create(h->slots, max_sequences, max_blocks, S(stream));
+    if (!st.ok()) {
+        delete h;
+        return to_code(st);
+    }
+    *out = h;
+    return 0;
+}
+
+extern "C" void psk_slot_pool_destroy(psk_slot_pool* p) { delete p; }
+
+extern "C" uint32_t* psk_slot_pool_block_tables(const psk_slot_pool* p) {
+    return p ? p->slots.device_block_tables() : nullptr;
+}
+
+extern "C" int psk_sequence_create(psk_sequence** out, psk_slot_pool* slots, psk_kv_pool* pool,
+                                   uint32_t max_seq_len, void* stream) {
+    if (out == nullptr || slots == nullptr || pool == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    auto* h = new (std::nothrow) psk_sequence();
+    if (h == nullptr) return PSK_ERR_INSUFFICIENT_MEMORY;
+    const Status st = create_paged_sequence_state(h->seq, slots->slots, pool->pool, max_seq_len, S(stream));
+    if (!st.ok()) {
+        delete h;
+        return to_code(st);
+    }
+    *out = h;
+    return 0;
+}
+
+extern "C" int psk_sequence_release(psk_sequence* s, void* stream) {
+    if (s == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    const int rc = to_code(release_paged_sequence_state(s->seq, S(stream)));
+    delete s;
+    return rc;
+}
+
+extern "C" int psk_sequence_reserve(psk_sequence* s, uint32_t token_count, void* stream) {
+    if (s == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(reserve_sequence_append(s->seq, token_count, S(stream)));
+}
+
+extern "C" int psk_sequence_rollback(psk_sequence* s, uint32_t old_block_count, void* stream) {
+    if (s == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(rollback_sequence_append(s->seq, old_block_count, S(stream)));
+}
+
+extern "C" int psk_sequence_commit(psk_sequence* s, uint32_t tokens) {
+    if (s == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(commit_sequence_append(s->seq, tokens));
+}
+
+extern "C" int psk_sequence_info(const psk_sequence* s, psk_sequence_info_t* out) {
+    if (s == nullptr || out == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    out->slot = s->seq.slot;
+    out->generation = s->seq.generation;
+    out->position = s->seq.position;
+    out->max_seq_len = s->seq.max_seq_len;
+    out->num_blocks = static_cast<uint32_t>(s->seq.block_table.size());
+    out->poisoned = s->seq.is_poisoned() ? 1u : 0u;
+    return 0;
+}
+
+extern "C" uint32_t psk_sequence_block_table(const psk_sequence* s, uint32_t* out, uint32_t cap) {
+    if (s == nullptr) return 0;
+    const uint32_t n = static_cast<uint32_t>(s->seq.block_table.size());
+    for (uint32_t i = 0; i < n && i < cap && out; ++i) out[i] = s->seq.block_table[i];
+    return n;
+}
+
+extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, uint32_t kv_dtype,
+                                        const void* k_pool, const void* v_pool,
+                                        const float* k_scale_pool, const float* v_scale_pool,
+                                        const psk_step_request* requests, uint32_t num_requests,
+                                        uint32_t max_visible_tokens, float* partials,
+                                        uint64_t partial_bytes, psk_step_plan_t* plan_out,
+                                        void* stream) {
+    using namespace ps::qwen35::runtime;
+    if (common == nullptr || (num_requests > 0 && requests == nullptr)) return hipErrorInvalidValue;
+    PagedAttentionStep step;
+    std::memcpy(&step.common, common, sizeof(step.common));
+    step.kv_dtype = kv_dtype == PSK_KV_FP8_E4M3 ? KVCacheDType::FP8_E4M3 : KVCacheDType::BF16;
+    if (kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_BF16) return hipErrorInvalidValue;
+    step.k_pool = k_pool;
+    step.v_pool = v_pool;
+    step.k_scale_pool = k_scale_pool;
+    step.v_scale_pool = v_scale_pool;
+    std::vector<StepRequest> reqs(num_requests);
+    for (uint32_t i = 0; i < num_requests; ++i)
+        reqs[i] = {requests[i].row_begin, requests[i].row_count, requests[i].execution_class};
+    step.requests = reqs.data();
+    step.num_requests = num_requests;
+    step.max_visible_tokens = max_visible_tokens;
+    step.partials = partials;
+    step.partial_bytes = partial_bytes;
+    PagedAttentionPlan plan;
+    const Status st = plan_paged_attention_step(step, plan);
+    if (!st.ok()) {
+        g_last_error = st.message;
+        return hipErrorInvalidValue;
+    }
+    if (plan_out) {
+        plan_out->count = plan.count;
+        for (uint32_t i = 0; i < plan.count && i < PSK_MAX_PLANNED; ++i) {
+            plan_out->kernels[i].kind = plan.kernels[i].kind == PlannedKernel::Kind::Tile ? 1u : 0u;
+            plan_out->kernels[i].row_begin = plan.kernels[i].row_begin;
+            plan_out->kernels[i].rows = plan.kernels[i].rows;
+            plan_out->kernels[i].splits = plan.kernels[i].splits;
+            plan_out->kernels[i].pages_per_split = plan.kernels[i].pages_per_split;
+        }
+    }
+    if (stream == reinterpret_cast<void*>(~uintptr_t(0))) return hipSuccess;   // plan only
+    return launch_paged_attention_plan(step, plan, S(stream));
+}

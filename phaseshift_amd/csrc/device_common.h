@@ -32,6 +32,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
 
+// a, b -> bf16 pairs hi = bf16(x), lo = bf16(x - hi): hi + lo carries ~16
+// mantissa bits of x (RNE at each step).
+// Returns {hi, lo}.
+__device__ __forceinline__ u32x2 split_bf16x2(float a, float b) {
+    const uint32_t hi = pack_bf16x2(a, b);
+    const float ah = __uint_as_float(hi << 16), bh = __uint_as_float(hi & 0xFFFF0000u);
+    return (u32x2){hi, pack_bf16x2(a - ah, b - bh)};
+}
+
 // Two FP8 E4M3 codes (bytes 0/1 or 2/3 of `w`) -> two bf16 (exact: every E4M3
 // value is a bf16 value). One v_cvt_scalef32_pk_bf16_fp8 with unit scale.
 __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w, bool hi) {

@@ -1,0 +1,246 @@
+// resolve -> plan -> launch for one PAGED_ATTENTION binding of a step.
+//
+// Reference planner: runtime/paged_attention_dispatch.hip:437-477 (split rule),
+// :705-788 (regions), :790-894 (physical launch). Regions follow the
+// reference: the decode region is every row before the first PREFILL request
+// (decode and SPEC_VERIFY rows alike); each PREFILL request is its own region,
+// run by the multi-row tile launcher when it has >= 128 rows
+// (paged_attention_dispatch.h:49). New here: FP8 KV also gets split-K, and the
+// split size is chosen from the step's work instead of a fixed 16.
+#include <phaseshift_kv/dispatch.h>
+
+#include <algorithm>
+#include <vector>
+
+namespace psk {
+hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
+                              const void* v, const float* ks, const float* vs,
+                              const uint32_t* tile_begin, const uint32_t* tile_rows,
+                              uint32_t n_tiles, float* partials, uint32_t splits,
+                              uint32_t pages_per_split, hipStream_t stream);
+bool paged_tiles_supported(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
+                           const void* v);
+}  // namespace psk
+
+namespace ps::qwen35::runtime {
+
+using ::ps::kernel::PagedAttentionCommonArgs;
+using ::ps::kernel::PagedAttentionOutputDType;
+
+namespace {
+
+PagedAttentionCommonArgs region_args(const PagedAttentionCommonArgs& c, uint32_t row_begin,
+                                     uint32_t rows) {
+    PagedAttentionCommonArgs r = c;
+    const size_t out_elem = c.output_dtype == PagedAttentionOutputDType::F32 ? 4 : 2;
+    r.q = c.q + (size_t)row_begin * c.q_row_stride;
+    r.output = static_cast<uint8_t*>(c.output) + (size_t)row_begin * c.output_row_stride * out_elem;
+    r.row_sequence_slots = c.row_sequence_slots + row_begin;
+    r.row_positions = c.row_positions + row_begin;
+    r.rows = rows;
+    return r;
+}
+
+}  // namespace
+
+DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_heads,
+                                uint32_t page_tokens, uint32_t max_visible_tokens,
+                                uint64_t partial_bytes) {
+    DecodeSplit s;
+    if (max_visible_tokens < kSplitMinVisible || rows == 0 || kv_heads == 0) return s;
+    const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
+    const uint64_t work = (uint64_t)rows * kv_heads * max_pages;   // page-heads, upper bound
+    uint64_t per = std::max<uint64_t>(kMinPagesPerSplit, (work + kTargetWorkgroups - 1) / kTargetWorkgroups);
+    const uint32_t q_per_kv = q_heads / kv_heads;
+    for (;;) {
+        const uint64_t splits = (max_pages + per - 1) / per;
+        const uint64_t need = (uint64_t)rows * kv_heads * splits * q_per_kv *
+                              (2u + ::ps::kernel::kPagedAttentionHeadLimit) * sizeof(float);
+        if (splits <= 1) return s;
+        if (splits <= kMaxSplits && need <= partial_bytes) {
+            s.splits = static_cast<uint32_t>(splits);
+            s.pages_per_split = static_cast<uint32_t>(per);
+            return s;
+        }
+        per *= 2;
+    }
+}
+
+namespace {
+
+DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t region_rows, uint32_t kv_heads,
+                              uint32_t q_heads, uint32_t page_tokens, uint32_t max_visible_tokens,
+                              uint64_t partial_bytes) {
+    DecodeSplit s;
+    if (max_visible_tokens < kSplitMinVisible || n_tiles == 0 || kv_heads == 0) return s;
+    const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
+    const uint64_t work = (uint64_t)n_tiles * kv_heads * max_pages;
+    uint64_t per = std::max<uint64_t>(kMinPagesPerSplit, (work + kTargetWorkgroups - 1) / kTargetWorkgroups);
+    const uint32_t q_per_kv = q_heads / kv_heads;
+    for (;;) {
+        const uint64_t splits = (max_pages + per - 1) / per;
+        if (splits <= 1) return s;
+        const uint64_t need = (uint64_t)region_rows * kv_heads * splits * q_per_kv *
+                              (2u + ::ps::kernel::kPagedAttentionHeadLimit) * sizeof(float);
+        if (splits <= kMaxSplits && need <= partial_bytes) {
+            s.splits = static_cast<uint32_t>(splits);
+            s.pages_per_split = static_cast<uint32_t>(per);
+            return s;
+        }
+        per *= 2;
+    }
+}
+
+bool is_tile_request(const StepRequest& r) {
+    return (r.execution_class == kExecPrefill && r.row_count >= kPrefillMinRows) ||
+           (r.execution_class == kExecSpecVerify && r.row_count >= kVerifyTileMinRows);
+}
+
+}  // namespace
+
+Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionPlan& plan) {
+    plan = PagedAttentionPlan{};
+    const auto& c = step.common;
+    if (c.rows == 0) return Status::make_ok();
+    if (step.kv_dtype != KVCacheDType::BF16 && step.kv_dtype != KVCacheDType::FP8_E4M3)
+        return Status::invalid_argument("KV cache dtype not provided by this build");
+    const uint64_t pbytes = step.partials ? step.partial_bytes : 0;
+    auto push = [&](const PlannedKernel& k) -> Status {
+        if (plan.count >= kMaxPlannedKernels) return Status::out_of_range("too many launches in a step");
+        plan.kernels[plan.count++] = k;
+        return Status::make_ok();
+    };
+    auto add_decode = [&](uint32_t row_begin, uint32_t rows) -> Status {
+        PlannedKernel k;
+        k.kind = PlannedKernel::Kind::Decode;
+        k.row_begin = row_begin;
+        k.rows = rows;
+        const DecodeSplit s = choose_decode_split(rows, c.kv_heads, c.q_heads, c.page_tokens,
+                                                  step.max_visible_tokens, pbytes);
+        k.splits = s.splits;
+        k.pages_per_split = s.pages_per_split;
+        return push(k);
+    };
+
+    // Requests must partition [0, rows); otherwise every row runs on the
+    // decode kernel (always correct: each row attends to its own prefix).
+    std::vector<StepRequest> reqs(step.requests, step.requests + step.num_requests);
+    std::sort(reqs.begin(), reqs.end(),
+              [](const StepRequest& x, const StepRequest& y) { return x.row_begin < y.row_begin; });
+    bool partition = !reqs.empty();
+    uint32_t next = 0;
+    for (const auto& r : reqs) {
+        if (r.row_begin != next || r.row_count == 0) partition = false;
+        next = r.row_begin + r.row_count;
+    }
+    if (next != c.rows) partition = false;
+    if (!partition) return add_decode(0, c.rows);
+
+    // decode launches: maximal runs of consecutive non-tile requests
+    for (size_t i = 0; i < reqs.size();) {
+        if (is_tile_request(reqs[i])) {
+            ++i;
+            continue;
+        }
+        const uint32_t b = reqs[i].row_begin;
+        uint32_t e = b;
+        while (i < reqs.size() && !is_tile_request(reqs[i])) e = reqs[i].row_begin + reqs[i++].row_count;
+        Status st = add_decode(b, e - b);
+        if (!st.ok()) return st;
+    }
+    // one tile launch per class (verify blocks typically split, prefill not)
+    for (const uint8_t cls : {kExecSpecVerify, kExecPrefill}) {
+        PlannedKernel k;
+        k.kind = PlannedKernel::Kind::Tile;
+        k.tile_first = static_cast<uint32_t>(plan.tiles.size());
+        k.req_first = static_cast<uint32_t>(plan.combine.size());
+        uint32_t lo = UINT32_MAX, hi = 0;
+        for (const auto& r : reqs) {
+            if (r.execution_class != cls || !is_tile_request(r)) continue;
+            for (uint32_t t = 0; t < r.row_count; t += kTileRowsPerTile)
+                plan.tiles.push_back({r.row_begin + t, std::min(kTileRowsPerTile, r.row_count - t)});
+            plan.combine.push_back(r);
+            lo = std::min(lo, r.row_begin);
+            hi = std::max(hi, r.row_begin + r.row_count);
+        }
+        k.tile_count = static_cast<uint32_t>(plan.tiles.size()) - k.tile_first;
+        k.req_count = static_cast<uint32_t>(plan.combine.size()) - k.req_first;
+        if (k.tile_count == 0) continue;
+        k.row_begin = lo;
+        k.rows = hi - lo;
+        const DecodeSplit s = choose_tile_split(k.tile_count, k.rows, c.kv_heads, c.q_heads,
+                                                c.page_tokens, step.max_visible_tokens, pbytes);
+        k.splits = s.splits;
+        k.pages_per_split = s.pages_per_split;
+        Status st = push(k);
+        if (!st.ok()) return st;
+    }
+    return Status::make_ok();
+}
+
+hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const PagedAttentionPlan& plan,
+                                       hipStream_t stream) {
+    using namespace ::ps::kernel;
+    const bool fp8 = step.kv_dtype == KVCacheDType::FP8_E4M3;
+    const auto* k8 = static_cast<const ::ps::qwen35::fp8e4m3_storage_t*>(step.k_pool);
+    const auto* v8 = static_cast<const ::ps::qwen35::fp8e4m3_storage_t*>(step.v_pool);
+    const auto* k16 = static_cast<const bf16_t*>(step.k_pool);
+    const auto* v16 = static_cast<const bf16_t*>(step.v_pool);
+    for (uint32_t i = 0; i < plan.count; ++i) {
+        const PlannedKernel& k = plan.kernels[i];
+        const PagedAttentionCommonArgs a = region_args(step.common, k.row_begin, k.rows);
+        hipError_t e = hipSuccess;
+        if (k.kind == PlannedKernel::Kind::Tile) {
+            // tile rows are relative to the launch region
+            std::vector<uint32_t> tb(k.tile_count), tr(k.tile_count);
+            for (uint32_t t = 0; t < k.tile_count; ++t) {
+                tb[t] = plan.tiles[k.tile_first + t].row_begin - k.row_begin;
+                tr[t] = plan.tiles[k.tile_first + t].rows;
+            }
+            const psk_paged_attention_args* ca = reinterpret_cast<const psk_paged_attention_args*>(&a);
+            const uint32_t kvd = fp8 ? PSK_KV_FP8_E4M3 : PSK_KV_BF16;
+            if (psk::paged_tiles_supported(*ca, kvd, step.k_pool, step.v_pool)) {
+                e = psk::launch_paged_tiles(*ca, kvd, step.k_pool, step.v_pool, step.k_scale_pool,
+                                            step.v_scale_pool, tb.data(), tr.data(), k.tile_count,
+                                            step.partials, k.splits, k.pages_per_split, stream);
+                for (uint32_t q = 0; e == hipSuccess && k.splits > 1 && q < k.req_count; ++q) {
+                    const StepRequest& r = plan.combine[k.req_first + q];
+                    const PagedAttentionCommonArgs ra =
+                        region_args(a, r.row_begin - k.row_begin, r.row_count);
+                    // the combine reads partials of the region's rows; shift them with it
+                    const uint64_t row_floats = (uint64_t)a.kv_heads * k.splits *
+                                                (a.q_heads / a.kv_heads) * (2u + kPagedAttentionHeadLimit);
+                    e = launch_attention_paged_split_reduce_ex(
+                        ra, step.partials + (uint64_t)(r.row_begin - k.row_begin) * row_floats,
+                        k.splits, k.pages_per_split, stream);
+                }
+            } else {
+                // shapes outside the tile kernel: every row of each tile on the decode kernel
+                for (uint32_t t = 0; e == hipSuccess && t < k.tile_count; ++t) {
+                    const PagedAttentionCommonArgs ta = region_args(a, tb[t], tr[t]);
+                    e = fp8 ? launch_attention_paged_fp8_e4m3(ta, k8, v8, step.k_scale_pool,
+                                                              step.v_scale_pool, stream)
+                            : launch_attention_paged_bf16(ta, k16, v16, stream);
+                }
+            }
+        } else if (k.splits > 1) {
+            e = fp8 ? launch_attention_paged_fp8_e4m3_split(a, k8, v8, step.k_scale_pool,
+                                                            step.v_scale_pool, step.partials,
+                                                            k.splits, k.pages_per_split, stream)
+                    : static_cast<hipError_t>(psk_attention_paged_bf16_split_ex(
+                          reinterpret_cast<const psk_paged_attention_args*>(&a), k16, v16,
+                          step.partials, k.splits, k.pages_per_split, stream));
+            if (e == hipSuccess)
+                e = launch_attention_paged_split_reduce_ex(a, step.partials, k.splits,
+                                                           k.pages_per_split, stream);
+        } else {
+            e = fp8 ? launch_attention_paged_fp8_e4m3(a, k8, v8, step.k_scale_pool,
+                                                      step.v_scale_pool, stream)
+                    : launch_attention_paged_bf16(a, k16, v16, stream);
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace ps::qwen35::runtime

@@ -48,17 +48,11 @@ __global__ __launch_bounds__(256) void gather_kernel(const psk_kv_gather_args a,
 }
 
 // ------------------------------------------------------------- page copy
-// grid.x = pages-pairs * layers * 4 tensors (K, V, K-scale, V-scale); every
+// grid.x = page pairs * layers * 4 tensors (K, V, K-scale, V-scale); every
 // block copies one page body (or one page's scale rows) with 16 B accesses.
-__global__ __launch_bounds__(256) void copy_pages_kernel(const psk_page_copy_args a, uint32_t eb,
-                                                         uint32_t vec16) {
-    const uint32_t tensor = blockIdx.x & 3u;
-    const uint32_t rest = blockIdx.x >> 2;
-    const uint32_t layer = rest % a.num_layers;
-    const uint32_t pair = rest / a.num_layers;
-    if (pair >= a.num_pairs) return;
-    const uint32_t dst_page = a.pairs[pair].dst_page;
-    const uint32_t src_page = a.pairs[pair].src_page;
+__device__ __forceinline__ void copy_one(const psk_page_copy_args& a, uint32_t eb, uint32_t vec16,
+                                         uint32_t dst_page, uint32_t src_page, uint32_t layer,
+                                         uint32_t tensor) {
     if (dst_page >= a.dst_num_pages || src_page >= a.src_num_pages) return;
     const uint64_t page_elems = (uint64_t)a.page_tokens * a.kv_heads * a.head_dim;
     const uint64_t page_scales = (uint64_t)a.page_tokens * a.kv_heads;
@@ -85,6 +79,32 @@ __global__ __launch_bounds__(256) void copy_pages_kernel(const psk_page_copy_arg
     } else {
         for (uint64_t o = threadIdx.x; o < bytes; o += 256u) d[o] = s[o];
     }
+}
+
+__global__ __launch_bounds__(256) void copy_pages_kernel(const psk_page_copy_args a, uint32_t eb,
+                                                         uint32_t vec16) {
+    const uint32_t rest = blockIdx.x >> 2;
+    const uint32_t pair = rest / a.num_layers;
+    if (pair >= a.num_pairs) return;
+    copy_one(a, eb, vec16, a.pairs[pair].dst_page, a.pairs[pair].src_page, rest % a.num_layers,
+             blockIdx.x & 3u);
+}
+
+// Pairs passed by value in the kernel arguments (host-driven copies: no
+// device staging buffer and no ordering hazard on a reused host buffer).
+constexpr uint32_t kInlinePairs = 32;
+struct InlinePairs {
+    psk_page_copy_pair p[kInlinePairs];
+};
+
+__global__ __launch_bounds__(256) void copy_pages_inline_kernel(const psk_page_copy_args a,
+                                                                const InlinePairs pairs, uint32_t eb,
+                                                                uint32_t vec16) {
+    const uint32_t rest = blockIdx.x >> 2;
+    const uint32_t pair = rest / a.num_layers;
+    if (pair >= a.num_pairs) return;
+    copy_one(a, eb, vec16, pairs.p[pair].dst_page, pairs.p[pair].src_page, rest % a.num_layers,
+             blockIdx.x & 3u);
 }
 
 // ------------------------------------------------------------------ fill
@@ -258,24 +278,59 @@ extern "C" int psk_kv_gather(const psk_kv_gather_args* a, const void* pool, void
     return hipGetLastError();
 }
 
-extern "C" int psk_kv_copy_pages(const psk_page_copy_args* a, void* stream) {
+namespace psk {
+namespace {
+hipError_t copy_validate(const psk_page_copy_args* a, uint32_t& eb, uint32_t& vec16) {
     if (a == nullptr) return hipErrorInvalidValue;
-    if (a->num_pairs == 0u) return hipSuccess;
-    if (a->pairs == nullptr || a->dst_k == nullptr || a->dst_v == nullptr || a->src_k == nullptr ||
-        a->src_v == nullptr || a->num_layers == 0u || a->page_tokens == 0u || a->kv_heads == 0u ||
-        a->head_dim == 0u)
+    if (a->dst_k == nullptr || a->dst_v == nullptr || a->src_k == nullptr || a->src_v == nullptr ||
+        a->num_layers == 0u || a->page_tokens == 0u || a->kv_heads == 0u || a->head_dim == 0u)
         return hipErrorInvalidValue;
     if (a->kv_dtype != PSK_KV_BF16 && a->kv_dtype != PSK_KV_FP8_E4M3) return hipErrorInvalidValue;
     if (a->kv_dtype == PSK_KV_FP8_E4M3 &&
         (a->dst_k_scale == nullptr || a->dst_v_scale == nullptr || a->src_k_scale == nullptr ||
          a->src_v_scale == nullptr))
         return hipErrorInvalidValue;
-    const uint32_t eb = a->kv_dtype == PSK_KV_FP8_E4M3 ? 1u : 2u;
+    eb = a->kv_dtype == PSK_KV_FP8_E4M3 ? 1u : 2u;
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16u == 0u; };
-    const uint32_t vec16 = al(a->dst_k) && al(a->dst_v) && al(a->src_k) && al(a->src_v) &&
-                           (a->kv_dtype != PSK_KV_FP8_E4M3 ||
-                            (al(a->dst_k_scale) && al(a->dst_v_scale) && al(a->src_k_scale) &&
-                             al(a->src_v_scale)));
+    vec16 = al(a->dst_k) && al(a->dst_v) && al(a->src_k) && al(a->src_v) &&
+            (a->kv_dtype != PSK_KV_FP8_E4M3 ||
+             (al(a->dst_k_scale) && al(a->dst_v_scale) && al(a->src_k_scale) && al(a->src_v_scale)));
+    return hipSuccess;
+}
+}  // namespace
+
+// Host-array variant used by the C++ pool layer: chunks of kInlinePairs pairs
+// go to the kernel by value.
+hipError_t copy_pages_host_pairs(const psk_page_copy_args& args, const psk_page_copy_pair* pairs,
+                                 uint32_t n, hipStream_t stream) {
+    uint32_t eb = 0, vec16 = 0;
+    const hipError_t e = copy_validate(&args, eb, vec16);
+    if (e != hipSuccess) return e;
+    for (uint32_t b = 0; b < n; b += kInlinePairs) {
+        psk_page_copy_args a = args;
+        a.num_pairs = n - b < kInlinePairs ? n - b : kInlinePairs;
+        a.pairs = nullptr;
+        InlinePairs ip{};
+        for (uint32_t i = 0; i < a.num_pairs; ++i) ip.p[i] = pairs[b + i];
+        const uint64_t blocks = (uint64_t)a.num_pairs * a.num_layers * 4u;
+        if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(copy_pages_inline_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
+                           a, ip, eb, vec16);
+        const hipError_t le = hipGetLastError();
+        if (le != hipSuccess) return le;
+    }
+    return hipSuccess;
+}
+
+}  // namespace psk
+
+extern "C" int psk_kv_copy_pages(const psk_page_copy_args* a, void* stream) {
+    if (a == nullptr) return hipErrorInvalidValue;
+    if (a->num_pairs == 0u) return hipSuccess;
+    if (a->pairs == nullptr) return hipErrorInvalidValue;
+    uint32_t eb = 0, vec16 = 0;
+    const hipError_t e = psk::copy_validate(a, eb, vec16);
+    if (e != hipSuccess) return e;
     const uint64_t blocks = (uint64_t)a->num_pairs * a->num_layers * 4u;
     if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
     hipLaunchKernelGGL(psk::copy_pages_kernel, dim3((uint32_t)blocks), dim3(256), 0,

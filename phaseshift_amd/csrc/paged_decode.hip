@@ -307,28 +307,34 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
 
         wave_lds_sync();
         // ---- O^T += V^T * P^T
+        // P (with v_scale folded in) as hi + lo bf16 pairs: two MFMAs keep
+        // ~16 mantissa bits of every weight (V and K are exact in bf16).
         if constexpr (KVB == 1) {
-            u32x4 pw;
-            pw[0] = pack_bf16x2(pv[0][0], pv[0][1]);
-            pw[1] = pack_bf16x2(pv[0][2], pv[0][3]);
-            pw[2] = pack_bf16x2(pv[1][0], pv[1][1]);
-            pw[3] = pack_bf16x2(pv[1][2], pv[1][3]);
-            const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
+            u32x4 ph, pl;
+            { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
+            { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
+            { const u32x2 t_ = split_bf16x2(pv[1][0], pv[1][1]); ph[2] = t_[0]; pl[2] = t_[1]; }
+            { const u32x2 t_ = split_bf16x2(pv[1][2], pv[1][3]); ph[3] = t_[0]; pl[3] = t_[1]; }
+            const bf16x8 pfh = __builtin_bit_cast(bf16x8, ph);
+            const bf16x8 pfl = __builtin_bit_cast(bf16x8, pl);
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
                 const i32x2 w = lds_read_tr8(vt + tr_off + 16 * db);
                 const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfh, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfl, o[db], 0, 0, 0);
             }
         } else {
-            u32x2 pw;
-            pw[0] = pack_bf16x2(pv[0][0], pv[0][1]);
-            pw[1] = pack_bf16x2(pv[0][2], pv[0][3]);
-            const i16x4 pf = __builtin_bit_cast(i16x4, pw);
+            u32x2 ph, pl;
+            { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
+            { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
+            const i16x4 pfh = __builtin_bit_cast(i16x4, ph);
+            const i16x4 pfl = __builtin_bit_cast(i16x4, pl);
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
                 const i16x4 vf = lds_read_tr16(vt + tr_off + 32 * db);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pfh, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pfl, o[db], 0, 0, 0);
             }
         }
         wave_lds_sync();

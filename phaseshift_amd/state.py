@@ -1,0 +1,170 @@
+"""Python handles over the host KV state of the C-ABI (PagedKVPool,
+SequenceSlotPool, PagedSequenceState) and the step planner.
+
+Reference classes: src/phaseshift/models/qwen35/state/paged_kv_pool.cpp,
+sequence_slot_pool.cpp, paged_sequence_state.cpp, and
+runtime/paged_attention_dispatch.hip (planner). Errors raise StateError with
+the reference's Status category (invalid_argument, out_of_range, ...).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+from . import (KV_BF16, KV_FP8, PLAN_ONLY, PoolInfo, SequenceInfo, StepPlan, StepRequest, check,
+               check_state, lib)
+from .ops import PoolGeometry, _stream
+
+
+class KVPool:
+    def __init__(self, num_pages, page_tokens, num_layers, kv_heads, head_dim, fp8=True):
+        self._h = C.c_void_p()
+        check_state("psk_pool_create", lib().psk_pool_create(
+            C.byref(self._h), num_pages, page_tokens, num_layers, kv_heads, head_dim,
+            KV_FP8 if fp8 else KV_BF16))
+        self.geom = PoolGeometry(num_layers, num_pages, page_tokens, kv_heads, head_dim)
+        self.fp8 = fp8
+
+    def close(self):
+        if self._h:
+            lib().psk_pool_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self) -> PoolInfo:
+        i = PoolInfo()
+        check_state("psk_pool_info", lib().psk_pool_info(self._h, C.byref(i)))
+        return i
+
+    def allocate(self) -> int:
+        p = C.c_uint32()
+        check_state("psk_pool_allocate", lib().psk_pool_allocate(self._h, C.byref(p)))
+        return p.value
+
+    def release(self, page: int) -> None:
+        check_state("psk_pool_release", lib().psk_pool_release(self._h, page))
+
+    def copy_pages_from(self, src: "KVPool", dst_pages, src_pages, stream=None) -> None:
+        n = len(dst_pages)
+        d = (C.c_uint32 * n)(*dst_pages)
+        s = (C.c_uint32 * n)(*src_pages)
+        check_state("psk_pool_copy_pages", lib().psk_pool_copy_pages(
+            self._h, src._h, d, s, n, _stream(stream)))
+
+    def tensors(self, torch):
+        """Views of the pools as torch tensors (no copy)."""
+        i = self.info()
+        g = self.geom
+        n = g.pool_elems
+        dt = torch.uint8 if self.fp8 else torch.int16
+        out = {"k": _wrap(torch, i.k_pool, n, dt), "v": _wrap(torch, i.v_pool, n, dt)}
+        if self.fp8:
+            out["k_scale"] = _wrap(torch, i.k_scale_pool, g.scale_elems, torch.float32)
+            out["v_scale"] = _wrap(torch, i.v_scale_pool, g.scale_elems, torch.float32)
+        return out
+
+
+def _wrap(torch, ptr, n, dtype):
+    """A torch tensor aliasing device memory owned by the library."""
+    itemsize = torch.tensor([], dtype=dtype).element_size()
+
+    class _Mem:
+        __cuda_array_interface__ = None
+
+    typestr = {torch.uint8: "|u1", torch.int16: "<i2", torch.float32: "<f4",
+               torch.int32: "<i4"}[dtype]
+    m = _Mem()
+    m.__cuda_array_interface__ = {"shape": (n,), "typestr": typestr, "data": (ptr, False),
+                                  "version": 3, "strides": (itemsize,)}
+    return torch.as_tensor(m, device="cuda")
+
+
+class SlotPool:
+    def __init__(self, max_sequences, max_blocks, stream=None):
+        self._h = C.c_void_p()
+        check_state("psk_slot_pool_create", lib().psk_slot_pool_create(
+            C.byref(self._h), max_sequences, max_blocks, _stream(stream)))
+        self.max_sequences, self.max_blocks = max_sequences, max_blocks
+
+    def block_tables(self, torch):
+        ptr = lib().psk_slot_pool_block_tables(self._h)
+        return _wrap(torch, ptr, self.max_sequences * self.max_blocks, torch.int32).view(
+            self.max_sequences, self.max_blocks)
+
+    def close(self):
+        if self._h:
+            lib().psk_slot_pool_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Sequence:
+    def __init__(self, slots: SlotPool, pool: KVPool, max_seq_len: int, stream=None):
+        self._h = C.c_void_p()
+        check_state("psk_sequence_create", lib().psk_sequence_create(
+            C.byref(self._h), slots._h, pool._h, max_seq_len, _stream(stream)))
+
+    def info(self) -> SequenceInfo:
+        i = SequenceInfo()
+        check_state("psk_sequence_info", lib().psk_sequence_info(self._h, C.byref(i)))
+        return i
+
+    @property
+    def slot(self) -> int:
+        return self.info().slot
+
+    @property
+    def position(self) -> int:
+        return self.info().position
+
+    def block_table(self) -> list[int]:
+        n = lib().psk_sequence_block_table(self._h, None, 0)
+        buf = (C.c_uint32 * max(n, 1))()
+        lib().psk_sequence_block_table(self._h, buf, n)
+        return list(buf[:n])
+
+    def reserve(self, tokens: int, stream=None) -> None:
+        check_state("psk_sequence_reserve", lib().psk_sequence_reserve(self._h, tokens,
+                                                                       _stream(stream)))
+
+    def rollback(self, old_block_count: int, stream=None) -> None:
+        check_state("psk_sequence_rollback", lib().psk_sequence_rollback(
+            self._h, old_block_count, _stream(stream)))
+
+    def commit(self, tokens: int) -> None:
+        check_state("psk_sequence_commit", lib().psk_sequence_commit(self._h, tokens))
+
+    def release(self, stream=None) -> None:
+        if self._h:
+            h, self._h = self._h, C.c_void_p()
+            check_state("psk_sequence_release", lib().psk_sequence_release(h, _stream(stream)))
+
+
+def plan_step(args, kv_dtype: int, requests, max_visible_tokens: int, partial_bytes: int,
+              partials_ptr=None, k_pool=None, v_pool=None, k_scale=None, v_scale=None,
+              stream=None, launch=False) -> StepPlan:
+    """psk_paged_attention_step: plan (and with launch=True run) one step's
+    PAGED_ATTENTION binding. requests: list of (row_begin, row_count, exec_class)."""
+    n = len(requests)
+    reqs = (StepRequest * max(n, 1))()
+    for i, (b, c, e) in enumerate(requests):
+        reqs[i].row_begin, reqs[i].row_count, reqs[i].execution_class = b, c, e
+    plan = StepPlan()
+    p = lambda t: None if t is None else (t if isinstance(t, int) else t.data_ptr())
+    # planning alone only needs a non-null partials pointer to allow split-K
+    part = p(partials_ptr) if partials_ptr is not None else (16 if partial_bytes else None)
+    rc = lib().psk_paged_attention_step(
+        C.byref(args), kv_dtype, p(k_pool), p(v_pool), p(k_scale), p(v_scale), reqs, n,
+        max_visible_tokens, part, partial_bytes, C.byref(plan),
+        _stream(stream) if launch else PLAN_ONLY)
+    check("psk_paged_attention_step", rc)
+    return plan

@@ -21,3 +21,10 @@ def dev():
     import phaseshift_amd
     phaseshift_amd.lib()   # fails loudly when the HIP library is missing
     return torch.device("cuda:0")
+
+
+def pytest_runtest_logstart(nodeid, location):
+    # name the case before it touches the GPU (flushed, so it survives a crash)
+    import sys
+    sys.stderr.write(f"\n[start] {nodeid}\n")
+    sys.stderr.flush()

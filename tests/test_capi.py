@@ -39,6 +39,15 @@ def test_library_exports_every_declared_symbol():
         getattr(L, n)
 
 
+def test_every_exported_entry_point_has_a_ctypes_prototype():
+    """Without a prototype ctypes passes device pointers as 32-bit ints."""
+    exported_c = {s for s in exported() if s.startswith("psk_")}
+    assert exported_c <= set(P.SIGNATURES), exported_c - set(P.SIGNATURES)
+    assert declared_c_symbols() == exported_c
+    with pytest.raises(AttributeError):
+        P.lib().psk_not_a_function
+
+
 def test_reference_cpp_launchers_exported():
     syms = exported()
     for name in ["launch_kv_append_bf16", "launch_kv_append_fp8_e4m3",

@@ -1,0 +1,70 @@
+"""Step planner (host logic, no GPU): region rules of the reference
+(paged_attention_dispatch.hip:705-788) plus the tile routing of verify blocks
+and the split sizing. Runs the C-ABI in plan-only mode."""
+import phaseshift_amd as P
+from phaseshift_amd import state
+
+
+def args(rows, qh=24, kvh=4, hd=256, page=16):
+    a = P.PagedAttentionArgs()
+    a.rows, a.q_heads, a.kv_heads, a.head_dim, a.page_tokens = rows, qh, kvh, hd, page
+    return a
+
+
+def kernels(plan):
+    return [(k.kind, k.row_begin, k.rows, k.splits, k.pages_per_split)
+            for k in plan.kernels[:plan.count]]
+
+
+def test_config5_mixed_step_layout():
+    reqs = ([(i, 1, 0) for i in range(48)] + [(48 + 16 * i, 16, 1) for i in range(8)] +
+            [(176 + 512 * i, 512, 2) for i in range(8)])
+    plan = state.plan_step(args(4272), P.KV_FP8, reqs, 16384, 256 << 20)
+    ks = kernels(plan)
+    assert ks[0][:3] == (0, 0, 48)               # decode rows, split-K
+    assert ks[0][3] > 1
+    assert ks[1][:3] == (1, 48, 128)             # 8 verify blocks -> one tile launch
+    assert ks[1][3] > 1                          # few tiles -> split-K
+    assert ks[2][:3] == (1, 176, 4096)           # 8 prefill chunks -> one tile launch
+    assert plan.count == 3
+
+
+def test_short_context_does_not_split_and_reference_threshold():
+    plan = state.plan_step(args(64), P.KV_FP8, [(i, 1, 0) for i in range(64)], 2047, 1 << 30)
+    assert kernels(plan) == [(0, 0, 64, 1, 0)]
+    plan = state.plan_step(args(64), P.KV_FP8, [(i, 1, 0) for i in range(64)], 2048, 1 << 30)
+    assert kernels(plan)[0][3] > 1
+
+
+def test_no_workspace_means_no_split():
+    plan = state.plan_step(args(64), P.KV_BF16, [(i, 1, 0) for i in range(64)], 32768, 0)
+    assert kernels(plan) == [(0, 0, 64, 1, 0)]
+
+
+def test_split_respects_workspace_cap():
+    cap = 32 << 20   # the reference's 32 MiB partial workspace (program_executor.h:21)
+    plan = state.plan_step(args(64), P.KV_FP8, [(i, 1, 0) for i in range(64)], 65536, cap)
+    k = plan.kernels[0]
+    need = 64 * 4 * k.splits * 6 * 258 * 4
+    assert k.splits > 1 and need <= cap
+    assert k.splits * k.pages_per_split >= 65536 // 16
+
+
+def test_small_prefill_and_small_verify_stay_on_decode():
+    reqs = [(0, 4, 1), (4, 100, 2), (104, 1, 0)]   # 4-row verify, 100-row prefill chunk
+    plan = state.plan_step(args(105), P.KV_BF16, reqs, 4096, 1 << 30)
+    ks = kernels(plan)
+    assert len(ks) == 1 and ks[0][:3] == (0, 0, 105)
+
+
+def test_gapped_requests_fall_back_to_one_decode_region():
+    plan = state.plan_step(args(40), P.KV_FP8, [(0, 8, 0), (16, 24, 1)], 100, 0)
+    assert kernels(plan) == [(0, 0, 40, 1, 0)]
+
+
+def test_decode_runs_between_tiles():
+    reqs = [(0, 2, 0), (2, 16, 1), (18, 3, 0), (21, 128, 2), (149, 1, 0)]
+    plan = state.plan_step(args(150), P.KV_FP8, reqs, 1000, 0)
+    ks = kernels(plan)
+    assert [(k[0], k[1], k[2]) for k in ks] == [(0, 0, 2), (0, 18, 3), (0, 149, 1),
+                                                 (1, 2, 16), (1, 21, 128)]
