@@ -59,3 +59,17 @@ hipError_t launch_kv_append_fp8_e4m3(const KvAppendCommonArgs& common,
                                      hipStream_t stream);
 
 }  // namespace ps::kernel
+
+namespace ps::kernel {
+// PSQ4_W32 / PSQ8_W32 appends (kv_append.h:99-125 of the reference): not
+// provided by this build; they return hipErrorNotSupported, which the
+// reference dispatcher turns into its correctness-kernel fallback.
+hipError_t launch_kv_append_psq4(const KvAppendCommonArgs& common, uint8_t* k_code_pool,
+                                 uint8_t* v_code_pool, bf16_t* k_scale_pool, bf16_t* v_scale_pool,
+                                 uint32_t blocks_per_head,
+                                 ::ps::qwen35::Psq4ScaleEstimator estimator, hipStream_t stream);
+hipError_t launch_kv_append_psq8(const KvAppendCommonArgs& common, uint8_t* k_code_pool,
+                                 uint8_t* v_code_pool, bf16_t* k_scale_pool, bf16_t* v_scale_pool,
+                                 uint32_t blocks_per_head,
+                                 ::ps::qwen35::Psq8ScaleEstimator estimator, hipStream_t stream);
+}  // namespace ps::kernel

@@ -101,3 +101,41 @@ hipError_t launch_attention_paged_split_reduce_ex(const PagedAttentionCommonArgs
                                                   hipStream_t stream);
 
 }  // namespace ps::kernel
+
+namespace ps::kernel {
+// PSQ attention launchers (paged_attention.h:203-283 of the reference) and the
+// split-reduce variant knob (:35): not provided by this build (PSQ KV is a
+// later row); the launchers return hipErrorNotSupported, which the reference
+// dispatcher turns into its correctness-kernel fallback.
+uint32_t paged_attention_split_reduce_qh_per_wg();
+hipError_t launch_attention_paged_psq4(const PagedAttentionCommonArgs& common,
+                                       const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                                       const bf16_t* k_scale_pool, const bf16_t* v_scale_pool,
+                                       uint32_t blocks_per_head, hipStream_t stream);
+hipError_t launch_attention_paged_psq8(const PagedAttentionCommonArgs& common,
+                                       const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                                       const bf16_t* k_scale_pool, const bf16_t* v_scale_pool,
+                                       uint32_t blocks_per_head, hipStream_t stream);
+hipError_t launch_attention_paged_prefill_psq4(const PagedAttentionCommonArgs& common,
+                                               const uint8_t* k_code_pool,
+                                               const uint8_t* v_code_pool,
+                                               const bf16_t* k_scale_pool,
+                                               const bf16_t* v_scale_pool,
+                                               uint32_t blocks_per_head, hipStream_t stream);
+hipError_t launch_attention_paged_prefill_psq8(const PagedAttentionCommonArgs& common,
+                                               const uint8_t* k_code_pool,
+                                               const uint8_t* v_code_pool,
+                                               const bf16_t* k_scale_pool,
+                                               const bf16_t* v_scale_pool,
+                                               uint32_t blocks_per_head, hipStream_t stream);
+hipError_t launch_attention_paged_psq8_split(const PagedAttentionCommonArgs& common,
+                                             const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                                             const bf16_t* k_scale_pool, const bf16_t* v_scale_pool,
+                                             uint32_t blocks_per_head, float* partials,
+                                             uint32_t splits, hipStream_t stream);
+hipError_t launch_attention_paged_psq4_split(const PagedAttentionCommonArgs& common,
+                                             const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                                             const bf16_t* k_scale_pool, const bf16_t* v_scale_pool,
+                                             uint32_t blocks_per_head, float* partials,
+                                             uint32_t splits, hipStream_t stream);
+}  // namespace ps::kernel

@@ -26,6 +26,11 @@ enum class KVCacheDType : uint8_t {
     PSQ8_W32 = 4,
 };
 
+// PSQ KV estimators (kv_cache_types.h:27-30,42-45); PSQ dtypes are declared
+// for signature compatibility, their launchers report hipErrorNotSupported.
+enum class Psq4ScaleEstimator : uint8_t { MaxAbs = 0, Lsq1 = 1 };
+enum class Psq8ScaleEstimator : uint8_t { MaxAbs = 0, Lsq1 = 1 };
+
 using PageId = uint32_t;
 using SequenceSlotId = uint32_t;
 inline constexpr PageId kInvalidPageId = std::numeric_limits<PageId>::max();
