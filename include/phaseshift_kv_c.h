@@ -206,9 +206,11 @@ uint64_t psk_attention_split_partials_bytes(uint32_t rows, uint32_t q_heads,
                                             uint32_t kv_heads, uint32_t splits);
 
 /* Multi-row tiles (speculative verify blocks, chunked prefill)
- * [attention/paged_prefill.hip:115-459,586-850]: rows [32*t, 32*t+32) of a
- * launch form one tile and must belong to one sequence with non-decreasing
- * positions (the reference's own tile contract, paged_prefill.hip:152-164). */
+ * [attention/paged_prefill.hip:115-459,586-850]: rows [16*t, 16*t+16) of a
+ * launch form one tile and belong to the sequence of the tile's first row
+ * (the reference's own tile contract, paged_prefill.hip:152-164); rows of
+ * another slot are left unwritten. Shapes outside the tile kernel (q_per_kv
+ * > 8) run row by row on the decode launcher. */
 int psk_attention_paged_prefill_bf16(const psk_paged_attention_args* a, const void* k_pool,
                                      const void* v_pool, void* stream);
 int psk_attention_paged_prefill_fp8_e4m3(const psk_paged_attention_args* a,
@@ -309,10 +311,14 @@ int psk_sequence_info(const psk_sequence* seq, psk_sequence_info_t* out);
 uint32_t psk_sequence_block_table(const psk_sequence* seq, uint32_t* out, uint32_t cap);
 
 /* ---- Step planner (paged_attention_dispatch.hip:437-894) -------------------
- * Plans and launches the PAGED_ATTENTION binding of one mixed step: decode
- * region (rows before the first PREFILL request) with split-K when
- * max_visible_tokens >= 2048 and partials fit, PREFILL requests of >= 128 rows
- * on the tile launcher. stream == (void*)~0 plans without launching. */
+ * Plans and launches the PAGED_ATTENTION binding of one mixed step. Requests
+ * must partition [0, rows) in order (else the whole step is one decode
+ * region). PREFILL requests of >= 128 rows (the reference rule) and
+ * SPEC_VERIFY requests of >= 8 rows go to one tile launch per class; runs of
+ * the other requests go to decode launches. A launch uses split-K when its
+ * max_visible_tokens >= 2048 and the partials fit partial_bytes; splits are
+ * sized to ~2048 workgroups of >= 16 pages. stream == (void*)~0 plans without
+ * launching. */
 #define PSK_MAX_PLANNED 16
 typedef struct psk_step_request {
     uint32_t row_begin;
