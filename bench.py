@@ -33,6 +33,21 @@ HBM_PEAK_GBPS = 8000.0
 BYTES_PER_TOKEN_FP8 = 2 * 4 * 256 + 2 * 4 * 4 + 4 / 16      # 2080.25
 BYTES_PER_TOKEN_BF16 = 2 * 4 * 256 * 2 + 4 / 16              # 4096.25
 APPEND_BYTES_PER_ROW_FP8 = 2 * 4 * 256 * 2 + 8 + 4 + 2 * 4 * 256 + 2 * 4 * 4   # 6188
+# Untimed warm-up runs at least `--warmup` steps and at least this long, so the
+# GPU clocks have ramped before a timed loop starts.
+WARM_MIN_S = 0.2
+
+
+def warm(torch, fn, steps):
+    """Runs fn() at least `steps` times and for at least WARM_MIN_S seconds."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < steps or time.perf_counter() - t0 < WARM_MIN_S:
+        fn()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
 
 
 def parse():
@@ -103,13 +118,10 @@ def decode_setup(torch, ops, lens, fp8, seed, dev):
                 bt=bt.to(dev), lens=np.asarray(lens), fp8=fp8, QH=QH)
 
 
-def choose_splits(lens, kv_heads=4, target_wgs=2048, min_pages=16):
-    """Pages per split so that rows*kv_heads*splits ~ target_wgs (>= 8 WGs per CU)."""
-    pages = np.ceil(np.asarray(lens) / 16).astype(int)
-    total = int(pages.sum()) * kv_heads
-    per = max(min_pages, int(math.ceil(total / target_wgs)))
-    splits = int(math.ceil(pages.max() / per))
-    return splits, per
+def choose_splits(ops, lens, fp8, kv_heads=4, q_heads=24, head_dim=256, page_tokens=16):
+    """The step planner's split choice for these rows (psk_choose_decode_split)."""
+    return ops.choose_decode_split(len(lens), q_heads, kv_heads, head_dim, page_tokens, fp8,
+                                   lens, 1 << 40)
 
 
 def run_decode(torch, ops, st, steps, warmup, dev, splits=None, pps=None):
@@ -118,7 +130,7 @@ def run_decode(torch, ops, st, steps, warmup, dev, splits=None, pps=None):
     from phaseshift_amd import lib, check
     g, lens = st["g"], st["lens"]
     if splits is None:
-        splits, pps = choose_splits(lens)
+        splits, pps = choose_splits(ops, lens, st["fp8"])
     rows = len(lens)
     a = ops.attention_args(g, 0, st["q"], st["out"], st["slots"], st["pos"], st["bt"], st["QH"])
     nbytes = ops.split_partials_bytes(rows, st["QH"], g.kv_heads, splits)
@@ -140,10 +152,11 @@ def run_decode(torch, ops, st, steps, warmup, dev, splits=None, pps=None):
         check("reduce", L.psk_attention_paged_split_reduce_ex(C.byref(a), partials.data_ptr(),
                                                               splits, pps, s))
 
-    for _ in range(warmup):
+    def step():
         split_launch()
         reduce_launch()
-    torch.cuda.synchronize()
+
+    warm(torch, step, warmup)
     # step time: K back-to-back steps
     t = Timer(torch)
     with t:
@@ -153,6 +166,7 @@ def run_decode(torch, ops, st, steps, warmup, dev, splits=None, pps=None):
     step_ms = t.ms() / steps
     # per-kernel durations: HIP events on the launch stream around `steps`
     # back-to-back launches of that kernel alone (amortizes the event gaps)
+    warm(torch, split_launch, 1)
     t1 = Timer(torch)
     with t1:
         for _ in range(steps):
@@ -188,9 +202,7 @@ def run_append(torch, ops, rows, steps, warmup, dev, seed=7):
     def launch():
         ops.kv_append(g, 0, k, v, slots, pos, bt, kp, vp, ks, vs)
 
-    for _ in range(warmup):
-        launch()
-    torch.cuda.synchronize()
+    warm(torch, launch, warmup)
     t = Timer(torch)
     with t:
         for _ in range(steps):
@@ -301,6 +313,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_s": WARM_MIN_S,
         "ms_per_step": round(step_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",

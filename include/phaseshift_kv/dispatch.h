@@ -17,8 +17,8 @@ inline constexpr uint8_t kExecDecode = 0, kExecSpecVerify = 1, kExecPrefill = 2,
 // split-K from 2048 visible tokens (paged_attention_dispatch.hip:437).
 inline constexpr uint32_t kPrefillMinRows = 128u;
 inline constexpr uint32_t kSplitMinVisible = 2048u;
-// Split sizing on MI355X: ~8 workgroups per CU over 256 CUs, splits of at
-// least 16 pages (256 tokens at page 16).
+// Split sizing on MI355X: tile launches aim at ~8 workgroups per CU over 256
+// CUs; every split holds at least 16 pages (256 tokens at page 16).
 inline constexpr uint64_t kTargetWorkgroups = 2048u;
 inline constexpr uint64_t kMinPagesPerSplit = 16u;
 inline constexpr uint64_t kMaxSplits = 1024u;
@@ -78,8 +78,13 @@ struct PagedAttentionPlan {
     std::vector<StepRequest> combine;   // row ranges combined after a split tile launch
 };
 
+// Split-K sizing of a decode launch: the split count (and pages per split)
+// whose units finish first under the decode kernel's XCD-aware dispatch, given
+// the rows' visible lengths (row_visible, host array; nullptr: every row at
+// max_visible_tokens) and the partials workspace. splits == 1: do not split.
 DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_heads,
-                                uint32_t page_tokens, uint32_t max_visible_tokens,
+                                uint32_t head_dim, uint32_t kv_bytes, uint32_t page_tokens,
+                                uint32_t max_visible_tokens, const uint32_t* row_visible,
                                 uint64_t partial_bytes);
 Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionPlan& plan);
 hipError_t launch_paged_attention_plan(const PagedAttentionStep& step,

@@ -346,6 +346,16 @@ int psk_paged_attention_step(const psk_paged_attention_args* common, uint32_t kv
                              uint32_t num_requests, uint32_t max_visible_tokens, float* partials,
                              uint64_t partial_bytes, psk_step_plan_t* plan_out, void* stream);
 
+/* Split-K sizing the planner uses for a decode launch (additive, no reference
+ * counterpart): the split count and pages per split that finish first under
+ * the decode kernel's XCD-aware dispatch on this device. row_visible is an
+ * optional host array of the rows' visible lengths (NULL: every row at
+ * max_visible_tokens); the partials must fit partial_bytes. *splits == 1:
+ * launch unsplit. Uses a->rows, q_heads, kv_heads, head_dim, page_tokens. */
+int psk_choose_decode_split(const psk_paged_attention_args* a, uint32_t kv_dtype,
+                            const uint32_t* row_visible, uint32_t max_visible_tokens,
+                            uint64_t partial_bytes, uint32_t* splits, uint32_t* pages_per_split);
+
 /* ---- Self-test hooks (diagnostics, no reference counterpart) --------------- */
 /* Runs the device E4M3 encoder of the append kernel on the floats whose bit
  * patterns are start_bits .. start_bits+count-1 (count % 4 == 0); word i of

@@ -146,6 +146,7 @@ SIGNATURES = {
     "psk_sequence_info": [_P, _P],
     "psk_sequence_block_table": [_P, _P, _U32],
     "psk_paged_attention_step": [_P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _P, C.c_uint64, _P, _P],
+    "psk_choose_decode_split": [_P, _U32, _P, _U32, C.c_uint64, _P, _P],
     "psk_selftest_e4m3_encode_range": [_U32, _U32, _P, _P],
     "psk_selftest_e4m3_decode_all": [_P, _P],
     "psk_version": [],

@@ -215,3 +215,20 @@ extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, 
     if (stream == reinterpret_cast<void*>(~uintptr_t(0))) return hipSuccess;   // plan only
     return launch_paged_attention_plan(step, plan, S(stream));
 }
+
+extern "C" int psk_choose_decode_split(const psk_paged_attention_args* a, uint32_t kv_dtype,
+                                       const uint32_t* row_visible, uint32_t max_visible_tokens,
+                                       uint64_t partial_bytes, uint32_t* splits,
+                                       uint32_t* pages_per_split) {
+    using namespace ps::qwen35::runtime;
+    if (a == nullptr || splits == nullptr || pages_per_split == nullptr || a->kv_heads == 0u ||
+        a->q_heads % a->kv_heads != 0u || a->page_tokens == 0u)
+        return hipErrorInvalidValue;
+    if (kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_BF16) return hipErrorInvalidValue;
+    const DecodeSplit s = choose_decode_split(a->rows, a->kv_heads, a->q_heads, a->head_dim,
+                                              kv_dtype == PSK_KV_FP8_E4M3 ? 1u : 2u, a->page_tokens,
+                                              max_visible_tokens, row_visible, partial_bytes);
+    *splits = s.splits;
+    *pages_per_split = s.pages_per_split;
+    return hipSuccess;
+}

@@ -10,9 +10,11 @@
 #include <phaseshift_kv/dispatch.h>
 
 #include <algorithm>
+#include <functional>
 #include <vector>
 
 namespace psk {
+size_t decode_workgroup_lds_bytes(int kvb, uint32_t head_dim);
 hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
                               const void* v, const float* ks, const float* vs,
                               const uint32_t* tile_begin, const uint32_t* tile_rows,
@@ -43,27 +45,109 @@ PagedAttentionCommonArgs region_args(const PagedAttentionCommonArgs& c, uint32_t
 
 }  // namespace
 
+namespace {
+
+// MI355X geometry the chooser models: workgroups are dealt round-robin to 8
+// XCDs (block b runs on XCD b mod 8), each with multiProcessorCount/8 CUs.
+constexpr uint32_t kXcds = 8;
+
+uint32_t device_cus() {
+    static const uint32_t cus = [] {
+        int dev = 0;
+        hipDeviceProp_t prop{};
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess ||
+            prop.multiProcessorCount <= 0) {
+            (void)hipGetLastError();
+            return 256u;   // MI355X
+        }
+        return static_cast<uint32_t>(prop.multiProcessorCount);
+    }();
+    return cus;
+}
+
+// Makespan of the decode kernel's units (dense, longest first, unit u on XCD
+// u mod 8) under greedy dispatch onto `slots` workgroup slots per XCD, in
+// pages of work; every unit also pays `c0` pages of start-up.
+double split_makespan(const std::vector<uint32_t>& units, uint32_t slots, double c0) {
+    double worst = 0.0;
+    std::vector<double> free_at;
+    for (uint32_t x = 0; x < kXcds; ++x) {
+        free_at.assign(slots, 0.0);
+        std::make_heap(free_at.begin(), free_at.end(), std::greater<double>());
+        for (size_t i = x; i < units.size(); i += kXcds) {
+            std::pop_heap(free_at.begin(), free_at.end(), std::greater<double>());
+            free_at.back() += units[i] + c0;
+            std::push_heap(free_at.begin(), free_at.end(), std::greater<double>());
+        }
+        for (double t : free_at) worst = std::max(worst, t);
+    }
+    return worst;
+}
+
+}  // namespace
+
 DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_heads,
-                                uint32_t page_tokens, uint32_t max_visible_tokens,
+                                uint32_t head_dim, uint32_t kv_bytes, uint32_t page_tokens,
+                                uint32_t max_visible_tokens, const uint32_t* row_visible,
                                 uint64_t partial_bytes) {
-    DecodeSplit s;
-    if (max_visible_tokens < kSplitMinVisible || rows == 0 || kv_heads == 0) return s;
-    const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
-    const uint64_t work = (uint64_t)rows * kv_heads * max_pages;   // page-heads, upper bound
-    uint64_t per = std::max<uint64_t>(kMinPagesPerSplit, (work + kTargetWorkgroups - 1) / kTargetWorkgroups);
+    DecodeSplit best;
+    if (max_visible_tokens < kSplitMinVisible || rows == 0 || kv_heads == 0 || page_tokens == 0)
+        return best;
+    const uint32_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
+    std::vector<uint32_t> pages(rows, max_pages);
+    if (row_visible != nullptr)
+        for (uint32_t r = 0; r < rows; ++r)
+            pages[r] = std::min(max_pages, (row_visible[r] + page_tokens - 1) / page_tokens);
     const uint32_t q_per_kv = q_heads / kv_heads;
-    for (;;) {
-        const uint64_t splits = (max_pages + per - 1) / per;
+    const uint32_t groups = (kv_heads + 3u) / 4u;   // independent-wave workgroups per unit
+    const size_t lds = psk::decode_workgroup_lds_bytes(kv_bytes == 1 ? 1 : 2, head_dim);
+    const uint32_t per_cu = std::max<uint32_t>(1u, (uint32_t)((160u * 1024u) / lds));
+    const uint32_t slots = std::max<uint32_t>(1u, device_cus() / kXcds) * per_cu;
+    const uint64_t total_slots = (uint64_t)slots * kXcds;
+    // Start-up of a workgroup (unit scan, block-table window, first chunk
+    // latency, epilogue), fitted on MI355X: ~8 pages of FP8 hd256 x 4 heads.
+    const double page_bytes = 4.0 * page_tokens * (head_dim * (double)kv_bytes + (kv_bytes == 1 ? 8 : 0));
+    const double c0 = 8.0 * 16 * 4 * (256 + 8) / page_bytes;
+    // Candidates (predicted makespan, splits, pages per split); splits == 1
+    // competes when the rows alone fill every slot (it saves the combine pass,
+    // ~2%).
+    struct Cand { double t; uint32_t splits, per; };
+    std::vector<Cand> cands;
+    std::vector<uint32_t> units;
+    if ((uint64_t)rows * groups >= total_slots) {
+        for (uint32_t r = 0; r < rows; ++r)
+            for (uint32_t k = 0; k < groups; ++k) units.push_back(pages[r]);
+        std::sort(units.begin(), units.end(), std::greater<uint32_t>());
+        cands.push_back({split_makespan(units, slots, c0) / 1.02, 1u, 0u});
+    }
+    for (uint32_t splits = 2; splits <= std::min<uint32_t>(kMaxSplits, max_pages); ++splits) {
+        const uint32_t per = (max_pages + splits - 1) / splits;
+        if (per < kMinPagesPerSplit) break;
+        if ((max_pages + per - 1) / per != splits) continue;   // same as a smaller count
         const uint64_t need = (uint64_t)rows * kv_heads * splits * q_per_kv *
                               (2u + ::ps::kernel::kPagedAttentionHeadLimit) * sizeof(float);
-        if (splits <= 1) return s;
-        if (splits <= kMaxSplits && need <= partial_bytes) {
-            s.splits = static_cast<uint32_t>(splits);
-            s.pages_per_split = static_cast<uint32_t>(per);
-            return s;
+        if (need > partial_bytes) break;
+        uint64_t n_units = 0;
+        for (uint32_t r = 0; r < rows; ++r) n_units += (pages[r] + per - 1) / per;
+        if (n_units * groups > 8 * total_slots) break;   // finer splits only add start-ups
+        units.clear();
+        for (uint32_t r = 0; r < rows; ++r)     // full splits first, then every row's last
+            for (uint32_t s = 0; s + 1 < (pages[r] + per - 1) / per; ++s)
+                for (uint32_t k = 0; k < groups; ++k) units.push_back(per);
+        for (uint32_t r = 0; r < rows; ++r) {
+            const uint32_t n = (pages[r] + per - 1) / per;
+            if (n == 0) continue;
+            for (uint32_t k = 0; k < groups; ++k) units.push_back(pages[r] - (n - 1) * per);
         }
-        per *= 2;
+        cands.push_back({split_makespan(units, slots, c0), splits, per});
     }
+    if (cands.empty()) return best;
+    const Cand* pick = &cands[0];
+    for (const Cand& c : cands)
+        if (c.t < pick->t) pick = &c;
+    best.splits = pick->splits;
+    best.pages_per_split = pick->per;
+    return best;
 }
 
 namespace {
@@ -115,8 +199,9 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         k.kind = PlannedKernel::Kind::Decode;
         k.row_begin = row_begin;
         k.rows = rows;
-        const DecodeSplit s = choose_decode_split(rows, c.kv_heads, c.q_heads, c.page_tokens,
-                                                  step.max_visible_tokens, pbytes);
+        const DecodeSplit s = choose_decode_split(
+            rows, c.kv_heads, c.q_heads, c.head_dim, step.kv_dtype == KVCacheDType::FP8_E4M3 ? 1u : 2u,
+            c.page_tokens, step.max_visible_tokens, nullptr, pbytes);
         k.splits = s.splits;
         k.pages_per_split = s.pages_per_split;
         return push(k);

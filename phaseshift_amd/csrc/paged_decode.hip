@@ -67,9 +67,6 @@ __device__ __forceinline__ bf16x8 load_q8(const uint16_t* q, bool ok) {
 template <int KVB>
 constexpr int chunk_halves() { return KVB == 1 ? 2 : 1; }   // 16-token halves per chunk
 
-template <int KVB, int D>
-constexpr int v_row_bytes() { return D * KVB + 16; }   // padded LDS row of one V token
-
 typedef __attribute__((ext_vector_type(2))) int i32x2;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
@@ -86,14 +83,150 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const uint8_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
 }
 
-template <int KVB, int D, bool kAl16>
-__global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeParams p) {
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// Global memory straight into LDS (gfx950 LDS DMA, global_load_lds_dword /
+// _dwordx4): lane l of the wave writes LDS[dst + BYTES*l]. `dst` must be
+// wave-uniform. The hardware counts these loads in vmcnt and writes LDS
+// asynchronously: the wave reads the data only after s_waitcnt vmcnt.
+template <int BYTES>
+__device__ __forceinline__ void load_lds(const void* src, uint8_t* dst) {
+    static_assert(BYTES == 4 || BYTES == 16, "DMA width");
+    if constexpr (BYTES == 16)
+        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 16, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 4, 0, 0);
+}
+
+// Waits until at most N vector-memory operations of this wave are
+// outstanding. The memory clobber keeps every load and LDS access on its side.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Units of work of one row: splits that hold pages, 0 for a row the kernel
+// skips (invalid slot, position past the block table).
+__device__ __forceinline__ uint32_t row_units(const psk_paged_attention_args& a, uint32_t splits,
+                                              uint32_t pps, uint32_t r) {
+    if (a.row_sequence_slots[r] >= a.max_sequences) return 0u;
+    const uint64_t vis = (uint64_t)a.row_positions[r] + 1u;
+    if (vis > (uint64_t)a.block_table_stride * a.page_tokens || vis > 0xFFFFFFFFull) return 0u;
+    const uint32_t pc = ((uint32_t)vis + a.page_tokens - 1u) / a.page_tokens;
+    const uint32_t per = split_pages(pc, splits, pps);
+    return min(splits, (pc + per - 1u) / per);
+}
+
+// Exclusive scan of two counters over the NW waves of the workgroup.
+template <int NW>
+__device__ __forceinline__ void block_scan2(uint32_t& x, uint32_t& y, uint32_t& tx, uint32_t& ty,
+                                            uint32_t* tmp /* 2*NW */) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t ix = x, iy = y;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t ux = __shfl_up(ix, o, 64), uy = __shfl_up(iy, o, 64);
+        if (lane >= (uint32_t)o) { ix += ux; iy += uy; }
+    }
+    if (lane == 63u) { tmp[wave] = ix; tmp[NW + wave] = iy; }
+    __syncthreads();
+    uint32_t bx = 0, by = 0;
+    tx = 0; ty = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        if ((uint32_t)w < wave) { bx += tmp[w]; by += tmp[NW + w]; }
+        tx += tmp[w];
+        ty += tmp[NW + w];
+    }
+    x = bx + ix - x;
+    y = by + iy - y;
+}
+
+// Maps a dense unit index to (row, split). Units are ordered so that the
+// workgroups of one launch spread evenly over the XCDs (block b runs on XCD
+// b mod 8) and the longest go first: every row's splits but the last
+// (row-major), then the last split of every row. Returns false past the last
+// unit. All NW*64 threads of the workgroup must call it.
+template <int NW>
+__device__ bool find_unit(const psk_paged_attention_args& a, uint32_t splits, uint32_t pps,
+                          uint32_t unit, uint32_t& row, uint32_t& split) {
+    __shared__ uint32_t tmp[2 * NW];
+    __shared__ uint32_t found[2];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t R = a.rows;
+    const uint32_t each = (R + NW * 64u - 1u) / (NW * 64u);
+    const uint32_t r0 = min(R, tid * each), r1 = min(R, r0 + each);
+    uint32_t nf = 0, nl = 0;   // this thread's non-last and last units
+    for (uint32_t r = r0; r < r1; ++r) {
+        const uint32_t u = row_units(a, splits, pps, r);
+        if (u != 0u) { nf += u - 1u; nl += 1u; }
+    }
+    if (tid == 0) found[0] = 0xFFFFFFFFu;
+    uint32_t pf = nf, pl = nl, F, L;
+    block_scan2<NW>(pf, pl, F, L, tmp);
+    if (unit < F) {
+        if (unit >= pf && unit < pf + nf) {
+            uint32_t k = unit - pf;
+            for (uint32_t r = r0; r < r1; ++r) {
+                const uint32_t u = row_units(a, splits, pps, r);
+                if (u > 1u) {
+                    if (k < u - 1u) { found[0] = r; found[1] = k; break; }
+                    k -= u - 1u;
+                }
+            }
+        }
+    } else if (unit - F < L) {
+        const uint32_t k0 = unit - F;
+        if (k0 >= pl && k0 < pl + nl) {
+            uint32_t k = k0 - pl;
+            for (uint32_t r = r0; r < r1; ++r) {
+                const uint32_t u = row_units(a, splits, pps, r);
+                if (u != 0u) {
+                    if (k == 0u) { found[0] = r; found[1] = u - 1u; break; }
+                    --k;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    row = found[0];
+    split = found[1];
+    return row != 0xFFFFFFFFu;
+}
+
+constexpr uint32_t kPageWindow = 1024;   // block-table entries staged in LDS per pass
+
+// LDS bytes of one pipeline stage of one wave: K and V of a chunk (lane-major
+// DMA layout) and, FP8, the k/v scales of its tokens.
+template <int KVB, int D>
+constexpr int stage_bytes() {
+    return 2 * chunk_halves<KVB>() * 16 * D * KVB + (KVB == 1 ? 2 * chunk_halves<KVB>() * 256 : 0);
+}
+
+// kIndep: the 4 waves of a workgroup are 4 independent items, the kv heads
+// 4*kv_group + w of one (row, split); they stream the same tokens (adjacent
+// head slices of each token row) and need no merge. Otherwise the 4 waves
+// share one (row, kv_head, split) item, take its chunks round robin and merge
+// through LDS at the end (used when the independent grid cannot fill the GPU).
+template <int KVB, int D, bool kIndep, int NW>
+__global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParams p) {
+    constexpr uint32_t NT = NW * 64;   // threads of the workgroup
+    static_assert(kIndep || NW == kWaves, "the shared-item merge uses 4 waves");
     constexpr int H = chunk_halves<KVB>();
-    constexpr int CT = 16 * H;         // tokens per wave iteration
+    constexpr int CT = 16 * H;         // tokens per chunk
     constexpr int NL = D * KVB / 64;   // 16 B loads per lane per 16-token half
     constexpr int NS = D / 32;         // MFMA K-steps of the score product
     constexpr int NDB = D / 16;        // 16-dim blocks of the output
-    constexpr int VROW = v_row_bytes<KVB, D>();
+    constexpr int HALF_BYTES = 16 * D * KVB;
+    constexpr int KV_BYTES = H * HALF_BYTES;               // K (or V) of one chunk
+    constexpr int SC_BYTES = KVB == 1 ? H * 256 : 0;       // k (or v) scales of one chunk
+    constexpr int STAGE = stage_bytes<KVB, D>();
+    constexpr int kWinBytes = (int)kPageWindow * 4;
+    // vector-memory operations of one issue(): K and V DMAs and the scale DMAs
+    constexpr int kStepOps = H * (2 * NL + (KVB == 1 ? 2 : 0));
+    constexpr uint32_t kStride = kIndep ? CT : NW * CT;   // a wave's chunk stride
     static_assert(NL >= 1 && NS >= 1, "head_dim too small for this kernel");
 
     extern __shared__ __align__(16) uint8_t lds[];
@@ -107,41 +240,37 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
     const uint32_t g = lane >> 4;    // lane group
 
     const uint32_t splits = p.splits;
-    const uint32_t split = blockIdx.x % splits;
-    const uint32_t rest = blockIdx.x / splits;
-    const uint32_t kv_head = rest % a.kv_heads;
-    const uint32_t row = rest / a.kv_heads;
-    if (row >= a.rows) return;
-
+    // blockIdx = unit * G + sub: G independent kv-head groups or G kv heads
+    const uint32_t G = kIndep ? (a.kv_heads + NW - 1u) / NW : a.kv_heads;
+    const uint32_t sub = blockIdx.x % G;
+    uint32_t row, split;
+    if (!find_unit<NW>(a, splits, p.pages_per_split, blockIdx.x / G, row, split)) return;
+    const uint32_t kv_head = kIndep ? sub * NW + wave : sub;
     const uint32_t slot = a.row_sequence_slots[row];
-    if (slot >= a.max_sequences) return;
-    const uint64_t vis64 = (uint64_t)a.row_positions[row] + 1u;
-    if (vis64 > (uint64_t)a.block_table_stride * a.page_tokens) return;
-    const uint32_t visible = (uint32_t)vis64;
+    const uint32_t visible = a.row_positions[row] + 1u;
     const uint32_t P = a.page_tokens;
     const uint32_t pc = (visible + P - 1u) / P;
     const uint32_t per = split_pages(pc, splits, p.pages_per_split);
     const uint32_t pb = split * per;
-    if (pb >= pc) return;   // empty split: the reduce never reads it
     const uint32_t pe = (split == splits - 1u) ? pc : min(pc, pb + per);
-    const uint32_t t_begin = pb * P;
     const uint32_t t_end = min(pe * P, visible);
     const uint32_t* bt = a.block_tables + (uint64_t)slot * a.block_table_stride;
-    // With page_tokens a multiple of 16, every 16-token half of a chunk lies in
-    // one page (chunks start page-aligned), so one table lookup serves it.
-    constexpr bool al16 = kAl16;   // launcher guarantees (P & 15) == 0
+    // Everything above is uniform over the workgroup (row, split), so every
+    // wave reaches the barriers below; an independent wave past the last kv
+    // head only helps stage the block table.
+    const bool active = kv_head < a.kv_heads;
+    const uint32_t kvh = active ? kv_head : 0u;
 
     const uint32_t qpk = a.q_heads / a.kv_heads;
-    if (tid == 0) bad_shared = 0u;
-    __syncthreads();
+    if (!kIndep && tid == 0) bad_shared = 0u;
 
     // Q fragments: lane (n, g) holds head n, the dims that lane group g covers
-    // in each K-step (the same dims the K loads below put in that lane).
+    // in each K-step (the dims the K DMA below puts in that lane's 16 bytes).
     bf16x8 qf[NS];
     {
         const bool hv = n < qpk;
         const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + (uint64_t)row * a.q_row_stride +
-                               (uint64_t)(kv_head * qpk + (hv ? n : 0u)) * D;
+                               (uint64_t)(kvh * qpk + (hv ? n : 0u)) * D;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const int d0 = KVB == 2 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
@@ -151,50 +280,25 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
 
     const uint64_t layer_base = (uint64_t)a.layer * a.elems_per_layer;
     const uint64_t scale_layer = (uint64_t)a.layer * a.num_pages;
-    uint8_t* vt = lds + (size_t)wave * CT * VROW;
+    uint32_t* const win = reinterpret_cast<uint32_t*>(lds);
+    uint8_t* const stage0 = lds + kWinBytes + (size_t)wave * 2 * STAGE;
+    uint8_t* const stage1 = stage0 + STAGE;
     bool bad = false;
 
-    // Page id of half hf of the chunk at cb (al16 geometry), or invalid when the
-    // half starts past the split's range.
-    auto half_page = [&](uint32_t cb, int hf) -> uint32_t {
-        const uint32_t hb = cb + hf * 16;
-        return (al16 && hb < t_end) ? bt[hb / P] : 0xFFFFFFFFu;
-    };
-
-    // Issues the K/V loads of the chunk at `cb`: lane owns token n of each
-    // half, and (FP8) that token's k/v scales.
-    auto load_chunk = [&](uint32_t cb, const uint32_t (&pgs)[H], u32x4 (&kr)[H][NL],
-                          u32x4 (&vr)[H][NL], float (&ksl)[H], float (&vsl)[H]) {
-#pragma unroll
-        for (int hf = 0; hf < H; ++hf) {
-            const uint32_t tau = cb + hf * 16 + n;
-            bool ok = tau < t_end;
-            const uint32_t page = al16 ? pgs[hf] : (ok ? bt[tau / P] : 0xFFFFFFFFu);
-            if (ok && page >= a.num_pages) {
-                bad = true;
-                ok = false;
-            }
-            const uint32_t off = tau % P;
-            const uint64_t elem = ok ? layer_base + (uint64_t)page * a.elems_per_page +
-                                           (uint64_t)off * a.elems_per_token + (uint64_t)kv_head * D
-                                     : 0;
-            const uint8_t* kb = p.k_pool + elem * KVB + g * 16;
-            const uint8_t* vb = p.v_pool + elem * KVB + g * 16;
-#pragma unroll
-            for (int i = 0; i < NL; ++i) {
-                kr[hf][i] = ok ? *reinterpret_cast<const u32x4*>(kb + i * 64) : (u32x4){0u, 0u, 0u, 0u};
-                vr[hf][i] = ok ? *reinterpret_cast<const u32x4*>(vb + i * 64) : (u32x4){0u, 0u, 0u, 0u};
-            }
-            if constexpr (KVB == 1) {
-                const uint64_t si = ok ? ((scale_layer + page) * P + off) * a.kv_heads + kv_head : 0;
-                ksl[hf] = ok ? p.k_scale[si] : 0.0f;
-                vsl[hf] = ok ? p.v_scale[si] : 0.0f;
-            } else {
-                ksl[hf] = 1.0f;
-                vsl[hf] = 1.0f;
-            }
-        }
-    };
+    // tr-read address of this lane inside the V part of a stage; output block
+    // db adds 256*KVB*db. Lane r of a 16-lane block names row r of the
+    // transpose:
+    //   FP8:  token (r>>1 < 4 ? 4g + (r>>1) : 16 + 4g + (r>>1) - 4), dims +8*(r&1)
+    //   BF16: token 4g + (r>>2), dims +4*(r&3)
+    // In the DMA layout byte b of token t (half t/16) sits at
+    // (t/16)*HALF_BYTES + 1024*(b/64) + 16*(16*((b%64)/16) + t%16) + b%16.
+    uint32_t tr_off;
+    if constexpr (KVB == 1) {
+        const uint32_t j = n >> 1;
+        tr_off = (j < 4u ? 0u : (uint32_t)HALF_BYTES) + 16u * (4u * g + (j & 3u)) + 8u * (n & 1u);
+    } else {
+        tr_off = 16u * (4u * g + (n >> 2)) + 256u * ((n >> 1) & 1u) + 8u * (n & 1u);
+    }
 
     float m_run = -INFINITY;   // running max (log2 units), head n
     float l_run = 0.0f;        // partial softmax sum of this lane's tokens
@@ -202,210 +306,271 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_kernel(const DecodeP
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    constexpr uint32_t kStep = kWaves * CT;   // a wave's stride between chunks
-    u32x4 kr[H][NL], vr[H][NL];
-    float ksl[H], vsl[H];
-    uint32_t pg_next[H];
-    uint32_t cbase = t_begin + wave * CT;
-    {
-        uint32_t pg0[H];
-#pragma unroll
-        for (int hf = 0; hf < H; ++hf) {
-            pg0[hf] = half_page(cbase, hf);
-            pg_next[hf] = half_page(cbase + kStep, hf);
-        }
-        if (cbase < t_end) load_chunk(cbase, pg0, kr, vr, ksl, vsl);
-    }
+    // One pass per window of kPageWindow pages (a single pass unless the
+    // split holds more pages than that).
+    for (uint32_t wp = pb; wp < pe; wp += kPageWindow) {
+        const uint32_t wp_end = min(pe, wp + kPageWindow);
+        __syncthreads();
+        for (uint32_t i = tid; i < wp_end - wp; i += NT) win[i] = bt[wp + i];
+        __syncthreads();
+        const uint32_t ts = wp * P;
+        const uint32_t te = min(wp_end * P, t_end);
+        const uint32_t t_last = te - 1u;
+        uint32_t cb = ts + (kIndep ? 0u : wave * CT);
+        if (!active || cb >= te) continue;
 
-    // tr-read address of this lane inside the V tile (dim offset added per block)
-    uint32_t tr_off;
-    if constexpr (KVB == 1) {
-        const uint32_t j = n >> 1;
-        const uint32_t tok = j < 4u ? 4u * g + j : 16u + 4u * g + (j - 4u);
-        tr_off = tok * VROW + 8u * (n & 1u);
-    } else {
-        tr_off = (4u * g + (n >> 2)) * VROW + 8u * (n & 3u);
-    }
-
-    for (; cbase < t_end; cbase += kStep) {
-        // ---- V of this chunk into the wave's LDS tile, natural layout
+        // Issues the DMAs of the chunk at c into stage `st`: load i of half
+        // hf of K (V) at +hf*HALF_BYTES + 1024*i, lane (n, g) at +16*(16g + n)
+        // holding bytes [64i + 16g, +16) of token n; the scales of token n at
+        // +4*(16g + n) of each 256 B scale block. Loads are branch-free:
+        // tokens past the range read the last token (their scores are
+        // masked), so every issue() has exactly kStepOps operations.
+        auto issue = [&](uint32_t c, uint8_t* st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int hf = 0; hf < H; ++hf)
+            for (int hf = 0; hf < H; ++hf) {
+                const uint32_t tau = min(c + (uint32_t)hf * 16u + n, t_last);
+                uint32_t page = win[tau / P - wp];
+                const bool inv = page >= a.num_pages;
+                bad |= inv;
+                page = inv ? 0u : page;
+                const uint32_t off = tau % P;
+                const uint64_t elem = layer_base + (uint64_t)page * a.elems_per_page +
+                                      (uint64_t)off * a.elems_per_token + (uint64_t)kvh * D;
+                const uint8_t* ks = p.k_pool + elem * KVB + g * 16;
+                const uint8_t* vs = p.v_pool + elem * KVB + g * 16;
 #pragma unroll
-            for (int i = 0; i < NL; ++i)
-                *reinterpret_cast<u32x4*>(vt + (hf * 16 + n) * VROW + i * 64 + g * 16) = vr[hf][i];
-
-        // ---- page ids two chunks ahead, then the next chunk's loads
-        const uint32_t nbase = cbase + kStep;
-        uint32_t pg_after[H];
+                for (int i = 0; i < NL; ++i) load_lds<16>(ks + i * 64, st + hf * HALF_BYTES + i * 1024);
 #pragma unroll
-        for (int hf = 0; hf < H; ++hf) pg_after[hf] = half_page(nbase + kStep, hf);
-        u32x4 kn[H][NL];
-        float ksn[H], vsn[H];
-        if (nbase < t_end) load_chunk(nbase, pg_next, kn, vr, ksn, vsn);
-
-        // ---- scores S^T (token x head)
-        f32x4 sc[H];
-#pragma unroll
-        for (int hf = 0; hf < H; ++hf) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                bf16x8 kf;
-                if constexpr (KVB == 2) {
-                    kf = __builtin_bit_cast(bf16x8, kr[hf][s]);
-                } else {
-                    const u32x4 w = kr[hf][s >> 1];
-                    kf = (s & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
-                }
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
-            }
-            sc[hf] = acc;
-        }
-
-        // ---- online softmax (log2 units) for head n; the scales of the tokens
-        // this lane holds (4*g + r) come from the lanes that loaded them.
-        float s2[H][4], vsc[H][4];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int hf = 0; hf < H; ++hf)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t src = 4u * g + (uint32_t)r;
-                const bool ok = cbase + hf * 16 + src < t_end;
-                float f = p.scale_log2, vs = 1.0f;
+                for (int i = 0; i < NL; ++i)
+                    load_lds<16>(vs + i * 64, st + KV_BYTES + hf * HALF_BYTES + i * 1024);
                 if constexpr (KVB == 1) {
-                    f *= __shfl(ksl[hf], (int)src, 64);
-                    vs = __shfl(vsl[hf], (int)src, 64);
+                    const uint64_t si = ((scale_layer + page) * P + off) * a.kv_heads + kvh;
+                    load_lds<4>(p.k_scale + si, st + 2 * KV_BYTES + hf * 256);
+                    load_lds<4>(p.v_scale + si, st + 2 * KV_BYTES + SC_BYTES + hf * 256);
                 }
-                s2[hf][r] = ok ? sc[hf][r] * f : -INFINITY;
-                vsc[hf][r] = vs;
-                mx = __builtin_fmaxf(mx, s2[hf][r]);
             }
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = __builtin_fmaxf(m_run, mx);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float pv[H][4];
-        float psum = 0.0f;
-#pragma unroll
-        for (int hf = 0; hf < H; ++hf)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
-                psum += e;
-                pv[hf][r] = e * vsc[hf][r];
-            }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        // O is rescaled only when some head's running max moved.
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-        }
+        };
 
-        wave_lds_sync();
-        // ---- O^T += V^T * P^T
-        // P (with v_scale folded in) as hi + lo bf16 pairs: two MFMAs keep
-        // ~16 mantissa bits of every weight (V and K are exact in bf16).
-        if constexpr (KVB == 1) {
-            u32x4 ph, pl;
-            { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
-            { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
-            { const u32x2 t_ = split_bf16x2(pv[1][0], pv[1][1]); ph[2] = t_[0]; pl[2] = t_[1]; }
-            { const u32x2 t_ = split_bf16x2(pv[1][2], pv[1][3]); ph[3] = t_[0]; pl[3] = t_[1]; }
-            const bf16x8 pfh = __builtin_bit_cast(bf16x8, ph);
-            const bf16x8 pfl = __builtin_bit_cast(bf16x8, pl);
+        // Scores, online softmax and PV of the chunk at c held in stage st.
+        auto consume = [&](uint32_t c, const uint8_t* st) __attribute__((always_inline)) {
+            f32x4 sc[H];
 #pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                const i32x2 w = lds_read_tr8(vt + tr_off + 16 * db);
-                const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfh, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfl, o[db], 0, 0, 0);
+            for (int hf = 0; hf < H; ++hf) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                const uint8_t* kb = st + hf * HALF_BYTES + 16 * lane;
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    bf16x8 kf;
+                    if constexpr (KVB == 2) {
+                        kf = *reinterpret_cast<const bf16x8*>(kb + 1024 * s);
+                    } else {
+                        const u32x4 w = *reinterpret_cast<const u32x4*>(kb + 1024 * (s >> 1));
+                        kf = (s & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
+                    }
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
+                }
+                sc[hf] = acc;
             }
+
+            // online softmax (log2 units) for head n over tokens 4g + r
+            float s2[H][4], vsc[H][4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int hf = 0; hf < H; ++hf) {
+                f32x4 kscale = {1.f, 1.f, 1.f, 1.f}, vscale = {1.f, 1.f, 1.f, 1.f};
+                if constexpr (KVB == 1) {
+                    kscale = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + hf * 256 + 16 * g);
+                    vscale = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + SC_BYTES + hf * 256 +
+                                                             16 * g);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool ok = c + hf * 16 + 4u * g + (uint32_t)r < te;
+                    s2[hf][r] = ok ? sc[hf][r] * (p.scale_log2 * kscale[r]) : -INFINITY;
+                    vsc[hf][r] = vscale[r];
+                    mx = __builtin_fmaxf(mx, s2[hf][r]);
+                }
+            }
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = __builtin_fmaxf(m_run, mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+            float pv[H][4];
+            float psum = 0.0f;
+#pragma unroll
+            for (int hf = 0; hf < H; ++hf)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
+                    psum += e;
+                    pv[hf][r] = e * vsc[hf][r];
+                }
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+            // O is rescaled only when some head's running max moved.
+            if (__any(alpha != 1.0f)) {
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+            }
+
+            // O^T += V^T * P^T. P (v_scale folded in) as hi + lo bf16 pairs:
+            // two MFMAs keep ~16 mantissa bits of every weight (V and K are
+            // exact in bf16).
+            const uint8_t* vb = st + KV_BYTES + tr_off;
+            if constexpr (KVB == 1) {
+                u32x4 ph, pl;
+                { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
+                { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
+                { const u32x2 t_ = split_bf16x2(pv[1][0], pv[1][1]); ph[2] = t_[0]; pl[2] = t_[1]; }
+                { const u32x2 t_ = split_bf16x2(pv[1][2], pv[1][3]); ph[3] = t_[0]; pl[3] = t_[1]; }
+                const bf16x8 pfh = __builtin_bit_cast(bf16x8, ph);
+                const bf16x8 pfl = __builtin_bit_cast(bf16x8, pl);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const i32x2 w = lds_read_tr8(vb + 256 * db);
+                    const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfh, o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfl, o[db], 0, 0, 0);
+                }
+            } else {
+                u32x2 ph, pl;
+                { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
+                { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
+                const i16x4 pfh = __builtin_bit_cast(i16x4, ph);
+                const i16x4 pfl = __builtin_bit_cast(i16x4, pl);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const i16x4 vf = lds_read_tr16(vb + 512 * db);
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pfh, o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pfl, o[db], 0, 0, 0);
+                }
+            }
+        };
+
+        // One pipeline step: the DMAs of the next chunk go out before the
+        // wait for chunk c, so the wave keeps two chunks in flight while it
+        // computes. The __restrict__ parameters tell the compiler that the
+        // DMA into `next` and the reads of `cur` touch different LDS; the
+        // ordering between a DMA and the later reads of its stage is the
+        // explicit wait_vmcnt, which leaves exactly the kStepOps operations
+        // of this step's issue() outstanding.
+        auto step = [&](uint32_t c, uint8_t* __restrict__ next,
+                        const uint8_t* __restrict__ cur) __attribute__((always_inline)) {
+            issue(c + kStride, next);
+            wait_vmcnt<kStepOps>();
+            consume(c, cur);
+        };
+
+        issue(cb, stage0);
+        for (;;) {
+            step(cb, stage1, stage0);
+            cb += kStride;
+            if (cb >= te) break;
+            step(cb, stage0, stage1);
+            cb += kStride;
+            if (cb >= te) break;
+        }
+        // The last step issued a chunk nobody reads: its DMAs must land
+        // before the stages are reused.
+        wait_vmcnt<0>();
+    }
+
+    const uint32_t q0 = kvh * qpk;
+    if constexpr (kIndep) {
+        if (!active) return;
+        const float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+        const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
+        if (n >= qpk) return;
+        if (p.partials == nullptr) {
+            // An invalid page leaves this row's output unwritten.
+            if (bad) return;
+            const float inv_l = 1.0f / l_all;
+            const uint64_t ob = (uint64_t)row * a.output_row_stride + (uint64_t)(q0 + n) * D + 4u * g;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float res = o[db][r] * inv_l;
+                    if (a.output_dtype == PSK_OUT_F32)
+                        static_cast<float*>(a.output)[ob + 16 * db + r] = res;
+                    else
+                        static_cast<uint16_t*>(a.output)[ob + 16 * db + r] = f32_to_bf16_bits(res);
+                }
         } else {
-            u32x2 ph, pl;
-            { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
-            { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
-            const i16x4 pfh = __builtin_bit_cast(i16x4, ph);
-            const i16x4 pfl = __builtin_bit_cast(i16x4, pl);
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                const i16x4 vf = lds_read_tr16(vt + tr_off + 32 * db);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pfh, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pfl, o[db], 0, 0, 0);
+            float* part = p.partials + ((uint64_t)(row * a.kv_heads + kvh) * splits + split) *
+                                           (uint64_t)(qpk * (2u + kPagedAttentionHeadLimit));
+            if (g == 0) {
+                // NaN marks a split that met an invalid page; the reduce then
+                // leaves the row unwritten.
+                part[n] = bad ? __builtin_nanf("") : m_run * 0.69314718055994531f;
+                part[qpk + n] = l_all;
             }
+            float* A = part + 2u * qpk + n * kPagedAttentionHeadLimit + 4u * g;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) A[16 * db + r] = o[db][r];
         }
-        wave_lds_sync();
-
-#pragma unroll
-        for (int hf = 0; hf < H; ++hf) {
-            pg_next[hf] = pg_after[hf];
-            ksl[hf] = ksn[hf];
-            vsl[hf] = vsn[hf];
-#pragma unroll
-            for (int i = 0; i < NL; ++i) kr[hf][i] = kn[hf][i];
-        }
-    }
-
-    // ---- merge the 4 waves: per wave m[16], l[16], O[qpk][D] in LDS
-    if (bad) bad_shared = 1u;
-    const float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-    const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
-    __syncthreads();
-    float* fm = reinterpret_cast<float*>(lds);
-    float* fl = fm + kWaves * 16;
-    float* fo = fl + kWaves * 16;   // [wave][qpk][D]
-    if (g == 0) {
-        fm[wave * 16 + n] = m_run;
-        fl[wave * 16 + n] = l_all;
-    }
-    if (n < qpk) {
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                fo[((size_t)wave * qpk + n) * D + db * 16 + 4 * g + r] = o[db][r];
-    }
-    __syncthreads();
-
-    const uint32_t q0 = kv_head * qpk;
-    float* part = nullptr;
-    if (p.partials != nullptr)
-        part = p.partials + ((uint64_t)(row * a.kv_heads + kv_head) * splits + split) *
-                                (uint64_t)(qpk * (2u + kPagedAttentionHeadLimit));
-    if (bad_shared != 0u) {
-        // An invalid page leaves this row's output unwritten; the NaN marks
-        // the split for the reduce, which then writes nothing either.
-        if (part != nullptr && tid < qpk) part[tid] = __builtin_nanf("");
         return;
-    }
-    for (uint32_t idx = tid; idx < qpk * D; idx += kThreads) {
-        const uint32_t h = idx / D, d = idx % D;
-        float gm = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) gm = __builtin_fmaxf(gm, fm[w * 16 + h]);
-        float L = 0.0f, O = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float wt = __builtin_amdgcn_exp2f(fm[w * 16 + h] - gm);
-            L += wt * fl[w * 16 + h];
-            O += wt * fo[((size_t)w * qpk + h) * D + d];
+    } else {
+        // ---- merge the 4 waves: per wave m[16], l[16], O[qpk][D] in LDS
+        if (bad) bad_shared = 1u;
+        const float l_tot = l_run + __shfl_xor(l_run, 16, 64);
+        const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
+        __syncthreads();
+        float* fm = reinterpret_cast<float*>(lds);
+        float* fl = fm + kWaves * 16;
+        float* fo = fl + kWaves * 16;   // [wave][qpk][D]
+        if (g == 0) {
+            fm[wave * 16 + n] = m_run;
+            fl[wave * 16 + n] = l_all;
         }
-        if (part == nullptr) {
-            const uint64_t oi = (uint64_t)row * a.output_row_stride + (uint64_t)(q0 + h) * D + d;
-            const float res = O / L;
-            if (a.output_dtype == PSK_OUT_F32)
-                static_cast<float*>(a.output)[oi] = res;
-            else
-                static_cast<uint16_t*>(a.output)[oi] = f32_to_bf16_bits(res);
-        } else {
-            if (d == 0) {
-                part[h] = gm * 0.69314718055994531f;   // back to natural-log units
-                part[qpk + h] = L;
+        if (n < qpk) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    fo[((size_t)wave * qpk + n) * D + db * 16 + 4 * g + r] = o[db][r];
+        }
+        __syncthreads();
+
+        float* part = nullptr;
+        if (p.partials != nullptr)
+            part = p.partials + ((uint64_t)(row * a.kv_heads + kvh) * splits + split) *
+                                    (uint64_t)(qpk * (2u + kPagedAttentionHeadLimit));
+        if (bad_shared != 0u) {
+            // An invalid page leaves this row's output unwritten; the NaN marks
+            // the split for the reduce, which then writes nothing either.
+            if (part != nullptr && tid < qpk) part[tid] = __builtin_nanf("");
+            return;
+        }
+        for (uint32_t idx = tid; idx < qpk * D; idx += kThreads) {
+            const uint32_t h = idx / D, d = idx % D;
+            float gm = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) gm = __builtin_fmaxf(gm, fm[w * 16 + h]);
+            float L = 0.0f, O = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float wt = __builtin_amdgcn_exp2f(fm[w * 16 + h] - gm);
+                L += wt * fl[w * 16 + h];
+                O += wt * fo[((size_t)w * qpk + h) * D + d];
             }
-            part[2u * qpk + h * kPagedAttentionHeadLimit + d] = O;
+            if (part == nullptr) {
+                const uint64_t oi = (uint64_t)row * a.output_row_stride + (uint64_t)(q0 + h) * D + d;
+                const float res = O / L;
+                if (a.output_dtype == PSK_OUT_F32)
+                    static_cast<float*>(a.output)[oi] = res;
+                else
+                    static_cast<uint16_t*>(a.output)[oi] = f32_to_bf16_bits(res);
+            } else {
+                if (d == 0) {
+                    part[h] = gm * 0.69314718055994531f;   // back to natural-log units
+                    part[qpk + h] = L;
+                }
+                part[2u * qpk + h * kPagedAttentionHeadLimit + d] = O;
+            }
         }
     }
 }
@@ -508,30 +673,49 @@ bool mfma_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
     return true;
 }
 
-template <int KVB, int D, bool kAl16>
-hipError_t launch_decode_t2(const DecodeParams& p, hipStream_t stream) {
+}  // namespace
+
+// LDS bytes of one independent-wave decode workgroup (the split chooser
+// derives workgroups per CU from it).
+size_t decode_workgroup_lds_bytes(int kvb, uint32_t head_dim) {
+    const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
+    const size_t H = kvb == 1 ? 2 : 1;
+    const size_t stage = 2 * H * 16 * D * kvb + (kvb == 1 ? 2 * H * 256 : 0);
+    return (size_t)kPageWindow * 4 + (size_t)kWaves * 2 * stage;
+}
+
+namespace {
+
+template <int KVB, int D, bool kIndep, int NW>
+hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
-    const size_t v_bytes = (size_t)kWaves * 16 * chunk_halves<KVB>() * v_row_bytes<KVB, D>();
-    const size_t m_bytes = (size_t)kWaves * 32 * sizeof(float) + (size_t)kWaves * qpk * D * sizeof(float);
+    // block-table window + two pipeline stages per wave; the shared-item merge
+    // later reuses the same LDS
+    const size_t v_bytes = (size_t)kPageWindow * 4 + (size_t)NW * 2 * stage_bytes<KVB, D>();
+    const size_t m_bytes = kIndep ? 0 : (size_t)NW * 32 * sizeof(float) +
+                                            (size_t)NW * qpk * D * sizeof(float);
     const size_t lds_bytes = v_bytes > m_bytes ? v_bytes : m_bytes;
-    const uint64_t grid = (uint64_t)p.a.rows * p.a.kv_heads * p.splits;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_decode_kernel<KVB, D, kAl16>),
+            reinterpret_cast<const void*>(&paged_decode_kernel<KVB, D, kIndep, NW>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((paged_decode_kernel<KVB, D, kAl16>), dim3((uint32_t)grid), dim3(kThreads),
-                       lds_bytes, stream, p);
+    hipLaunchKernelGGL((paged_decode_kernel<KVB, D, kIndep, NW>), dim3((uint32_t)grid),
+                       dim3(NW * 64), lds_bytes, stream, p);
     return hipGetLastError();
 }
 
+// Independent waves (one kv head each) when that grid fills the GPU's 256
+// CUs; otherwise the 4 waves share each (row, kv_head, split) item.
 template <int KVB, int D>
 hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
-    return (p.a.page_tokens & 15u) == 0u ? launch_decode_t2<KVB, D, true>(p, stream)
-                                         : launch_decode_t2<KVB, D, false>(p, stream);
+    const uint64_t units = (uint64_t)p.a.rows * p.splits;
+    const uint64_t groups = (p.a.kv_heads + kWaves - 1u) / kWaves;
+    if (units * groups >= 256u) return launch_decode_t2<KVB, D, true, kWaves>(p, units * groups, stream);
+    return launch_decode_t2<KVB, D, false, kWaves>(p, units * p.a.kv_heads, stream);
 }
 
 template <int KVB>

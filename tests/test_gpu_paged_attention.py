@@ -190,3 +190,59 @@ def test_position_past_table_skips_row(dev):
     pos[1] = 16 * lay.block_tables.shape[1]     # visible = stride*P + 1 > capacity
     got = run_gpu(lay, 8, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
     assert np.all(got[1] == 7.0) and not np.all(got[0] == 7.0)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_unsplit_independent_waves(dev, fp8):
+    """>= 256 rows unsplit: the 4 waves of a workgroup are the 4 kv heads of one
+    row and each writes its heads' output straight from registers."""
+    rng = np.random.default_rng(71 + fp8)
+    lens = rng.integers(1, 200, 300)
+    _, lay, kp, vp, ks, vs, q, slots, pos = case(71 + fp8, lens, 24, 4, 256, 16, fp8, dev)
+    want = oracle_out(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
+    got = run_gpu(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
+    assert np.max(np.abs(got - want)) < TOL[fp8]
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_independent_waves_partial_head_group(dev, fp8):
+    """kv_heads = 6: the second group of each row has 2 of 4 waves active."""
+    rng = np.random.default_rng(81 + fp8)
+    lens = rng.integers(1, 90, 260)
+    _, lay, kp, vp, ks, vs, q, slots, pos = case(81 + fp8, lens, 12, 6, 64, 16, fp8, dev)
+    want = oracle_out(lay, 12, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
+    for splits, pps in ((1, 0), (3, 2)):
+        got = run_gpu(lay, 12, q, slots, pos, lay.block_tables, kp, vp, ks, vs, splits=splits,
+                      pages_per_split=pps)
+        assert np.max(np.abs(got - want)) < TOL[fp8], (splits, pps)
+
+
+def test_split_window_passes(dev):
+    """Splits of more than 1024 pages stage the block table in several passes."""
+    rng = np.random.default_rng(91)
+    lens = np.array([40000, 20000, 17000, 1500] * 64)[:256]
+    _, lay, kp, vp, ks, vs, q, slots, pos = case(91, lens[:4], 24, 4, 256, 16, True, dev)
+    # 4 distinct rows replicated: 256 rows share 4 block tables
+    bt = lay.block_tables
+    reps = 64
+    slots_r = np.tile(slots, reps)
+    pos_r = np.tile(pos, reps)
+    q_r = np.tile(q, (reps, 1))
+    ref = run_gpu(lay, 24, q_r[:4], slots_r[:4], pos_r[:4], bt, kp, vp, ks, vs, splits=1)
+    want = oracle_out(lay, 24, q[:4], slots[:4], pos[:4], bt, kp, vp, ks, vs)
+    assert np.max(np.abs(ref - want)) < TOL[True]
+    got = run_gpu(lay, 24, q_r, slots_r, pos_r, bt, kp, vp, ks, vs, splits=2, pages_per_split=1100)
+    assert np.max(np.abs(got - np.tile(ref, (reps, 1)))) < 1e-2
+
+
+def test_invalid_page_independent_split(dev):
+    """Invalid pages under the independent-wave split kernel (>= 256 units)."""
+    _, lay, kp, vp, ks, vs, q, slots, pos = case(14, [600] * 8, 24, 4, 256, 16, True, dev)
+    bt = lay.block_tables.copy()
+    bt[1, 20] = INVALID
+    bt[5, 3] = 1 << 30
+    got = run_gpu(lay, 24, q, slots, pos, bt, kp, vp, ks, vs, splits=38, pages_per_split=1)
+    assert np.all(got[1] == 7.0) and np.all(got[5] == 7.0)
+    keep = [0, 2, 3, 4, 6, 7]
+    want = oracle_out(lay, 24, q[keep], slots[keep], pos[keep], bt, kp, vp, ks, vs)
+    assert np.max(np.abs(got[keep] - want)) < 5e-2
