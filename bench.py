@@ -33,6 +33,9 @@ HBM_PEAK_GBPS = 8000.0
 BYTES_PER_TOKEN_FP8 = 2 * 4 * 256 + 2 * 4 * 4 + 4 / 16      # 2080.25
 BYTES_PER_TOKEN_BF16 = 2 * 4 * 256 * 2 + 4 / 16              # 4096.25
 APPEND_BYTES_PER_ROW_FP8 = 2 * 4 * 256 * 2 + 8 + 4 + 2 * 4 * 256 + 2 * 4 * 4   # 6188
+# HBM bytes per main-line decode launch measured with rocprofv3 --pmc on this
+# kernel (FETCH_SIZE 2,139,725 KiB x 2.0 calibration + WRITE_SIZE 6,208 KiB).
+DECODE_TRAFFIC_BYTES = 2139725 * 1024 * 2 + 6208 * 1024
 # Untimed warm-up runs at least `--warmup` steps and at least this long, so the
 # GPU clocks have ramped before a timed loop starts.
 WARM_MIN_S = 0.2
@@ -326,7 +329,10 @@ def main():
                        round(value / HBM_PEAK_GBPS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "paged_decode_kernel<1,256> (FP8 split)",
+                     "traffic": DECODE_TRAFFIC_BYTES,
+                     "traffic_source": "profiles/paged_decode_fp8_b64_ctx32k.md (rocprofv3 --pmc "
+                                       "FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per dispatch)",
+                     "kernel": "paged_decode_kernel<1,256> (FP8 split)",
                      "kernel_ms": round(k_ms, 5), "reduce_ms": round(r_ms, 5),
                      "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
