@@ -59,7 +59,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append")
+    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times), the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -214,6 +214,116 @@ def run_append(torch, ops, rows, steps, warmup, dev, seed=7):
     return ms, rows * APPEND_BYTES_PER_ROW_FP8
 
 
+def run_mixed_step(torch, ops, steps, warmup, dev):
+    """BASELINE config 5, one continuous-batching step on the device: row
+    metadata from the request descriptors, KV append (fused FP8 quantization) of
+    all 4272 rows, the planned PAGED_ATTENTION launches (48 decode rows, 8 verify
+    blocks of 16 causal drafts on the tile kernel, 8 prefill chunks of 512 rows
+    on the tile kernel) and the CoW restore of 32 prefix pages. Contexts
+    U[2k,16k], FP8 KV, 24/4 heads, hd 256, page 16. Rollback (page truncation)
+    changes the step's work, so it is timed once on its own."""
+    from phaseshift_amd import KV_FP8, state
+    rng = np.random.default_rng(5005)
+    QH, H, D, Pt = 24, 4, 256, 16
+    n_pre, n_dec, n_ver = 8, 48, 8
+    ctx = rng.integers(2048, 16385, n_pre + n_dec + n_ver)
+    max_len = int(ctx.max()) + 512 + 16
+    need_pages = int(sum(math.ceil((c + 512) / Pt) for c in ctx)) + 64
+    pool = state.KVPool(need_pages, Pt, 1, H, D, fp8=True)
+    cache = state.KVPool(64, Pt, 1, H, D, fp8=True)
+    slots = state.SlotPool(n_pre + n_dec + n_ver + 1, math.ceil(max_len / Pt))
+    g = pool.geom
+    T = pool.tensors(torch)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    for k in ("k", "v"):
+        T[k].copy_(torch.randint(0, 126, T[k].shape, generator=gen, device=dev,
+                                 dtype=torch.int32).to(torch.uint8))
+    for k in ("k_scale", "v_scale"):
+        T[k].copy_(torch.rand(T[k].shape, generator=gen, device=dev) * 0.02 + 1e-3)
+    seqs = [state.Sequence(slots, pool, max_len) for _ in range(len(ctx))]
+    for sq, c in zip(seqs, ctx):
+        sq.reserve(int(c))
+        sq.commit(int(c))
+    cache_pages = [cache.allocate() for _ in range(32)]
+    dst_pages = seqs[0].block_table()[:32]
+    reqs, descs, row = [], [], 0
+    layout = [(n_pre + i, 1, 0) for i in range(n_dec)] + \
+             [(n_pre + n_dec + i, 16, 1) for i in range(n_ver)] + [(i, 512, 2) for i in range(n_pre)]
+    visible = []
+    for si, cnt, cls in layout:
+        sq = seqs[si]
+        reqs.append((row, cnt, cls, sq.position + cnt))
+        descs.append(dict(slot=sq.slot, row_begin=row, row_count=cnt, prefix_length=sq.position,
+                          execution_class=cls))
+        visible += [sq.position + j + 1 for j in range(cnt)]
+        sq.reserve(cnt)
+        row += cnt
+    rows = row
+    raw = torch.from_numpy(np.frombuffer(ops.pack_requests(descs), np.uint8).copy()).to(dev)
+    rslots = torch.empty(rows, dtype=torch.int32, device=dev)
+    rpos = torch.empty(rows, dtype=torch.int32, device=dev)
+    bt = slots.block_tables(torch)
+    kin = torch.randn((rows, H * D), generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+    vin = torch.randn((rows, H * D), generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+    q = torch.randn((rows, QH * D), generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+    out = torch.empty((rows, QH * D), dtype=torch.bfloat16, device=dev)
+    a = ops.attention_args(g, 0, q, out, rslots, rpos, bt, QH)
+    part = torch.empty((256 << 20) // 4, dtype=torch.float32, device=dev)
+    maxvis = int(ctx.max()) + 512
+
+    def meta():
+        ops.prepare_row_metadata(raw, len(descs), rows, rslots, rpos)
+
+    def append():
+        ops.kv_append(g, 0, kin, vin, rslots, rpos, bt, T["k"], T["v"], T["k_scale"],
+                      T["v_scale"])
+
+    def attend():
+        return state.plan_step(a, KV_FP8, reqs, maxvis, part.numel() * 4, partials_ptr=part,
+                               k_pool=T["k"], v_pool=T["v"], k_scale=T["k_scale"],
+                               v_scale=T["v_scale"], launch=True)
+
+    def cow():
+        pool.copy_pages_from(cache, dst_pages, cache_pages)
+
+    def step():
+        meta()
+        append()
+        attend()
+        cow()
+
+    warm(torch, step, warmup)
+    plan = attend()
+    t = Timer(torch)
+    with t:
+        for _ in range(steps):
+            step()
+    step_ms = t.ms() / steps
+    parts = {}
+    for name, fn in (("append", append), ("attention", attend), ("cow_copy", cow)):
+        tt = Timer(torch)
+        with tt:
+            for _ in range(steps):
+                fn()
+        parts[name] = round(tt.ms() / steps, 4)
+    # rollback of the 8 verify blocks: keep a seeded accepted prefix of each
+    rb = Timer(torch)
+    with rb:
+        for i in range(n_ver):
+            sq = seqs[n_pre + n_dec + i]
+            keep = math.ceil((sq.position + int(rng.integers(0, 17))) / Pt)
+            sq.rollback(keep)
+    parts["rollback_8_blocks"] = round(rb.ms(), 4)
+    vis = np.asarray(visible, np.float64)
+    flops = float((vis * QH * D * 4).sum())
+    kinds = [(int(k.kind), int(k.rows), int(k.splits)) for k in plan.kernels[:plan.count]]
+    return dict(ms_per_step=round(step_ms, 4), rows=rows,
+                tokens_per_s=round(rows / (step_ms * 1e-3), 1), parts_ms=parts,
+                attention_tflops=round(flops / (parts["attention"] * 1e-3) / 1e12, 2),
+                attention_flops=flops, plan=kinds)
+
+
 def cpu_baseline(lens_row, seconds_cap=30.0):
     """Scalar C oracle (1 thread) on a bounded sample of the same workload:
     FP8 decode of whole rows at context 32768, until ~10 s of CPU work."""
@@ -263,7 +373,7 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 5}))
         return
-    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append"}
+    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5"}
     extra = {}
 
     # ---- main: north-star point, FP8 batch 64 @ 32k
@@ -307,6 +417,11 @@ def main():
                                       GBps=round(nb / (ms * 1e-3) / 1e9, 1),
                                       frac_of_peak=round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
         extra["kv_append_fp8"] = ap
+
+    if "cfg5" in only:
+        extra["cfg5_mixed_step"] = run_mixed_step(torch, ops, max(5, args.steps // 2),
+                                                  args.warmup, dev)
+        torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline(32768)
     line = {

@@ -33,6 +33,7 @@ struct StepRequest {
     uint32_t row_begin = 0;
     uint32_t row_count = 0;
     uint8_t execution_class = kExecDecode;
+    uint32_t max_visible = 0;   // largest visible length of its rows; 0: unknown
 };
 
 struct PagedAttentionStep {

@@ -325,6 +325,8 @@ typedef struct psk_step_request {
     uint32_t row_count;
     uint8_t execution_class;           /* 0 DECODE 1 SPEC_VERIFY 2 PREFILL 3 SPEC_DRAFT */
     uint8_t reserved[3];
+    uint32_t max_visible;              /* largest visible length of its rows (prefix + count);
+                                          0: unknown, the step's max_visible_tokens is used */
 } psk_step_request;
 
 typedef struct psk_planned_kernel {

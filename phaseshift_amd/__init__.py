@@ -76,7 +76,8 @@ class SequenceInfo(C.Structure):
 
 class StepRequest(C.Structure):
     _fields_ = [("row_begin", C.c_uint32), ("row_count", C.c_uint32),
-                ("execution_class", C.c_uint8), ("reserved", C.c_uint8 * 3)]
+                ("execution_class", C.c_uint8), ("reserved", C.c_uint8 * 3),
+                ("max_visible", C.c_uint32)]
 
 
 class PlannedKernel(C.Structure):

@@ -190,7 +190,8 @@ extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, 
     step.v_scale_pool = v_scale_pool;
     std::vector<StepRequest> reqs(num_requests);
     for (uint32_t i = 0; i < num_requests; ++i)
-        reqs[i] = {requests[i].row_begin, requests[i].row_count, requests[i].execution_class};
+        reqs[i] = {requests[i].row_begin, requests[i].row_count, requests[i].execution_class,
+                   requests[i].max_visible};
     step.requests = reqs.data();
     step.num_requests = num_requests;
     step.max_visible_tokens = max_visible_tokens;

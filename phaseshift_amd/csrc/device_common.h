@@ -107,6 +107,41 @@ __device__ __forceinline__ float wave_max(float x) {
     return x;
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+// Global memory straight into LDS (gfx950 LDS DMA, global_load_lds_dword /
+// _dwordx4): lane l of the wave writes LDS[dst + BYTES*l] (the instruction's
+// immediate offset would be added to both addresses; it is 0 here). `dst`
+// must be wave-uniform. The hardware counts these loads in vmcnt and writes
+// LDS asynchronously: the data may be read only after s_waitcnt vmcnt.
+template <int BYTES>
+__device__ __forceinline__ void load_lds(const void* src, uint8_t* dst) {
+    static_assert(BYTES == 4 || BYTES == 16, "DMA width");
+    if constexpr (BYTES == 16)
+        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 16, 0, 0);
+    else
+        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 4, 0, 0);
+}
+
+// Waits until at most N vector-memory operations of this wave are
+// outstanding. The memory clobber keeps every load and LDS access on its side.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// wait_vmcnt<N> followed by a workgroup barrier without memory fences (a
+// fenced __syncthreads would also wait for every outstanding load). After it,
+// every wave's LDS DMAs older than its last N vector-memory operations have
+// landed in LDS.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // Orders this wave's LDS writes before its later LDS reads by other lanes.
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

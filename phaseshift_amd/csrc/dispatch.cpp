@@ -15,6 +15,7 @@
 
 namespace psk {
 size_t decode_workgroup_lds_bytes(int kvb, uint32_t head_dim);
+uint32_t tile_workgroups_per_cu(int kvb, uint32_t head_dim, uint32_t q_per_kv);
 hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
                               const void* v, const float* ks, const float* vs,
                               const uint32_t* tile_begin, const uint32_t* tile_rows,
@@ -68,7 +69,7 @@ uint32_t device_cus() {
 // Makespan of the decode kernel's units (dense, longest first, unit u on XCD
 // u mod 8) under greedy dispatch onto `slots` workgroup slots per XCD, in
 // pages of work; every unit also pays `c0` pages of start-up.
-double split_makespan(const std::vector<uint32_t>& units, uint32_t slots, double c0) {
+double split_makespan(const std::vector<double>& units, uint32_t slots, double c0) {
     double worst = 0.0;
     std::vector<double> free_at;
     for (uint32_t x = 0; x < kXcds; ++x) {
@@ -113,11 +114,31 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
     // ~2%).
     struct Cand { double t; uint32_t splits, per; };
     std::vector<Cand> cands;
-    std::vector<uint32_t> units;
-    if ((uint64_t)rows * groups >= total_slots) {
+    std::vector<double> units;
+    // Units of one launch in dispatch order: every row's splits but the last,
+    // then every row's last split. At >= 128 workgroups each (row, split) is
+    // `groups` independent-wave workgroups; below that the decode launcher
+    // runs one 4-wave workgroup per (row, split, kv head), a quarter of the
+    // work each (in pages of 4 kv heads).
+    auto build = [&](uint32_t per, uint64_t n_units) {
+        units.clear();
+        const bool indep = n_units * groups >= 128;
+        const uint32_t copies = indep ? groups : kv_heads;
+        const double share = indep ? 1.0 : 0.25;
         for (uint32_t r = 0; r < rows; ++r)
-            for (uint32_t k = 0; k < groups; ++k) units.push_back(pages[r]);
-        std::sort(units.begin(), units.end(), std::greater<uint32_t>());
+            for (uint32_t s = 0; s + 1 < (pages[r] + per - 1) / per; ++s)
+                for (uint32_t k = 0; k < copies; ++k) units.push_back(per * share);
+        for (uint32_t r = 0; r < rows; ++r) {
+            const uint32_t n = (pages[r] + per - 1) / per;
+            if (n == 0) continue;
+            for (uint32_t k = 0; k < copies; ++k) units.push_back((pages[r] - (n - 1) * per) * share);
+        }
+    };
+    if ((uint64_t)rows * groups >= total_slots) {
+        // Enough rows to fill every slot unsplit: splitting must then win by
+        // more than the combine pass costs (~2%).
+        build(max_pages, rows);
+        std::sort(units.begin(), units.end(), std::greater<double>());
         cands.push_back({split_makespan(units, slots, c0) / 1.02, 1u, 0u});
     }
     for (uint32_t splits = 2; splits <= std::min<uint32_t>(kMaxSplits, max_pages); ++splits) {
@@ -130,15 +151,7 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
         uint64_t n_units = 0;
         for (uint32_t r = 0; r < rows; ++r) n_units += (pages[r] + per - 1) / per;
         if (n_units * groups > 8 * total_slots) break;   // finer splits only add start-ups
-        units.clear();
-        for (uint32_t r = 0; r < rows; ++r)     // full splits first, then every row's last
-            for (uint32_t s = 0; s + 1 < (pages[r] + per - 1) / per; ++s)
-                for (uint32_t k = 0; k < groups; ++k) units.push_back(per);
-        for (uint32_t r = 0; r < rows; ++r) {
-            const uint32_t n = (pages[r] + per - 1) / per;
-            if (n == 0) continue;
-            for (uint32_t k = 0; k < groups; ++k) units.push_back(pages[r] - (n - 1) * per);
-        }
+        build(per, n_units);
         cands.push_back({split_makespan(units, slots, c0), splits, per});
     }
     if (cands.empty()) return best;
@@ -152,27 +165,34 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
 
 namespace {
 
+// Tile launches: split only until the grid fills the GPU's tile workgroup
+// slots (prefill chunks of 512 rows usually fill them unsplit; a few verify
+// blocks over long contexts need splits to occupy the CUs).
 DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t region_rows, uint32_t kv_heads,
-                              uint32_t q_heads, uint32_t page_tokens, uint32_t max_visible_tokens,
+                              uint32_t q_heads, uint32_t head_dim, uint32_t kv_bytes,
+                              uint32_t page_tokens, uint32_t max_visible_tokens,
                               uint64_t partial_bytes) {
     DecodeSplit s;
     if (max_visible_tokens < kSplitMinVisible || n_tiles == 0 || kv_heads == 0) return s;
-    const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
-    const uint64_t work = (uint64_t)n_tiles * kv_heads * max_pages;
-    uint64_t per = std::max<uint64_t>(kMinPagesPerSplit, (work + kTargetWorkgroups - 1) / kTargetWorkgroups);
     const uint32_t q_per_kv = q_heads / kv_heads;
-    for (;;) {
-        const uint64_t splits = (max_pages + per - 1) / per;
-        if (splits <= 1) return s;
+    const uint64_t slots = (uint64_t)device_cus() *
+                           psk::tile_workgroups_per_cu(kv_bytes == 1 ? 1 : 2, head_dim, q_per_kv);
+    const uint64_t wgs = (uint64_t)n_tiles * kv_heads;
+    if (wgs >= slots) return s;
+    const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
+    uint64_t splits = std::min<uint64_t>((slots + wgs - 1) / wgs, max_pages / kMinPagesPerSplit);
+    splits = std::min<uint64_t>(splits, kMaxSplits);
+    while (splits > 1) {
         const uint64_t need = (uint64_t)region_rows * kv_heads * splits * q_per_kv *
                               (2u + ::ps::kernel::kPagedAttentionHeadLimit) * sizeof(float);
-        if (splits <= kMaxSplits && need <= partial_bytes) {
-            s.splits = static_cast<uint32_t>(splits);
-            s.pages_per_split = static_cast<uint32_t>(per);
-            return s;
-        }
-        per *= 2;
+        if (need <= partial_bytes) break;
+        splits /= 2;
     }
+    if (splits <= 1) return s;
+    const uint64_t per = (max_pages + splits - 1) / splits;
+    s.splits = static_cast<uint32_t>((max_pages + per - 1) / per);
+    s.pages_per_split = static_cast<uint32_t>(per);
+    return s;
 }
 
 bool is_tile_request(const StepRequest& r) {
@@ -194,14 +214,28 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         plan.kernels[plan.count++] = k;
         return Status::make_ok();
     };
+    // Upper bounds of the rows' visible lengths where the requests carry them
+    // (StepRequest::max_visible), else the step's max_visible_tokens.
+    std::vector<uint32_t> row_vis;
     auto add_decode = [&](uint32_t row_begin, uint32_t rows) -> Status {
         PlannedKernel k;
         k.kind = PlannedKernel::Kind::Decode;
         k.row_begin = row_begin;
         k.rows = rows;
+        row_vis.assign(rows, step.max_visible_tokens);
+        for (uint32_t i = 0; i < step.num_requests; ++i) {
+            const StepRequest& r = step.requests[i];
+            if (r.max_visible == 0 || r.row_begin >= row_begin + rows ||
+                r.row_begin + r.row_count <= row_begin)
+                continue;
+            const uint32_t lo = std::max(r.row_begin, row_begin);
+            const uint32_t hi = std::min(r.row_begin + r.row_count, row_begin + rows);
+            for (uint32_t j = lo; j < hi; ++j)
+                row_vis[j - row_begin] = std::min(r.max_visible, step.max_visible_tokens);
+        }
         const DecodeSplit s = choose_decode_split(
             rows, c.kv_heads, c.q_heads, c.head_dim, step.kv_dtype == KVCacheDType::FP8_E4M3 ? 1u : 2u,
-            c.page_tokens, step.max_visible_tokens, nullptr, pbytes);
+            c.page_tokens, step.max_visible_tokens, row_vis.data(), pbytes);
         k.splits = s.splits;
         k.pages_per_split = s.pages_per_split;
         return push(k);
@@ -240,21 +274,33 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         k.tile_first = static_cast<uint32_t>(plan.tiles.size());
         k.req_first = static_cast<uint32_t>(plan.combine.size());
         uint32_t lo = UINT32_MAX, hi = 0;
+        std::vector<std::pair<uint32_t, PlannedTile>> tiles;   // (visible bound, tile)
         for (const auto& r : reqs) {
             if (r.execution_class != cls || !is_tile_request(r)) continue;
-            for (uint32_t t = 0; t < r.row_count; t += kTileRowsPerTile)
-                plan.tiles.push_back({r.row_begin + t, std::min(kTileRowsPerTile, r.row_count - t)});
+            for (uint32_t t = 0; t < r.row_count; t += kTileRowsPerTile) {
+                const uint32_t n = std::min(kTileRowsPerTile, r.row_count - t);
+                // rows of a request see prefix + index + 1 tokens
+                const uint32_t vis = r.max_visible != 0 ? r.max_visible - (r.row_count - t - n)
+                                                        : step.max_visible_tokens;
+                tiles.push_back({vis, {r.row_begin + t, n}});
+            }
             plan.combine.push_back(r);
             lo = std::min(lo, r.row_begin);
             hi = std::max(hi, r.row_begin + r.row_count);
         }
+        // longest tiles first: workgroups are dispatched in tile order
+        std::stable_sort(tiles.begin(), tiles.end(),
+                         [](const auto& x, const auto& y) { return x.first > y.first; });
+        for (const auto& t : tiles) plan.tiles.push_back(t.second);
         k.tile_count = static_cast<uint32_t>(plan.tiles.size()) - k.tile_first;
         k.req_count = static_cast<uint32_t>(plan.combine.size()) - k.req_first;
         if (k.tile_count == 0) continue;
         k.row_begin = lo;
         k.rows = hi - lo;
-        const DecodeSplit s = choose_tile_split(k.tile_count, k.rows, c.kv_heads, c.q_heads,
-                                                c.page_tokens, step.max_visible_tokens, pbytes);
+        const DecodeSplit s = choose_tile_split(
+            k.tile_count, k.rows, c.kv_heads, c.q_heads, c.head_dim,
+            step.kv_dtype == KVCacheDType::FP8_E4M3 ? 1u : 2u, c.page_tokens,
+            step.max_visible_tokens, pbytes);
         k.splits = s.splits;
         k.pages_per_split = s.pages_per_split;
         Status st = push(k);

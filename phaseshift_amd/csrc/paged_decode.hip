@@ -83,30 +83,6 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const uint8_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void global_void_t;
-
-// Global memory straight into LDS (gfx950 LDS DMA, global_load_lds_dword /
-// _dwordx4): lane l of the wave writes LDS[dst + BYTES*l]. `dst` must be
-// wave-uniform. The hardware counts these loads in vmcnt and writes LDS
-// asynchronously: the wave reads the data only after s_waitcnt vmcnt.
-template <int BYTES>
-__device__ __forceinline__ void load_lds(const void* src, uint8_t* dst) {
-    static_assert(BYTES == 4 || BYTES == 16, "DMA width");
-    if constexpr (BYTES == 16)
-        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 16, 0, 0);
-    else
-        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 4, 0, 0);
-}
-
-// Waits until at most N vector-memory operations of this wave are
-// outstanding. The memory clobber keeps every load and LDS access on its side.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // Units of work of one row: splits that hold pages, 0 for a row the kernel
 // skips (invalid slot, position past the block table).
 __device__ __forceinline__ uint32_t row_units(const psk_paged_attention_args& a, uint32_t splits,
@@ -202,7 +178,7 @@ constexpr uint32_t kPageWindow = 1024;   // block-table entries staged in LDS pe
 // DMA layout) and, FP8, the k/v scales of its tokens.
 template <int KVB, int D>
 constexpr int stage_bytes() {
-    return 2 * chunk_halves<KVB>() * 16 * D * KVB + (KVB == 1 ? 2 * chunk_halves<KVB>() * 256 : 0);
+    return 2 * chunk_halves<KVB>() * (16 * D * KVB + 128) + (KVB == 1 ? 2 * chunk_halves<KVB>() * 256 : 0);
 }
 
 // kIndep: the 4 waves of a workgroup are 4 independent items, the kv heads
@@ -219,8 +195,11 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
     constexpr int NL = D * KVB / 64;   // 16 B loads per lane per 16-token half
     constexpr int NS = D / 32;         // MFMA K-steps of the score product
     constexpr int NDB = D / 16;        // 16-dim blocks of the output
-    constexpr int HALF_BYTES = 16 * D * KVB;
-    constexpr int KV_BYTES = H * HALF_BYTES;               // K (or V) of one chunk
+    // a 16-token half of K (V) in LDS, padded by 128 B so that the two halves
+    // of a chunk fall on opposite halves of the 64 LDS banks (the transposing
+    // V reads of one instruction touch both)
+    constexpr int HALF_STRIDE = 16 * D * KVB + 128;
+    constexpr int KV_BYTES = H * HALF_STRIDE;               // K (or V) of one chunk
     constexpr int SC_BYTES = KVB == 1 ? H * 256 : 0;       // k (or v) scales of one chunk
     constexpr int STAGE = stage_bytes<KVB, D>();
     constexpr int kWinBytes = (int)kPageWindow * 4;
@@ -291,11 +270,11 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
     //   FP8:  token (r>>1 < 4 ? 4g + (r>>1) : 16 + 4g + (r>>1) - 4), dims +8*(r&1)
     //   BF16: token 4g + (r>>2), dims +4*(r&3)
     // In the DMA layout byte b of token t (half t/16) sits at
-    // (t/16)*HALF_BYTES + 1024*(b/64) + 16*(16*((b%64)/16) + t%16) + b%16.
+    // (t/16)*HALF_STRIDE + 1024*(b/64) + 16*(16*((b%64)/16) + t%16) + b%16.
     uint32_t tr_off;
     if constexpr (KVB == 1) {
         const uint32_t j = n >> 1;
-        tr_off = (j < 4u ? 0u : (uint32_t)HALF_BYTES) + 16u * (4u * g + (j & 3u)) + 8u * (n & 1u);
+        tr_off = (j < 4u ? 0u : (uint32_t)HALF_STRIDE) + 16u * (4u * g + (j & 3u)) + 8u * (n & 1u);
     } else {
         tr_off = 16u * (4u * g + (n >> 2)) + 256u * ((n >> 1) & 1u) + 8u * (n & 1u);
     }
@@ -320,7 +299,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
         if (!active || cb >= te) continue;
 
         // Issues the DMAs of the chunk at c into stage `st`: load i of half
-        // hf of K (V) at +hf*HALF_BYTES + 1024*i, lane (n, g) at +16*(16g + n)
+        // hf of K (V) at +hf*HALF_STRIDE + 1024*i, lane (n, g) at +16*(16g + n)
         // holding bytes [64i + 16g, +16) of token n; the scales of token n at
         // +4*(16g + n) of each 256 B scale block. Loads are branch-free:
         // tokens past the range read the last token (their scores are
@@ -339,10 +318,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
                 const uint8_t* ks = p.k_pool + elem * KVB + g * 16;
                 const uint8_t* vs = p.v_pool + elem * KVB + g * 16;
 #pragma unroll
-                for (int i = 0; i < NL; ++i) load_lds<16>(ks + i * 64, st + hf * HALF_BYTES + i * 1024);
+                for (int i = 0; i < NL; ++i) load_lds<16>(ks + i * 64, st + hf * HALF_STRIDE + i * 1024);
 #pragma unroll
                 for (int i = 0; i < NL; ++i)
-                    load_lds<16>(vs + i * 64, st + KV_BYTES + hf * HALF_BYTES + i * 1024);
+                    load_lds<16>(vs + i * 64, st + KV_BYTES + hf * HALF_STRIDE + i * 1024);
                 if constexpr (KVB == 1) {
                     const uint64_t si = ((scale_layer + page) * P + off) * a.kv_heads + kvh;
                     load_lds<4>(p.k_scale + si, st + 2 * KV_BYTES + hf * 256);
@@ -357,7 +336,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
 #pragma unroll
             for (int hf = 0; hf < H; ++hf) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                const uint8_t* kb = st + hf * HALF_BYTES + 16 * lane;
+                const uint8_t* kb = st + hf * HALF_STRIDE + 16 * lane;
 #pragma unroll
                 for (int s = 0; s < NS; ++s) {
                     bf16x8 kf;
@@ -680,7 +659,7 @@ bool mfma_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
 size_t decode_workgroup_lds_bytes(int kvb, uint32_t head_dim) {
     const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
     const size_t H = kvb == 1 ? 2 : 1;
-    const size_t stage = 2 * H * 16 * D * kvb + (kvb == 1 ? 2 * H * 256 : 0);
+    const size_t stage = 2 * H * (16 * D * kvb + 128) + (kvb == 1 ? 2 * H * 256 : 0);
     return (size_t)kPageWindow * 4 + (size_t)kWaves * 2 * stage;
 }
 
@@ -708,13 +687,14 @@ hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t st
     return hipGetLastError();
 }
 
-// Independent waves (one kv head each) when that grid fills the GPU's 256
-// CUs; otherwise the 4 waves share each (row, kv_head, split) item.
+// Independent waves (one kv head each) when that grid fills at least half of
+// the GPU's 256 CUs; otherwise the 4 waves share each (row, kv_head, split)
+// item. The split chooser assumes the same rule.
 template <int KVB, int D>
 hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
     const uint64_t units = (uint64_t)p.a.rows * p.splits;
     const uint64_t groups = (p.a.kv_heads + kWaves - 1u) / kWaves;
-    if (units * groups >= 256u) return launch_decode_t2<KVB, D, true, kWaves>(p, units * groups, stream);
+    if (units * groups >= 128u) return launch_decode_t2<KVB, D, true, kWaves>(p, units * groups, stream);
     return launch_decode_t2<KVB, D, false, kWaves>(p, units * p.a.kv_heads, stream);
 }
 

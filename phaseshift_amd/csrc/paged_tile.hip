@@ -68,23 +68,44 @@ __device__ __forceinline__ bf16x8 q8(const uint16_t* q, bool ok) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
+constexpr uint32_t kTilePageWindow = 1024;   // block-table entries staged in LDS per pass
+
+// LDS bytes of one pipeline stage: K and V of a 32-token chunk (lane-major DMA
+// layout) and, FP8, the k/v scales of its tokens.
 template <int KVB, int D>
-__global__ __launch_bounds__(kMaxTileWaves * 64) void paged_tile_kernel(const TileParams p) {
-    constexpr int CT = 32;               // tokens per chunk (two 16-token halves)
-    constexpr int TB = D * KVB;          // bytes of one token's head slice
-    constexpr int ROW = TB + 16;         // padded LDS row
-    constexpr int NL = TB / 64;          // 16 B pieces per lane per half
+constexpr int tile_stage_bytes() {
+    return 2 * 2 * (16 * D * KVB + 128) + (KVB == 1 ? 2 * 2 * 256 : 0);
+}
+constexpr int kTileStages = 4;
+
+template <int KVB, int D, int NW>
+__global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams p) {
+    constexpr int H = 2;                 // 16-token halves per chunk
+    constexpr int CT = 16 * H;           // tokens per chunk
+    constexpr int NL = D * KVB / 64;     // 16 B DMA pieces per lane per half
     constexpr int NS = D / 32;           // K-steps of QK^T
     constexpr int NDB = D / 16;          // 16-dim output blocks
-    constexpr int PIECES = CT * TB / 16; // 16 B pieces of one K (or V) chunk
+    // a 16-token half of K (V) in LDS, padded by 128 B so that the two halves
+    // of a chunk fall on opposite halves of the 64 LDS banks (the transposing
+    // V reads of one instruction touch both)
+    constexpr int HALF_STRIDE = 16 * D * KVB + 128;
+    constexpr int KV_BYTES = H * HALF_STRIDE;
+    constexpr int SC_BYTES = KVB == 1 ? H * 256 : 0;
+    constexpr int STAGE = tile_stage_bytes<KVB, D>();
+    // DMA instructions of one chunk (K, V, then FP8 k/v scales), dealt
+    // round-robin over the NW waves; every wave issues DPW of them (the
+    // remainder repeats earlier ones, which rewrite identical bytes), so the
+    // vmcnt bookkeeping is one compile-time count per wave.
+    constexpr int NI = 2 * H * NL + (KVB == 1 ? 2 * H : 0);
+    constexpr int DPW = (NI + NW - 1) / NW;
+    constexpr int kWinBytes = (int)kTilePageWindow * 4;
+    static_assert(NL >= 1 && NS >= 1 && 2 * DPW < 64, "tile geometry");
 
-    __shared__ __align__(16) uint8_t k_lds[CT * ROW];
-    __shared__ __align__(16) uint8_t v_lds[CT * ROW];
-    __shared__ float ks_lds[CT], vs_lds[CT];
+    extern __shared__ __align__(16) uint8_t lds[];
     __shared__ uint32_t bad_lds;
 
     const psk_paged_attention_args& a = p.a;
-    const uint32_t tid = threadIdx.x, nthreads = blockDim.x;
+    const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u, w = tid >> 6;
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t qpk = a.q_heads / a.kv_heads;
@@ -120,7 +141,7 @@ __global__ __launch_bounds__(kMaxTileWaves * 64) void paged_tile_kernel(const Ti
     uint32_t vis_max = vis;
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) vis_max = max(vis_max, (uint32_t)__shfl_xor((int)vis_max, o, 64));
-    if (vis_max == 0u) return;   // uniform: every lane saw the same 16 rows
+    if (vis_max == 0u) return;   // uniform: every wave saw the same 16 rows
     const uint32_t P = a.page_tokens;
     const uint32_t pc = (vis_max + P - 1u) / P;
     const uint32_t per = p.pages_per_split != 0u ? p.pages_per_split : (pc + p.splits - 1u) / p.splits;
@@ -131,11 +152,15 @@ __global__ __launch_bounds__(kMaxTileWaves * 64) void paged_tile_kernel(const Ti
     const uint32_t* bt = a.block_tables + (uint64_t)slot * a.block_table_stride;
     const uint64_t layer_base = (uint64_t)a.layer * a.elems_per_layer;
     const uint64_t scale_layer = (uint64_t)a.layer * a.num_pages;
+    // Everything above is uniform over the workgroup, so all waves reach the
+    // barriers below; a wave past the last query head of the group only
+    // issues its share of the DMAs.
+    const bool computes = w < qpk;
 
     if (tid == 0) bad_lds = 0u;
 
     // this wave's query head; Q fragments of the 16 rows (column n = row n)
-    const uint32_t head = kv_head * qpk + w;
+    const uint32_t head = kv_head * qpk + (computes ? w : 0u);
     bf16x8 qf[NS];
     {
         const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
@@ -143,7 +168,7 @@ __global__ __launch_bounds__(kMaxTileWaves * 64) void paged_tile_kernel(const Ti
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const int d0 = KVB == 2 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
-            qf[s] = q8(qrow + d0, row_ok);
+            qf[s] = q8(qrow + d0, row_ok && computes);
         }
     }
 
@@ -152,147 +177,200 @@ __global__ __launch_bounds__(kMaxTileWaves * 64) void paged_tile_kernel(const Ti
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    // tr-read offsets of this lane inside a V tile (token slots as in the decode kernel)
-    uint32_t tr_off0, tr_off1 = 0;
+    // tr-read offsets of this lane inside the V part of a stage. Lane r of a
+    // 16-lane block names row r of the transpose; in the DMA layout byte b of
+    // token t sits at (t/16)*HALF_STRIDE + 1024*(b/64) + 16*(16*((b%64)/16) + t%16) + b%16.
+    //   FP8:  token (r>>1 < 4 ? 4g + (r>>1) : 16 + 4g + (r>>1) - 4), dims +8*(r&1); block db +256*db
+    //   BF16: token 4g + (r>>2) of each half, dims +4*(r&3); block db +512*db
+    uint32_t tr_off;
     if constexpr (KVB == 1) {
         const uint32_t j = n >> 1;
-        const uint32_t tok = j < 4u ? 4u * g + j : 16u + 4u * g + (j - 4u);
-        tr_off0 = tok * ROW + 8u * (n & 1u);
+        tr_off = (j < 4u ? 0u : (uint32_t)HALF_STRIDE) + 16u * (4u * g + (j & 3u)) + 8u * (n & 1u);
     } else {
-        tr_off0 = (4u * g + (n >> 2)) * ROW + 8u * (n & 3u);
-        tr_off1 = (16u + 4u * g + (n >> 2)) * ROW + 8u * (n & 3u);
+        tr_off = 16u * (4u * g + (n >> 2)) + 256u * ((n >> 1) & 1u) + 8u * (n & 1u);
     }
 
-    for (uint32_t cb = t_begin; cb < t_end; cb += CT) {
-        __syncthreads();   // previous chunk fully consumed
-        // ---- stage K/V (and FP8 scales) of tokens cb .. cb+31 in LDS
-        for (uint32_t idx = tid; idx < (uint32_t)PIECES; idx += nthreads) {
-            const uint32_t t = idx / (TB / 16), part = idx % (TB / 16);
-            const uint32_t tau = cb + t;
-            u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-            if (tau < t_end) {
-                const uint32_t page = bt[tau / P];
-                if (page < a.num_pages) {
-                    const uint64_t e = layer_base + (uint64_t)page * a.elems_per_page +
-                                       (uint64_t)(tau % P) * a.elems_per_token + (uint64_t)kv_head * D;
-                    kv = *reinterpret_cast<const u32x4*>(p.k_pool + e * KVB + part * 16);
-                    vv = *reinterpret_cast<const u32x4*>(p.v_pool + e * KVB + part * 16);
-                } else {
-                    bad_lds = 1u;
-                }
-            }
-            *reinterpret_cast<u32x4*>(k_lds + t * ROW + part * 16) = kv;
-            *reinterpret_cast<u32x4*>(v_lds + t * ROW + part * 16) = vv;
-        }
-        if constexpr (KVB == 1) {
-            if (tid < (uint32_t)CT) {
-                const uint32_t tau = cb + tid;
-                float ksv = 0.0f, vsv = 0.0f;
-                if (tau < t_end) {
-                    const uint32_t page = bt[tau / P];
-                    if (page < a.num_pages) {
-                        const uint64_t si = ((scale_layer + page) * P + tau % P) * a.kv_heads + kv_head;
-                        ksv = p.k_scale[si];
-                        vsv = p.v_scale[si];
-                    }
-                }
-                ks_lds[tid] = ksv;
-                vs_lds[tid] = vsv;
-            }
-        }
-        __syncthreads();
-        if (w >= qpk) continue;   // spare waves only help staging
+    uint32_t* const win = reinterpret_cast<uint32_t*>(lds);
+    uint8_t* const stages = lds + kWinBytes;
+    // pool pointers and the wave index in scalar registers: the DMA dealing
+    // below selects among them per wave without memory accesses
+    const uint8_t* const k_pool = p.k_pool;
+    const uint8_t* const v_pool = p.v_pool;
+    const float* const k_scale = p.k_scale;
+    const float* const v_scale = p.v_scale;
+    const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
 
-        // ---- S^T for both halves: K fragment of token hf*16+n from LDS
-        f32x4 sc[2];
+    for (uint32_t wp = pb; wp < pe; wp += kTilePageWindow) {
+        const uint32_t wp_end = min(pe, wp + kTilePageWindow);
+        __syncthreads();
+        for (uint32_t i = tid; i < wp_end - wp; i += NW * 64u) win[i] = bt[wp + i];
+        __syncthreads();
+        const uint32_t ts = max(wp * P, t_begin);
+        const uint32_t te = min(wp_end * P, t_end);
+        if (ts >= te) continue;
+        const uint32_t t_last = te - 1u;
+
+        // This wave's DMAs of the chunk at c into stage st (branch-free;
+        // tokens past the range read the last token and are masked later).
+        auto issue = [&](uint32_t c, uint8_t* st) __attribute__((always_inline)) {
+            // page ids of this lane's token in both halves first: no LDS read
+            // follows a DMA of this step
+            uint32_t pg[H], off[H];
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const uint8_t* kr = k_lds + (hf * 16 + n) * ROW + g * 16;
+            for (int hf = 0; hf < H; ++hf) {
+                const uint32_t tau = min(c + (uint32_t)hf * 16u + n, t_last);
+                const uint32_t page = win[tau / P - wp];
+                const bool inv = page >= a.num_pages;
+                if (inv) bad_lds = 1u;
+                pg[hf] = inv ? 0u : page;
+                off[hf] = tau % P;
+            }
 #pragma unroll
-            for (int i = 0; i < NL; ++i) {
-                const u32x4 wv = *reinterpret_cast<const u32x4*>(kr + i * 64);
-                if constexpr (KVB == 2) {
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv), qf[i],
-                                                                  acc, 0, 0, 0);
+            for (int t = 0; t < DPW; ++t) {
+                const uint32_t j = (wu + (uint32_t)NW * t) % (uint32_t)NI;   // scalar
+                if (j < 2u * H * NL) {
+                    const uint32_t kind = j / (H * NL), hf = (j % (H * NL)) / NL, i = j % NL;
+                    const uint64_t elem = layer_base + (uint64_t)pg[hf] * a.elems_per_page +
+                                          (uint64_t)off[hf] * a.elems_per_token + (uint64_t)kv_head * D;
+                    const uint8_t* src = (kind == 0u ? k_pool : v_pool) + elem * KVB + g * 16 + i * 64;
+                    load_lds<16>(src, st + kind * KV_BYTES + hf * HALF_STRIDE + i * 1024);
                 } else {
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(wv[0], wv[1]),
-                                                                  qf[2 * i], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16x8(wv[2], wv[3]),
-                                                                  qf[2 * i + 1], acc, 0, 0, 0);
+                    const uint32_t kind = (j - 2u * H * NL) & 1u, hf = (j - 2u * H * NL) >> 1;
+                    const uint64_t si = ((scale_layer + pg[hf]) * P + off[hf]) * a.kv_heads + kv_head;
+                    load_lds<4>((kind == 0u ? k_scale : v_scale) + si,
+                                st + 2 * KV_BYTES + kind * SC_BYTES + hf * 256);
                 }
             }
-            sc[hf] = acc;
-        }
-        // ---- lane (n, g): row n, tokens cb + 16*hf + 4*g + r; causal per row
-        float s2[2][4], vsc[2][4];
-        float mx = -INFINITY;
+        };
+
+        // Scores, causal online softmax and PV of the chunk at c in stage st.
+        auto consume = [&](uint32_t c, const uint8_t* st) __attribute__((always_inline)) {
+            f32x4 sc[H];
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+            for (int hf = 0; hf < H; ++hf) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                const uint8_t* kb = st + hf * HALF_STRIDE + 16 * lane;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t tl = hf * 16 + 4 * g + r;
-                const uint32_t tau = cb + tl;
-                float f = p.scale_log2, vs = 1.0f;
+                for (int s = 0; s < NS; ++s) {
+                    // one K-step at a time keeps the converted fragments short-lived
+                    if (s % 2 == 0) __builtin_amdgcn_sched_barrier(0);
+                    bf16x8 kf;
+                    if constexpr (KVB == 2) {
+                        kf = *reinterpret_cast<const bf16x8*>(kb + 1024 * s);
+                    } else {
+                        const u32x4 wv = *reinterpret_cast<const u32x4*>(kb + 1024 * (s >> 1));
+                        kf = (s & 1) ? fp8x8_to_bf16x8(wv[2], wv[3]) : fp8x8_to_bf16x8(wv[0], wv[1]);
+                    }
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
+                }
+                sc[hf] = acc;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // lane (n, g): row n, tokens c + 16*hf + 4*g + r; causal per row
+            float s2[H][4], vsc[H][4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int hf = 0; hf < H; ++hf) {
+                f32x4 kscale = {1.f, 1.f, 1.f, 1.f}, vscale = {1.f, 1.f, 1.f, 1.f};
                 if constexpr (KVB == 1) {
-                    f *= ks_lds[tl];
-                    vs = vs_lds[tl];
+                    kscale = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + hf * 256 + 16 * g);
+                    vscale = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + SC_BYTES + hf * 256 +
+                                                             16 * g);
                 }
-                s2[hf][r] = (tau < vis && tau < t_end) ? sc[hf][r] * f : -INFINITY;
-                vsc[hf][r] = vs;
-                mx = __builtin_fmaxf(mx, s2[hf][r]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t tau = c + hf * 16 + 4 * g + r;
+                    s2[hf][r] = (tau < vis && tau < te) ? sc[hf][r] * (p.scale_log2 * kscale[r])
+                                                        : -INFINITY;
+                    vsc[hf][r] = vscale[r];
+                    mx = __builtin_fmaxf(mx, s2[hf][r]);
+                }
             }
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = __builtin_fmaxf(m_run, mx);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-        float pv[2][4], psum = 0.0f;
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = __builtin_fmaxf(m_run, mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+            float pv[H][4], psum = 0.0f;
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+            for (int hf = 0; hf < H; ++hf)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
-                psum += e;
-                pv[hf][r] = e * vsc[hf][r];
+                for (int r = 0; r < 4; ++r) {
+                    const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
+                    psum += e;
+                    pv[hf][r] = e * vsc[hf][r];
+                }
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+            if (__any(alpha != 1.0f)) {
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
             }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (__any(alpha != 1.0f)) {
+            // P as hi + lo bf16 pairs (two MFMAs, ~16 mantissa bits per weight)
+            u32x4 ph, pl;
+            { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
+            { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
+            { const u32x2 t_ = split_bf16x2(pv[1][0], pv[1][1]); ph[2] = t_[0]; pl[2] = t_[1]; }
+            { const u32x2 t_ = split_bf16x2(pv[1][2], pv[1][3]); ph[3] = t_[0]; pl[3] = t_[1]; }
+            const bf16x8 pfh = __builtin_bit_cast(bf16x8, ph);
+            const bf16x8 pfl = __builtin_bit_cast(bf16x8, pl);
+            // O^T += V^T P^T
+            const uint8_t* vb = st + KV_BYTES + tr_off;
+            // Blocks of 4 output-dim groups: the scheduling barriers keep the
+            // compiler from hoisting every V read of the chunk at once, which
+            // would need more registers than 3 waves per SIMD leave.
 #pragma unroll
-            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+            for (int db = 0; db < NDB; ++db) {
+                if (db % 2 == 0) __builtin_amdgcn_sched_barrier(0);
+                bf16x8 vf;
+                if constexpr (KVB == 1) {
+                    const i32x2 x = tr8(vb + 256 * db);
+                    vf = fp8x8_to_bf16x8((uint32_t)x[0], (uint32_t)x[1]);
+                } else {
+                    const i16x4 x0 = tr16(vb + 512 * db);
+                    const i16x4 x1 = tr16(vb + HALF_STRIDE + 512 * db);
+                    u32x4 u;
+                    u[0] = __builtin_bit_cast(u32x2, x0)[0];
+                    u[1] = __builtin_bit_cast(u32x2, x0)[1];
+                    u[2] = __builtin_bit_cast(u32x2, x1)[0];
+                    u[3] = __builtin_bit_cast(u32x2, x1)[1];
+                    vf = __builtin_bit_cast(bf16x8, u);
+                }
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfh, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfl, o[db], 0, 0, 0);
+            }
+        };
+
+        // One step: after this wave's DMAs of chunk c landed (vmcnt leaves the
+        // next chunk's DPW outstanding) the barrier makes every wave's DMAs of
+        // c visible and guarantees every wave finished the chunk before c, so
+        // its stage may be refilled with the chunk two ahead. __restrict__
+        // tells the compiler that the DMA into `next` and the reads of `cur`
+        // touch different LDS; their real ordering is the wait + barrier.
+        auto step = [&](uint32_t c, uint8_t* __restrict__ next,
+                        const uint8_t* __restrict__ cur) __attribute__((always_inline)) {
+            issue(c + (kTileStages - 1u) * CT, next);
+            if (computes) consume(c, cur);
+        };
+
+        // kTileStages - 1 chunks in flight: the DMAs of chunk k go out
+        // kTileStages - 1 steps before it is consumed
+        constexpr uint32_t kAhead = kTileStages - 1;
+#pragma unroll
+        for (uint32_t a_ = 0; a_ < kAhead; ++a_) issue(ts + a_ * CT, stages + a_ * STAGE);
+        uint32_t sc = 0;   // stage of the chunk at c
+        for (uint32_t c = ts; c < te; c += CT) {
+            wait_vmcnt_barrier<(kAhead - 1) * DPW>();
+            const uint32_t sn = sc == 0u ? kTileStages - 1u : sc - 1u;   // stage of chunk c + kAhead
+            step(c, stages + sn * STAGE, stages + sc * STAGE);
+            sc = sc == kTileStages - 1u ? 0u : sc + 1u;
         }
-        // P as hi + lo bf16 pairs (two MFMAs, ~16 mantissa bits per weight)
-        u32x4 ph, pl;
-        { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
-        { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
-        { const u32x2 t_ = split_bf16x2(pv[1][0], pv[1][1]); ph[2] = t_[0]; pl[2] = t_[1]; }
-        { const u32x2 t_ = split_bf16x2(pv[1][2], pv[1][3]); ph[3] = t_[0]; pl[3] = t_[1]; }
-        const bf16x8 pfh = __builtin_bit_cast(bf16x8, ph);
-        const bf16x8 pfl = __builtin_bit_cast(bf16x8, pl);
-        // ---- O^T += V^T P^T
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-            bf16x8 vf;
-            if constexpr (KVB == 1) {
-                const i32x2 x = tr8(v_lds + tr_off0 + 16 * db);
-                vf = fp8x8_to_bf16x8((uint32_t)x[0], (uint32_t)x[1]);
-            } else {
-                const i16x4 x0 = tr16(v_lds + tr_off0 + 32 * db);
-                const i16x4 x1 = tr16(v_lds + tr_off1 + 32 * db);
-                u32x4 u;
-                u[0] = __builtin_bit_cast(u32x2, x0)[0];
-                u[1] = __builtin_bit_cast(u32x2, x0)[1];
-                u[2] = __builtin_bit_cast(u32x2, x1)[0];
-                u[3] = __builtin_bit_cast(u32x2, x1)[1];
-                vf = __builtin_bit_cast(bf16x8, u);
-            }
-            o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfh, o[db], 0, 0, 0);
-            o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfl, o[db], 0, 0, 0);
-        }
+        // The last steps issued chunks nobody reads: their DMAs must land
+        // before the LDS is reused.
+        wait_vmcnt<0>();
     }
     __syncthreads();
-    if (w >= qpk) return;
+    if (!computes) return;
     const float l_tot = l_run + __shfl_xor(l_run, 16, 64);
     const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
     float* part = nullptr;
@@ -347,16 +425,32 @@ bool tile_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
     return true;
 }
 
+template <int KVB, int D, int NW>
+hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream) {
+    const size_t lds_bytes = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * tile_stage_bytes<KVB, D>();
+    if (lds_bytes > 64u * 1024u) {
+        // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&paged_tile_kernel<KVB, D, NW>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+        if (attr != hipSuccess) return attr;
+    }
+    hipLaunchKernelGGL((paged_tile_kernel<KVB, D, NW>), dim3((uint32_t)grid), dim3(NW * 64), lds_bytes,
+                       stream, p);
+    return hipGetLastError();
+}
+
+// One wave per query head of the GQA group (at least 4 waves, so every SIMD
+// issues part of the DMAs).
 template <int KVB, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     const uint64_t tiles = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1) / kTileRows;
     const uint64_t grid = tiles * p.a.kv_heads * p.splits;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    // at least 4 waves so every SIMD helps stage K/V
-    const uint32_t waves = qpk < 4u ? 4u : qpk;
-    hipLaunchKernelGGL((paged_tile_kernel<KVB, D>), dim3((uint32_t)grid), dim3(waves * 64), 0, stream, p);
-    return hipGetLastError();
+    if (qpk <= 4u) return launch_tile_t2<KVB, D, 4>(p, grid, stream);
+    if (qpk <= 6u) return launch_tile_t2<KVB, D, 6>(p, grid, stream);
+    return launch_tile_t2<KVB, D, 8>(p, grid, stream);
 }
 
 template <int KVB>
@@ -431,6 +525,19 @@ hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dty
         if (le != hipSuccess) return le;
     }
     return hipSuccess;
+}
+
+// Tile workgroups that fit one CU: LDS (block-table window + pipeline
+// stages) and waves (at most 3 per SIMD at the kernel's register budget).
+uint32_t tile_workgroups_per_cu(int kvb, uint32_t head_dim, uint32_t q_per_kv) {
+    const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
+    const size_t stage = 2 * 2 * (16 * D * kvb + 128) + (kvb == 1 ? 2 * 2 * 256 : 0);
+    const size_t lds = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * stage + 64;
+    const uint32_t by_lds = (uint32_t)((160u * 1024u) / lds);
+    const uint32_t nw = q_per_kv <= 4u ? 4u : q_per_kv <= 6u ? 6u : 8u;
+    const uint32_t by_waves = 12u / nw;
+    const uint32_t n = by_lds < by_waves ? by_lds : by_waves;
+    return n == 0u ? 1u : n;
 }
 
 bool paged_tiles_supported(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,

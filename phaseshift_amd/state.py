@@ -153,11 +153,13 @@ def plan_step(args, kv_dtype: int, requests, max_visible_tokens: int, partial_by
               partials_ptr=None, k_pool=None, v_pool=None, k_scale=None, v_scale=None,
               stream=None, launch=False) -> StepPlan:
     """psk_paged_attention_step: plan (and with launch=True run) one step's
-    PAGED_ATTENTION binding. requests: list of (row_begin, row_count, exec_class)."""
+    PAGED_ATTENTION binding. requests: list of (row_begin, row_count, exec_class)
+    or (row_begin, row_count, exec_class, max_visible)."""
     n = len(requests)
     reqs = (StepRequest * max(n, 1))()
-    for i, (b, c, e) in enumerate(requests):
-        reqs[i].row_begin, reqs[i].row_count, reqs[i].execution_class = b, c, e
+    for i, r in enumerate(requests):
+        reqs[i].row_begin, reqs[i].row_count, reqs[i].execution_class = r[0], r[1], r[2]
+        reqs[i].max_visible = r[3] if len(r) > 3 else 0
     plan = StepPlan()
     p = lambda t: None if t is None else (t if isinstance(t, int) else t.data_ptr())
     # planning alone only needs a non-null partials pointer to allow split-K
