@@ -73,9 +73,9 @@ __device__ __forceinline__ bool fast_div_ok(float scale) {
 }
 
 // Fast path: head_dim % 8 == 0, head_dim <= 8 * L, every access aligned. A
-// wave runs kUnroll groups of 64/L tasks. All input loads of the kUnroll
-// groups are issued first, then the kUnroll slot/position loads, then the
-// kUnroll block-table loads, so the HBM reads overlap the lookup chain
+// wave runs kUnroll groups of 64/L tasks. The kUnroll slot/position loads go
+// out first, then all input loads, then the block-table loads (which wait
+// only for slot/position), so the HBM reads overlap the lookup chain
 // (reference skip rules: kv_append.hip:31-55).
 constexpr int kUnroll = 4;
 
@@ -95,6 +95,9 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
     uint32_t row[kUnroll], head[kUnroll];
     bool live[kUnroll];
     u32x4 kw[kUnroll], vw[kUnroll];
+    uint32_t slot[kUnroll], pos[kUnroll];
+    // slot/position loads first: the block-table loads below need only them
+    // (vmcnt retires in order), so their round trip overlaps the K/V reads
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
         const uint32_t task = (wave_global * kUnroll + u) * tasks_per_wave + (lane >> p.log2_lanes);
@@ -102,6 +105,11 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
         const uint32_t t = live[u] ? task : 0u;
         row[u] = t / a.kv_heads;
         head[u] = t - row[u] * a.kv_heads;
+        slot[u] = a.row_sequence_slots[row[u]];
+        pos[u] = a.row_positions[row[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
         // lanes without a chunk read the slice start (always in bounds) and
         // drop the value, so the loads need no branch
         const uint32_t e = has_chunk ? e0 : 0u;
@@ -111,12 +119,6 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
                              (uint64_t)row[u] * a.v_row_stride + head[u] * D + e;
         kw[u] = *reinterpret_cast<const u32x4*>(ks);
         vw[u] = *reinterpret_cast<const u32x4*>(vs);
-    }
-    uint32_t slot[kUnroll], pos[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        slot[u] = a.row_sequence_slots[row[u]];
-        pos[u] = a.row_positions[row[u]];
     }
     uint32_t page[kUnroll], off[kUnroll];
     bool valid[kUnroll];

@@ -78,7 +78,9 @@ constexpr int tile_stage_bytes() {
 }
 constexpr int kTileStages = 4;
 
-template <int KVB, int D, int NW>
+// kAl16: page_tokens % 16 == 0, so every page-aligned 16-token half lies in one
+// page and its page id, base address and in-page offset are wave-uniform.
+template <int KVB, int D, int NW, bool kAl16>
 __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams p) {
     constexpr int H = 2;                 // 16-token halves per chunk
     constexpr int CT = 16 * H;           // tokens per chunk
@@ -219,20 +221,38 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
 #pragma unroll
             for (int hf = 0; hf < H; ++hf) {
                 const uint32_t tau = min(c + (uint32_t)hf * 16u + n, t_last);
-                const uint32_t page = win[tau / P - wp];
+                uint32_t page;
+                if constexpr (kAl16) {
+                    // the half's page (chunks start page-aligned), read once
+                    const uint32_t hb = min(c + (uint32_t)hf * 16u, t_last);
+                    const uint32_t pi = hb / P;
+                    page = __builtin_amdgcn_readfirstlane(win[pi - wp]);
+                    off[hf] = tau - pi * P;
+                } else {
+                    page = win[tau / P - wp];
+                    off[hf] = tau % P;
+                }
                 const bool inv = page >= a.num_pages;
                 if (inv) bad_lds = 1u;
                 pg[hf] = inv ? 0u : page;
-                off[hf] = tau % P;
             }
 #pragma unroll
             for (int t = 0; t < DPW; ++t) {
                 const uint32_t j = (wu + (uint32_t)NW * t) % (uint32_t)NI;   // scalar
                 if (j < 2u * H * NL) {
                     const uint32_t kind = j / (H * NL), hf = (j % (H * NL)) / NL, i = j % NL;
-                    const uint64_t elem = layer_base + (uint64_t)pg[hf] * a.elems_per_page +
-                                          (uint64_t)off[hf] * a.elems_per_token + (uint64_t)kv_head * D;
-                    const uint8_t* src = (kind == 0u ? k_pool : v_pool) + elem * KVB + g * 16 + i * 64;
+                    const uint8_t* src;
+                    if constexpr (kAl16) {
+                        // uniform page base + 32-bit lane offset
+                        const uint64_t base = (layer_base + (uint64_t)pg[hf] * a.elems_per_page +
+                                               (uint64_t)kv_head * D) * KVB;
+                        src = (kind == 0u ? k_pool : v_pool) + base +
+                              (off[hf] * a.elems_per_token * KVB + g * 16u + i * 64u);
+                    } else {
+                        const uint64_t elem = layer_base + (uint64_t)pg[hf] * a.elems_per_page +
+                                              (uint64_t)off[hf] * a.elems_per_token + (uint64_t)kv_head * D;
+                        src = (kind == 0u ? k_pool : v_pool) + elem * KVB + g * 16 + i * 64;
+                    }
                     load_lds<16>(src, st + kind * KV_BYTES + hf * HALF_STRIDE + i * 1024);
                 } else {
                     const uint32_t kind = (j - 2u * H * NL) & 1u, hf = (j - 2u * H * NL) >> 1;
@@ -425,19 +445,25 @@ bool tile_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
     return true;
 }
 
-template <int KVB, int D, int NW>
-hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream) {
+template <int KVB, int D, int NW, bool kAl16>
+hipError_t launch_tile_t3(const TileParams& p, uint64_t grid, hipStream_t stream) {
     const size_t lds_bytes = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * tile_stage_bytes<KVB, D>();
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_tile_kernel<KVB, D, NW>),
+            reinterpret_cast<const void*>(&paged_tile_kernel<KVB, D, NW, kAl16>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((paged_tile_kernel<KVB, D, NW>), dim3((uint32_t)grid), dim3(NW * 64), lds_bytes,
-                       stream, p);
+    hipLaunchKernelGGL((paged_tile_kernel<KVB, D, NW, kAl16>), dim3((uint32_t)grid), dim3(NW * 64),
+                       lds_bytes, stream, p);
     return hipGetLastError();
+}
+
+template <int KVB, int D, int NW>
+hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream) {
+    return (p.a.page_tokens & 15u) == 0u ? launch_tile_t3<KVB, D, NW, true>(p, grid, stream)
+                                         : launch_tile_t3<KVB, D, NW, false>(p, grid, stream);
 }
 
 // One wave per query head of the GQA group (at least 4 waves, so every SIMD

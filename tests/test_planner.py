@@ -68,3 +68,38 @@ def test_decode_runs_between_tiles():
     ks = kernels(plan)
     assert [(k[0], k[1], k[2]) for k in ks] == [(0, 0, 2), (0, 18, 3), (0, 149, 1),
                                                  (1, 2, 16), (1, 21, 128)]
+
+
+def test_prefill_tiles_unsplit_when_they_fill_the_gpu():
+    """256 prefill tiles x 4 kv heads already fill every tile slot: no split
+    (and no combine pass); 8 verify blocks alone get split-K."""
+    reqs = [(512 * i, 512, 2, 9000 + 512) for i in range(8)]
+    ks = kernels(state.plan_step(args(4096), P.KV_FP8, reqs, 16384, 256 << 20))
+    assert ks == [(1, 0, 4096, 1, 0)]
+    reqs = [(16 * i, 16, 1, 9000) for i in range(8)]
+    ks = kernels(state.plan_step(args(128), P.KV_FP8, reqs, 16384, 256 << 20))
+    assert ks[0][:3] == (1, 0, 128) and ks[0][3] > 1
+
+
+def test_request_lengths_shape_the_decode_split():
+    """Rows announced as short (max_visible per request) need fewer splits than
+    rows assumed at the step's max_visible_tokens."""
+    unknown = [(i, 1, 0) for i in range(48)]
+    short = [(i, 1, 0, 3000) for i in range(48)]
+    a = kernels(state.plan_step(args(48), P.KV_FP8, unknown, 65536, 1 << 30))[0]
+    b = kernels(state.plan_step(args(48), P.KV_FP8, short, 65536, 1 << 30))[0]
+    assert a[3] > 1 and b[3] >= 1
+    assert b[3] * b[4] < a[3] * a[4] or b[4] < a[4]
+
+
+def test_choose_decode_split_export():
+    """psk_choose_decode_split: the north-star workload splits (B=64 x 32k FP8
+    on 256 CUs), every split holds >= 16 pages, and the cap is honoured."""
+    from phaseshift_amd import ops
+    sp, pp = ops.choose_decode_split(64, 24, 4, 256, 16, True, [32768] * 64, 1 << 40)
+    assert sp > 1 and pp >= 16 and sp * pp >= 2048
+    cap = 64 * 4 * 2 * 6 * 258 * 4
+    sp, pp = ops.choose_decode_split(64, 24, 4, 256, 16, True, [32768] * 64, cap)
+    assert sp <= 2
+    sp, pp = ops.choose_decode_split(64, 24, 4, 256, 16, True, [1000] * 64, 1 << 40)
+    assert sp == 1   # below the reference's 2048-token split threshold
