@@ -46,6 +46,8 @@ extern "C" {
 /* KVCacheDType values [state/kv_cache_types.h:9-14]. */
 #define PSK_KV_BF16 0u
 #define PSK_KV_FP8_E4M3 1u
+#define PSK_KV_PSQ4_W32 3u
+#define PSK_KV_PSQ8_W32 4u
 
 /* PagedAttentionOutputDType values [paged_attention.h:37-40]. */
 #define PSK_OUT_BF16 0u
@@ -226,6 +228,61 @@ int psk_attention_paged_tile_split(const psk_paged_attention_args* a, uint32_t k
                                    const float* k_scale_pool, const float* v_scale_pool,
                                    float* partials, uint32_t splits, uint32_t pages_per_split,
                                    void* stream);
+
+/* ---- PSQ4_W32 / PSQ8_W32 KV ----------------------------------------------
+ * Pools [state/kv_cache_types.h:16-46]: blocks of 32 values of one (token,
+ * kv head); block index bi = (((layer*num_pages + page)*page_tokens + off)
+ * *kv_heads + head)*blocks_per_head + b, b = d/32. Codes at bi*16 (PSQ4:
+ * byte j = cb10 code of value j | code of value j+16 << 4) or bi*32 (PSQ8:
+ * E4M3 codes); one bf16 scale per block at bi. head_dim must equal
+ * 32*blocks_per_head (else hipErrorNotSupported, as the reference). */
+/* [kv_append.h:99-123]; estimator 0 = MaxAbs, 1 = Lsq1. */
+int psk_kv_append_psq4(const psk_kv_append_args* a, uint8_t* k_code_pool, uint8_t* v_code_pool,
+                       uint16_t* k_scale_pool, uint16_t* v_scale_pool,
+                       uint32_t blocks_per_head, uint32_t estimator, void* stream);
+int psk_kv_append_psq8(const psk_kv_append_args* a, uint8_t* k_code_pool, uint8_t* v_code_pool,
+                       uint16_t* k_scale_pool, uint16_t* v_scale_pool,
+                       uint32_t blocks_per_head, uint32_t estimator, void* stream);
+/* [attention/paged_attention.h:203-225] */
+int psk_attention_paged_psq4(const psk_paged_attention_args* a, const uint8_t* k_code_pool,
+                             const uint8_t* v_code_pool, const uint16_t* k_scale_pool,
+                             const uint16_t* v_scale_pool, uint32_t blocks_per_head,
+                             void* stream);
+int psk_attention_paged_psq8(const psk_paged_attention_args* a, const uint8_t* k_code_pool,
+                             const uint8_t* v_code_pool, const uint16_t* k_scale_pool,
+                             const uint16_t* v_scale_pool, uint32_t blocks_per_head,
+                             void* stream);
+/* [paged_attention.h:227-249]: every row attends to its own pos + 1 tokens. */
+int psk_attention_paged_prefill_psq4(const psk_paged_attention_args* a,
+                                     const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                                     const uint16_t* k_scale_pool, const uint16_t* v_scale_pool,
+                                     uint32_t blocks_per_head, void* stream);
+int psk_attention_paged_prefill_psq8(const psk_paged_attention_args* a,
+                                     const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                                     const uint16_t* k_scale_pool, const uint16_t* v_scale_pool,
+                                     uint32_t blocks_per_head, void* stream);
+/* [paged_attention.h:251-283]: q_per_kv 4 or 6, splits 2/4/8/16, as the
+ * reference; combine with psk_attention_paged_bf16_split_reduce. */
+int psk_attention_paged_psq4_split(const psk_paged_attention_args* a, const uint8_t* k_code_pool,
+                                   const uint8_t* v_code_pool, const uint16_t* k_scale_pool,
+                                   const uint16_t* v_scale_pool, uint32_t blocks_per_head,
+                                   float* partials, uint32_t splits, void* stream);
+int psk_attention_paged_psq8_split(const psk_paged_attention_args* a, const uint8_t* k_code_pool,
+                                   const uint8_t* v_code_pool, const uint16_t* k_scale_pool,
+                                   const uint16_t* v_scale_pool, uint32_t blocks_per_head,
+                                   float* partials, uint32_t splits, void* stream);
+/* Additive: kv_dtype PSK_KV_PSQ4_W32 / PSK_KV_PSQ8_W32 forms; the split form
+ * takes any q_per_kv <= 16, splits <= 1024 and pages_per_split as
+ * psk_attention_paged_fp8_e4m3_split (combine: psk_attention_paged_split_reduce_ex). */
+int psk_attention_paged_psq(const psk_paged_attention_args* a, uint32_t kv_dtype,
+                            const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                            const uint16_t* k_scale_pool, const uint16_t* v_scale_pool,
+                            uint32_t blocks_per_head, void* stream);
+int psk_attention_paged_psq_split_ex(const psk_paged_attention_args* a, uint32_t kv_dtype,
+                                     const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                                     const uint16_t* k_scale_pool, const uint16_t* v_scale_pool,
+                                     uint32_t blocks_per_head, float* partials,
+                                     uint32_t splits, uint32_t pages_per_split, void* stream);
 
 /* ---- Page-level operations ------------------------------------------------- */
 /* elem_bytes: 2 (bf16 pool), 1 (fp8 codes) or 4 (fp32 scale pool, with

@@ -56,8 +56,15 @@ def lib() -> C.CDLL:
         L.or_e4m3_decode_array.argtypes = [_u8p, _f32p, C.c_uint64]
         L.or_f32_to_bf16_array.argtypes = [_f32p, _u16p, C.c_uint64]
         for name in ("or_kv_append_bf16", "or_kv_append_fp8", "or_kv_gather",
-                     "or_paged_attention", "or_split_reduce", "or_copy_page"):
+                     "or_paged_attention", "or_split_reduce", "or_copy_page",
+                     "or_kv_append_psq", "or_paged_attention_psq"):
             getattr(L, name).restype = None
+        L.or_psq_bf16_round_array.argtypes = [_f32p, _f32p, C.c_uint64]
+        L.or_cb10_encode_array.argtypes = [_f32p, _f32p, _u8p, C.c_uint64]
+        L.or_cb10_decode.restype = C.c_float
+        L.or_cb10_decode.argtypes = [C.c_uint8]
+        L.or_psq_encode_block.restype = None
+        L.or_psq_encode_block.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, _u16p, _u8p]
     return _lib
 
 
@@ -69,6 +76,12 @@ def ref_lib():
         _ref.ref_e4m3_encode_range.argtypes = [C.c_uint32, C.c_uint32, _u8p]
         _ref.ref_e4m3_decode_all.argtypes = [_f32p]
         _ref.ref_f32_to_bf16_range.argtypes = [C.c_uint32, C.c_uint32, _u16p]
+        _ref.ref_psq4_encode_block.argtypes = [_f32p, C.c_uint32, _f32p, _u8p]
+        _ref.ref_psq4_pack_codes.argtypes = [_u8p, _u8p]
+        _ref.ref_psq_bf16_round_array.argtypes = [_f32p, _f32p, C.c_uint64]
+        _ref.ref_cb10_encode_array.argtypes = [_f32p, _f32p, _u8p, C.c_uint64]
+        _ref.ref_cb10_code_to_f32.restype = C.c_float
+        _ref.ref_cb10_code_to_f32.argtypes = [C.c_uint8]
     return _ref
 
 
@@ -98,6 +111,39 @@ def e4m3_decode(c: np.ndarray) -> np.ndarray:
     out = np.empty(c.shape, np.float32)
     lib().or_e4m3_decode_array(c.reshape(-1), out.reshape(-1), c.size)
     return out
+
+
+# ---------------------------------------------------------------- PSQ codecs
+def psq_bf16_round(x: np.ndarray) -> np.ndarray:
+    """or_psq_bf16_round (psq4_kv.h:9-18) over an array."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib().or_psq_bf16_round_array(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def cb10_encode(x: np.ndarray, inv_scale) -> np.ndarray:
+    """or_cb10_encode (psq_device.h:22-35) elementwise."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    inv = np.ascontiguousarray(np.broadcast_to(np.float32(inv_scale), x.shape), dtype=np.float32)
+    out = np.empty(x.shape, np.uint8)
+    lib().or_cb10_encode_array(x.reshape(-1), inv.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def cb10_decode(c: np.ndarray) -> np.ndarray:
+    L = lib()
+    return np.array([L.or_cb10_decode(int(v)) for v in np.asarray(c).reshape(-1)],
+                    np.float32).reshape(np.shape(c))
+
+
+def psq_encode_block(x: np.ndarray, fmt: int, lsq1: bool, device_order: bool = True):
+    """or_psq_encode_block: 32 floats -> (bf16 scale bits, 32 unpacked codes)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(32)
+    sb = np.zeros(1, np.uint16)
+    codes = np.zeros(32, np.uint8)
+    lib().or_psq_encode_block(x, fmt, int(lsq1), int(device_order), sb, codes)
+    return int(sb[0]), codes
 
 
 # --------------------------------------------------------------- arg structs
@@ -169,6 +215,28 @@ def kv_append(geom: dict, k_in: np.ndarray, v_in: np.ndarray, slots, positions,
         lib().or_kv_append_fp8(C.byref(a), _p(k_pool), _p(v_pool), _p(k_scale), _p(v_scale))
 
 
+def kv_append_psq(geom: dict, k_in: np.ndarray, v_in: np.ndarray, slots, positions,
+                  block_tables: np.ndarray, k_code: np.ndarray, v_code: np.ndarray,
+                  k_scale: np.ndarray, v_scale: np.ndarray, fmt: int, lsq1: bool,
+                  device_order: bool = True) -> None:
+    """In place: or_kv_append_psq. Code pools uint8 [blocks*16|32], scale
+    pools uint16 (bf16 bits) [blocks]; geom as kv_append."""
+    k_in = np.ascontiguousarray(k_in, np.uint16)
+    v_in = np.ascontiguousarray(v_in, np.uint16)
+    slots, positions, bt = _u32(slots), _u32(positions), _u32(block_tables)
+    a = _AppendArgs()
+    a.k_input, a.v_input = _p(k_in), _p(v_in)
+    a.k_row_stride, a.v_row_stride = k_in.shape[1], v_in.shape[1]
+    a.row_sequence_slots, a.row_positions, a.block_tables = _p(slots), _p(positions), _p(bt)
+    a.rows = k_in.shape[0]
+    for n in ("block_table_stride", "max_sequences", "layer", "page_tokens", "num_pages",
+              "num_attention_layers", "kv_heads", "head_dim"):
+        setattr(a, n, geom[n])
+    lib().or_kv_append_psq(C.byref(a), C.c_uint32(fmt), C.c_uint32(int(lsq1)),
+                           C.c_uint32(int(device_order)), _p(k_code), _p(v_code), _p(k_scale),
+                           _p(v_scale))
+
+
 def kv_gather(geom: dict, pool: np.ndarray, block_tables, seq_slots, seq_lengths,
               elems_per_token: int | None = None, elems_per_page: int | None = None,
               out: np.ndarray | None = None) -> np.ndarray:
@@ -222,6 +290,34 @@ def paged_attention(geom: dict, q: np.ndarray, slots, positions, block_tables,
     lib().or_paged_attention(C.byref(a), C.c_uint32(1 if fp8 else 0),
                              _p(np.ascontiguousarray(k_pool)), _p(np.ascontiguousarray(v_pool)),
                              _p(k_scale), _p(v_scale))
+    return out
+
+
+def paged_attention_psq(geom: dict, q: np.ndarray, slots, positions, block_tables, k_code,
+                        v_code, k_scale, v_scale, fmt: int, scale=None,
+                        output_dtype: str = "f32", out: np.ndarray | None = None) -> np.ndarray:
+    """or_paged_attention_psq: every K/V value dequantised (bf16 block scale x
+    codebook value) in fp32, then the two-pass fp32 softmax."""
+    q = np.ascontiguousarray(q, np.uint16)
+    rows = q.shape[0]
+    H, D = geom["q_heads"], geom["head_dim"]
+    if out is None:
+        out = np.zeros((rows, H * D), np.float32 if output_dtype == "f32" else np.uint16)
+    slots, positions, bt = _u32(slots), _u32(positions), _u32(block_tables)
+    a = _AttnArgs()
+    a.q, a.output = _p(q), _p(out)
+    a.output_dtype = 1 if out.dtype == np.float32 else 0
+    a.q_row_stride, a.output_row_stride = q.shape[1], out.shape[1]
+    a.row_sequence_slots, a.row_positions, a.block_tables = _p(slots), _p(positions), _p(bt)
+    a.rows = rows
+    for n in ("block_table_stride", "max_sequences", "layer", "page_tokens", "num_pages",
+              "num_attention_layers", "q_heads", "kv_heads", "head_dim"):
+        setattr(a, n, geom[n])
+    a.scale = float(scale if scale is not None else 1.0 / np.sqrt(D))
+    lib().or_paged_attention_psq(C.byref(a), C.c_uint32(fmt),
+                                 _p(np.ascontiguousarray(k_code)), _p(np.ascontiguousarray(v_code)),
+                                 _p(np.ascontiguousarray(k_scale)),
+                                 _p(np.ascontiguousarray(v_scale)))
     return out
 
 

@@ -386,3 +386,224 @@ void or_copy_page(uint8_t* dst_k, uint8_t* dst_v, float* dst_ks, float* dst_vs,
         }
     }
 }
+
+/* ------------------------------------------------------------------------- */
+/* PSQ4_W32 / PSQ8_W32 KV (blocks of 32 values, one bf16 scale per block).   */
+/* Codec: include/phaseshift/quantization/psq/psq_device.h:13-35 (cb10),     */
+/*        psq4_kv.h:9-18 (bf16 round), psq8_kv.h:12-27 (e4m3 codes).         */
+/* Append: kernels/optimized/kv_append.hip:276-643; host block encoders       */
+/*        psq4_kv.h:20-79, psq8_kv.h:29-83.                                   */
+
+/* bf16 round-to-nearest-even by bit arithmetic, as psq_bf16_round
+ * (psq4_kv.h:9-18): no NaN special case. */
+float or_psq_bf16_round(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    u &= 0xFFFF0000u;
+    float out;
+    memcpy(&out, &u, 4);
+    return out;
+}
+
+/* cb10 codebook: magnitudes {0,1,2,3,4,6,8,10}, bit 3 = sign. */
+float or_cb10_decode(uint8_t code) {
+    static const float mag[8] = {0.0f, 1.0f, 2.0f, 3.0f, 4.0f, 6.0f, 8.0f, 10.0f};
+    const float m = mag[code & 7u];
+    return (code & 8u) ? -m : m;
+}
+
+/* a = |x| * inv_scale, thresholds at the midpoints 0.5, 1.5, 2.5, 3.5, 5, 7, 9
+ * (comparisons false for NaN -> index 7, as the reference's chain). */
+uint8_t or_cb10_encode(float x, float inv_scale) {
+    const float a = (x < 0.0f ? -x : x) * inv_scale;
+    const uint8_t m = (a <= 0.5f) ? 0u : (a <= 1.5f) ? 1u : (a <= 2.5f) ? 2u : (a <= 3.5f) ? 3u
+                    : (a <= 5.0f) ? 4u : (a <= 7.0f) ? 5u : (a <= 9.0f) ? 6u : 7u;
+    return (uint8_t)(m | (x < 0.0f ? 8u : 0u));
+}
+
+static uint8_t or_psq_code(uint32_t fmt, float x, float s) {
+    if (fmt == 4u) return or_cb10_encode(x, 1.0f / s);
+    return or_e4m3_encode(x * (1.0f / s));
+}
+
+static float or_psq_value(uint32_t fmt, uint8_t c) {
+    return fmt == 4u ? or_cb10_decode(c) : or_e4m3_decode(c);
+}
+
+/* Sum of v[0..31] in the order of the device kernels' 32-lane xor butterfly
+ * (x += shfl_xor(x, o) for o = 16, 8, 4, 2, 1; every lane ends with the same
+ * bits, kv_append.hip:293-299,433-439). */
+static float or_butterfly32(const float* v) {
+    float a[32], b[32];
+    for (int i = 0; i < 32; ++i) a[i] = v[i];
+    for (int o = 16; o >= 1; o >>= 1) {
+        for (int i = 0; i < 32; ++i) b[i] = a[i] + a[i ^ o];
+        for (int i = 0; i < 32; ++i) a[i] = b[i];
+    }
+    return a[0];
+}
+
+/* One block of 32 values -> scale (bf16 bits) and 32 codes (unpacked).
+ * fmt 4: s0 = bf16(amax * 0.1f), cb10 codes of x * (1/s);
+ * fmt 8: s0 = bf16(amax * (1/448)), e4m3 SATFINITE codes of x * (1/s).
+ * lsq1: s1 = bf16(sum x q / sum q q) over the decoded codes q, then re-encode;
+ * a non-positive s1 gives scale 0 and all-zero codes. The sums follow the
+ * device kernels' butterfly order (device_order = 1) or the reference host
+ * encoders' sequential loop (device_order = 0). The first scale follows
+ * the device kernels (any positive amax; the host encoders also require
+ * amax < FLT_MAX, psq4_kv.h:28). */
+void or_psq_encode_block(const float* x, uint32_t fmt, uint32_t lsq1, uint32_t device_order,
+                         uint16_t* scale_bits, uint8_t* codes) {
+    float amax = 0.0f;   /* NaN never compares greater: dropped, as fmaxf on the device */
+    for (int i = 0; i < 32; ++i) {
+        const float ax = x[i] < 0.0f ? -x[i] : x[i];
+        if (ax > amax) amax = ax;
+    }
+    float s = 0.0f;
+    if (amax > 0.0f) s = or_psq_bf16_round(amax * (fmt == 4u ? 0.1f : (1.0f / 448.0f)));
+    for (int i = 0; i < 32; ++i) codes[i] = (s > 0.0f) ? or_psq_code(fmt, x[i], s) : 0u;
+    if (lsq1) {
+        float num[32], den[32];
+        for (int i = 0; i < 32; ++i) {
+            const float q = or_psq_value(fmt, codes[i]);
+            num[i] = x[i] * q;
+            den[i] = q * q;
+        }
+        float sn = 0.0f, sd = 0.0f;
+        if (device_order) {
+            sn = or_butterfly32(num);
+            sd = or_butterfly32(den);
+        } else {
+            for (int i = 0; i < 32; ++i) { sn += num[i]; sd += den[i]; }
+        }
+        const float sl = (sd > 0.0f) ? (sn / sd) : 0.0f;
+        float s1 = or_psq_bf16_round(sl);
+        if (!(s1 > 0.0f)) {
+            s1 = 0.0f;
+            for (int i = 0; i < 32; ++i) codes[i] = 0u;
+        } else {
+            for (int i = 0; i < 32; ++i) codes[i] = or_psq_code(fmt, x[i], s1);
+        }
+        s = s1;
+    }
+    uint32_t u;
+    memcpy(&u, &s, 4);
+    *scale_bits = (uint16_t)(u >> 16);
+}
+
+/* PSQ append: for each row and kv head, blocks b = 0..head_dim/32-1 of the
+ * head slice; block index bi = (((layer*num_pages + page)*page_tokens + off)
+ * *kv_heads + h)*blocks_per_head + b; codes at bi*16 (PSQ4, byte j = code[j] |
+ * code[j+16] << 4) or bi*32 (PSQ8), bf16 scale at bi. Skip rules as the
+ * other appends. */
+void or_kv_append_psq(const or_append_args* a, uint32_t fmt, uint32_t lsq1, uint32_t device_order,
+                      uint8_t* k_code, uint8_t* v_code, uint16_t* k_scale, uint16_t* v_scale) {
+    const uint32_t bph = a->head_dim / 32u;
+    const uint32_t cbytes = fmt == 4u ? 16u : 32u;
+    for (uint32_t row = 0; row < a->rows; ++row) {
+        uint64_t base;
+        uint32_t page, off;
+        if (!or_append_target(a, row, &base, &page, &off)) continue;
+        for (uint32_t h = 0; h < a->kv_heads; ++h) {
+            for (int t = 0; t < 2; ++t) {
+                const uint16_t* src = (t == 0 ? a->k_input : a->v_input) +
+                                      (uint64_t)row * (t == 0 ? a->k_row_stride : a->v_row_stride) +
+                                      (uint64_t)h * a->head_dim;
+                uint8_t* cp = t == 0 ? k_code : v_code;
+                uint16_t* sp = t == 0 ? k_scale : v_scale;
+                for (uint32_t b = 0; b < bph; ++b) {
+                    const uint64_t bi =
+                        ((((uint64_t)a->layer * a->num_pages + page) * a->page_tokens + off) * a->kv_heads + h) * bph + b;
+                    float x[32];
+                    for (int i = 0; i < 32; ++i) x[i] = or_bf16_to_f32(src[b * 32u + (uint32_t)i]);
+                    uint8_t codes[32];
+                    or_psq_encode_block(x, fmt, lsq1, device_order, sp + bi, codes);
+                    if (fmt == 4u) {
+                        for (int j = 0; j < 16; ++j)
+                            cp[bi * cbytes + (uint32_t)j] = (uint8_t)((codes[j] & 0xFu) | ((codes[j + 16] & 0xFu) << 4));
+                    } else {
+                        for (int j = 0; j < 32; ++j) cp[bi * cbytes + (uint32_t)j] = codes[j];
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* Dequantized value d of (block index bi): scale * codebook(code), fp32
+ * (paged_decode.hip:1206-1215 psq4_value, :1667-1673 psq8_value). */
+static float or_psq_dequant(uint32_t fmt, const uint8_t* code_pool, const uint16_t* scale_pool,
+                            uint64_t bi, uint32_t j) {
+    const float s = or_bf16_to_f32(scale_pool[bi]);
+    uint8_t c;
+    if (fmt == 4u) {
+        const uint8_t byte = code_pool[bi * 16u + (j & 15u)];
+        c = (uint8_t)(j < 16u ? (byte & 0xFu) : (byte >> 4));
+    } else {
+        c = code_pool[bi * 32u + j];
+    }
+    return s * or_psq_value(fmt, c);
+}
+
+/* Paged attention over PSQ pools: as or_paged_attention with every K and V
+ * element dequantized (scale * codebook value, fp32) before the fp32
+ * two-pass softmax (paged_decode.hip:1219-1383, 1677-1847). */
+void or_paged_attention_psq(const or_attn_args* a, uint32_t fmt, const uint8_t* k_code,
+                            const uint8_t* v_code, const uint16_t* k_scale, const uint16_t* v_scale) {
+    const uint32_t D = a->head_dim;
+    const uint32_t bph = D / 32u;
+    const uint32_t group = a->q_heads / a->kv_heads;
+    float* qv = (float*)malloc(sizeof(float) * D);
+    float* acc = (float*)malloc(sizeof(float) * D);
+    for (uint32_t row = 0; row < a->rows; ++row) {
+        const uint32_t slot = a->row_sequence_slots[row];
+        if (slot >= a->max_sequences) continue;
+        const uint64_t visible = (uint64_t)a->row_positions[row] + 1u;
+        if (visible > (uint64_t)a->block_table_stride * a->page_tokens) continue;
+        const uint32_t* bt = a->block_tables + (uint64_t)slot * a->block_table_stride;
+        for (uint32_t h = 0; h < a->q_heads; ++h) {
+            const uint32_t kvh = h / group;
+            const uint16_t* q = a->q + (uint64_t)row * a->q_row_stride + (uint64_t)h * D;
+            for (uint32_t i = 0; i < D; ++i) qv[i] = or_bf16_to_f32(q[i]);
+            float max_score = -3.402823466e+38f, sum = 0.0f;
+            int bad = 0;
+            for (int pass = 0; pass < 2 && !bad; ++pass) {
+                sum = 0.0f;
+                for (uint32_t i = 0; i < D; ++i) acc[i] = 0.0f;
+                for (uint32_t p = 0; p < visible; ++p) {
+                    const uint32_t lb = p / a->page_tokens, off = p % a->page_tokens;
+                    const uint32_t page = bt[lb];
+                    if (page >= a->num_pages) { bad = 1; break; }
+                    const uint64_t tb =
+                        ((((uint64_t)a->layer * a->num_pages + page) * a->page_tokens + off) * a->kv_heads + kvh) * bph;
+                    float sc = 0.0f;
+                    for (uint32_t i = 0; i < D; ++i)
+                        sc += qv[i] * or_psq_dequant(fmt, k_code, k_scale, tb + i / 32u, i % 32u);
+                    sc *= a->scale;
+                    if (pass == 0) {
+                        if (sc > max_score) max_score = sc;
+                    } else {
+                        const float pv = expf(sc - max_score);
+                        sum += pv;
+                        for (uint32_t i = 0; i < D; ++i)
+                            acc[i] += pv * or_psq_dequant(fmt, v_code, v_scale, tb + i / 32u, i % 32u);
+                    }
+                }
+            }
+            if (bad) continue;
+            const uint64_t ob = (uint64_t)row * a->output_row_stride + (uint64_t)h * D;
+            for (uint32_t i = 0; i < D; ++i) or_store(a, ob + i, acc[i] / sum);
+        }
+    }
+    free(qv);
+    free(acc);
+}
+
+void or_psq_bf16_round_array(const float* in, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = or_psq_bf16_round(in[i]);
+}
+
+void or_cb10_encode_array(const float* x, const float* inv, uint8_t* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = or_cb10_encode(x[i], inv[i]);
+}

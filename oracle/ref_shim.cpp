@@ -4,8 +4,15 @@
 //   ps::quantization::fpx::e4m3_encode_u8 / e4m3_decode_f32
 //       reference src/phaseshift/quantization/fpx/e4m3.cpp:45-99
 //   ps::f32_to_bf16_rne   reference include/phaseshift/core/memory/types.h:11-21
+//   ps::quantization::psq::psq4_{maxabs,lsq1}_encode_block, psq4_pack_codes,
+//   psq_bf16_round, cb10_encode / cb10_code_to_f32
+//       reference include/phaseshift/quantization/psq/psq4_kv.h:9-79,
+//       psq_device.h:13-35 (header-only host code)
+// psq8_kv.h is not built: it includes hip/hip_fp8.h, which a host compiler
+// cannot take.
 #include <phaseshift/core/memory/types.h>
 #include <phaseshift/quantization/fpx/e4m3.h>
+#include <phaseshift/quantization/psq/psq4_kv.h>
 
 #include <cstdint>
 #include <cstring>
@@ -34,5 +41,26 @@ void ref_f32_to_bf16_range(uint32_t start_bits, uint32_t count, uint16_t* out) {
         out[i] = ps::f32_to_bf16_rne(f);
     }
 }
+
+void ref_psq4_encode_block(const float* x, uint32_t lsq1, float* scale, uint8_t* codes) {
+    if (lsq1)
+        ps::quantization::psq::psq4_lsq1_encode_block(x, 32u, *scale, codes);
+    else
+        ps::quantization::psq::psq4_maxabs_encode_block(x, 32u, *scale, codes);
+}
+
+void ref_psq4_pack_codes(const uint8_t* codes32, uint8_t* bytes16) {
+    ps::quantization::psq::psq4_pack_codes(codes32, bytes16);
+}
+
+void ref_psq_bf16_round_array(const float* in, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = ps::quantization::psq::psq_bf16_round(in[i]);
+}
+
+void ref_cb10_encode_array(const float* x, const float* inv, uint8_t* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = ps::quantization::psq::cb10_encode(x[i], inv[i]);
+}
+
+float ref_cb10_code_to_f32(uint8_t c) { return ps::quantization::psq::cb10_code_to_f32(c); }
 
 }  // extern "C"

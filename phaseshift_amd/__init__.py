@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libphaseshift_kv.so")
 
 PSK_INVALID_PAGE_ID = 0xFFFFFFFF
 KV_BF16, KV_FP8 = 0, 1
+KV_PSQ4, KV_PSQ8 = 3, 4   # KVCacheDType PSQ4_W32 / PSQ8_W32
 OUT_BF16, OUT_F32 = 0, 1
 HIP_SUCCESS, HIP_INVALID_VALUE, HIP_NOT_SUPPORTED = 0, 1, 801
 
@@ -125,6 +126,16 @@ SIGNATURES = {
     "psk_attention_paged_prefill_bf16": [_P, _P, _P, _P],
     "psk_attention_paged_prefill_fp8_e4m3": [_P, _P, _P, _P, _P, _P],
     "psk_attention_paged_tile_split": [_P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _P],
+    "psk_kv_append_psq4": [_P, _P, _P, _P, _P, _U32, _U32, _P],
+    "psk_kv_append_psq8": [_P, _P, _P, _P, _P, _U32, _U32, _P],
+    "psk_attention_paged_psq4": [_P, _P, _P, _P, _P, _U32, _P],
+    "psk_attention_paged_psq8": [_P, _P, _P, _P, _P, _U32, _P],
+    "psk_attention_paged_prefill_psq4": [_P, _P, _P, _P, _P, _U32, _P],
+    "psk_attention_paged_prefill_psq8": [_P, _P, _P, _P, _P, _U32, _P],
+    "psk_attention_paged_psq4_split": [_P, _P, _P, _P, _P, _U32, _P, _U32, _P],
+    "psk_attention_paged_psq8_split": [_P, _P, _P, _P, _P, _U32, _P, _U32, _P],
+    "psk_attention_paged_psq": [_P, _U32, _P, _P, _P, _P, _U32, _P],
+    "psk_attention_paged_psq_split_ex": [_P, _U32, _P, _P, _P, _P, _U32, _P, _U32, _U32, _P],
     "psk_kv_gather": [_P, _P, _P, _U32, _P],
     "psk_kv_copy_pages": [_P, _P],
     "psk_fill_u32": [_P, _U32, C.c_uint64, _P],

@@ -14,7 +14,7 @@
 #include <vector>
 
 namespace psk {
-size_t decode_workgroup_lds_bytes(int kvb, uint32_t head_dim);
+size_t decode_workgroup_lds_bytes(uint32_t kv_dtype, uint32_t head_dim);
 uint32_t tile_workgroups_per_cu(int kvb, uint32_t head_dim, uint32_t q_per_kv);
 hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
                               const void* v, const float* ks, const float* vs,
@@ -101,7 +101,7 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
             pages[r] = std::min(max_pages, (row_visible[r] + page_tokens - 1) / page_tokens);
     const uint32_t q_per_kv = q_heads / kv_heads;
     const uint32_t groups = (kv_heads + 3u) / 4u;   // independent-wave workgroups per unit
-    const size_t lds = psk::decode_workgroup_lds_bytes(kv_bytes == 1 ? 1 : 2, head_dim);
+    const size_t lds = psk::decode_workgroup_lds_bytes(kv_bytes == 1 ? PSK_KV_FP8_E4M3 : PSK_KV_BF16, head_dim);
     const uint32_t per_cu = std::max<uint32_t>(1u, (uint32_t)((160u * 1024u) / lds));
     const uint32_t slots = std::max<uint32_t>(1u, device_cus() / kXcds) * per_cu;
     const uint64_t total_slots = (uint64_t)slots * kXcds;

@@ -8,6 +8,11 @@
 //   code = e4m3_satfinite(x / scale), scale store   kv_append.hip:148-272
 //   launcher validation                             kv_append.hip:105-115,546-558
 //
+//   PSQ4_W32 / PSQ8_W32 body: per 32-value block
+//   amax, s = bf16(amax*0.1 | amax/448), codes of x/s,
+//   LSQ1 refit s1 = bf16(sum xq / sum qq)            kv_append.hip:276-643
+//   block index, nibble packing, bf16 scale store   kv_append.hip:368-399
+//
 // Layout of the work: one "head task" = (row, kv_head). A task is handled by
 // L = lanes_per_head lanes (a power of two <= 64), each lane owning chunks of
 // 8 consecutive elements (16 B of bf16 input); a wave runs 64/L tasks. For
@@ -264,6 +269,217 @@ __global__ __launch_bounds__(256) void kv_append_generic_kernel(const AppendPara
     }
 }
 
+// ---------------------------------------------------------------- PSQ
+// One task = one 32-value block of one (row, K|V, kv head); 4 consecutive
+// lanes hold it, lane k the values 8k..8k+7 (one 16 B load). Tasks are
+// ordered (row, K|V, head, block) so a wave reads 16 consecutive blocks of
+// input and writes 16 consecutive code blocks.
+struct PsqAppendParams {
+    psk_kv_append_args a;
+    uint8_t* k_code;
+    uint8_t* v_code;
+    uint16_t* k_scale;
+    uint16_t* v_scale;
+    uint32_t bph;           // blocks per head
+    uint32_t head_blocks;   // kv_heads * bph
+    uint64_t tasks;         // rows * 2 * head_blocks
+    uint32_t vec_in;        // 16 B input loads legal
+    uint32_t vec_out;       // 8 B code stores legal
+};
+
+// psq_bf16_round (psq4_kv.h:9-18): round to bf16 by adding 0x7FFF plus the
+// kept LSB, then truncating.
+__device__ __forceinline__ float psq_bf16_round(float v) {
+    uint32_t u = __float_as_uint(v);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return __uint_as_float(u & 0xFFFF0000u);
+}
+
+// cb10_encode (psq_device.h:22-35): magnitude index of |x| * inv against the
+// midpoints 0.5 1.5 2.5 3.5 5 7 9 (NaN -> 7), sign in bit 3.
+__device__ __forceinline__ uint32_t cb10_code(float x, float inv) {
+    const float a = __builtin_fabsf(x) * inv;
+    const uint32_t m = (a <= 0.5f) ? 0u : (a <= 1.5f) ? 1u : (a <= 2.5f) ? 2u : (a <= 3.5f) ? 3u
+                     : (a <= 5.0f) ? 4u : (a <= 7.0f) ? 5u : (a <= 9.0f) ? 6u : 7u;
+    return m | (x < 0.0f ? 8u : 0u);
+}
+
+// cb10 value of a code: magnitudes 0 1 2 3 4 6 8 10.
+__device__ __forceinline__ float cb10_value(uint32_t c) {
+    const uint32_t m = c & 7u;
+    const float mag = (float)(m < 5u ? m : 2u * m - 4u);
+    return (c & 8u) ? -mag : mag;
+}
+
+// Lane k of a quad reads lane k^1 (CTRL 0xB1) or k^2 (0x4E).
+template <int CTRL>
+__device__ __forceinline__ float quad_swap(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t quad_swap_u(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+
+template <bool kPsq4>
+__device__ __forceinline__ void psq_codes(const float (&x)[8], float s, uint32_t (&c)[8]) {
+#pragma clang fp contract(off)
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = 0u;
+    if (!(s > 0.0f)) return;
+    if constexpr (kPsq4) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = cb10_code(x[i], inv);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const uint32_t w = e4m3_encode_pair(x[i] * inv, x[i + 1] * inv, 0u, false);
+            c[i] = w & 0xFFu;
+            c[i + 1] = (w >> 8) & 0xFFu;
+        }
+    }
+}
+
+template <bool kPsq4, bool kLsq1>
+__global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParams p) {
+#pragma clang fp contract(off)
+    const psk_kv_append_args& a = p.a;
+    const uint64_t task = ((uint64_t)blockIdx.x * 256u + threadIdx.x) >> 2;
+    const uint32_t k = threadIdx.x & 3u;
+    if (task >= p.tasks) return;   // a quad is one task: it leaves whole
+    const uint32_t hb = (uint32_t)(task % p.head_blocks);
+    const uint64_t rest = task / p.head_blocks;
+    const bool is_v = (rest & 1u) != 0u;
+    const uint32_t row = (uint32_t)(rest >> 1);
+
+    // row -> (page, offset), the reference skip rules (kv_append.hip:335-360)
+    const uint32_t slot = a.row_sequence_slots[row];
+    if (slot >= a.max_sequences) return;
+    const uint32_t pos = a.row_positions[row];
+    const uint32_t lb = pos / a.page_tokens;
+    if (lb >= a.block_table_stride) return;
+    const uint32_t page = a.block_tables[(uint64_t)slot * a.block_table_stride + lb];
+    if (page >= a.num_pages) return;
+    const uint32_t off = pos - lb * a.page_tokens;
+
+    const uint16_t* src = static_cast<const uint16_t*>(is_v ? a.v_input : a.k_input) +
+                          (uint64_t)row * (is_v ? a.v_row_stride : a.k_row_stride) +
+                          (uint64_t)hb * 32u + 8u * k;
+    float x[8];
+    if (p.vec_in) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = __uint_as_float(w[i] << 16);
+            x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = bf16_bits_to_f32(src[i]);
+    }
+
+    // block amax (order-free; fmaxf drops NaN as the reference's does)
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
+    amax = __builtin_fmaxf(amax, quad_swap<0xB1>(amax));
+    amax = __builtin_fmaxf(amax, quad_swap<0x4E>(amax));
+    float s = amax > 0.0f ? psq_bf16_round(amax * (kPsq4 ? 0.1f : (1.0f / 448.0f))) : 0.0f;
+    uint32_t c[8];
+    psq_codes<kPsq4>(x, s, c);
+
+    if constexpr (kLsq1) {
+        // num = sum x q, den = sum q q over the block in the order of the
+        // reference's 32-lane xor butterfly (16, 8, 4, 2, 1): value j = 8k + i,
+        // so xor 16 is lane k^2, xor 8 lane k^1, xor 4/2/1 element i^4/^2/^1.
+        float nm[8], dn[8];
+        if constexpr (kPsq4) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float q = cb10_value(c[i]);
+                nm[i] = x[i] * q;
+                dn[i] = q * q;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const f32x2 q = __builtin_amdgcn_cvt_pk_f32_fp8(c[i] | (c[i + 1] << 8), false);
+                nm[i] = x[i] * q[0];
+                dn[i] = q[0] * q[0];
+                nm[i + 1] = x[i + 1] * q[1];
+                dn[i + 1] = q[1] * q[1];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            nm[i] = nm[i] + quad_swap<0x4E>(nm[i]);
+            dn[i] = dn[i] + quad_swap<0x4E>(dn[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            nm[i] = nm[i] + quad_swap<0xB1>(nm[i]);
+            dn[i] = dn[i] + quad_swap<0xB1>(dn[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            nm[i] = nm[i] + nm[i + 4];
+            dn[i] = dn[i] + dn[i + 4];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            nm[i] = nm[i] + nm[i + 2];
+            dn[i] = dn[i] + dn[i + 2];
+        }
+        const float num = nm[0] + nm[1], den = dn[0] + dn[1];
+        const float sl = den > 0.0f ? num / den : 0.0f;
+        float s1 = psq_bf16_round(sl);
+        if (!(s1 > 0.0f)) s1 = 0.0f;
+        psq_codes<kPsq4>(x, s1, c);
+        s = s1;
+    }
+
+    const uint64_t bi = ((((uint64_t)a.layer * a.num_pages + page) * a.page_tokens + off) *
+                         a.kv_heads) * p.bph + hb;
+    uint8_t* code = is_v ? p.v_code : p.k_code;
+    if constexpr (kPsq4) {
+        // byte j = code j | code j+16 << 4: lanes 0, 1 pair with lanes 2, 3
+        uint32_t own = 0u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) own |= c[i] << (4 * i);
+        const uint32_t hi = quad_swap_u<0x4E>(own);
+        if (k < 2u) {
+            u32x2 w;
+            w[0] = 0u;
+            w[1] = 0u;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t b = ((own >> (4 * i)) & 0xFu) | (((hi >> (4 * i)) & 0xFu) << 4);
+                w[i >> 2] |= b << (8 * (i & 3));
+            }
+            uint8_t* dst = code + bi * 16u + 8u * k;
+            if (p.vec_out) {
+                *reinterpret_cast<u32x2*>(dst) = w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dst[i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+            }
+        }
+    } else {
+        u32x2 w;
+        w[0] = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+        w[1] = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+        uint8_t* dst = code + bi * 32u + 8u * k;
+        if (p.vec_out) {
+            *reinterpret_cast<u32x2*>(dst) = w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dst[i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+        }
+    }
+    if (k == 0u) (is_v ? p.v_scale : p.k_scale)[bi] = (uint16_t)(__float_as_uint(s) >> 16);
+}
+
 hipError_t validate(const psk_kv_append_args& c, const void* k_pool, const void* v_pool) {
     if (c.rows == 0u || c.head_dim == 0u || c.kv_heads == 0u) return hipErrorInvalidValue;
     if (c.page_tokens == 0u || c.block_table_stride == 0u || c.num_pages == 0u)
@@ -325,6 +541,50 @@ hipError_t launch(const AppendParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+hipError_t launch_psq(const psk_kv_append_args& c, bool psq4, uint8_t* kc, uint8_t* vc,
+                      uint16_t* ks, uint16_t* vs, uint32_t bph, uint32_t estimator,
+                      hipStream_t stream) {
+    // the reference's checks (kv_append.hip:578-590); any blocks_per_head
+    // >= 1 runs here (the reference's kernel needs exactly 8)
+    if (c.rows == 0u || c.head_dim == 0u || c.kv_heads == 0u) return hipErrorInvalidValue;
+    if (c.page_tokens == 0u || c.block_table_stride == 0u || c.num_pages == 0u)
+        return hipErrorInvalidValue;
+    if (c.k_input == nullptr || c.v_input == nullptr || c.row_sequence_slots == nullptr ||
+        c.row_positions == nullptr || c.block_tables == nullptr || kc == nullptr || vc == nullptr ||
+        ks == nullptr || vs == nullptr)
+        return hipErrorInvalidValue;
+    if (bph == 0u || c.head_dim != 32u * bph) return hipErrorNotSupported;
+    if (estimator > 1u) return hipErrorInvalidValue;
+    PsqAppendParams p{};
+    p.a = c;
+    p.k_code = kc;
+    p.v_code = vc;
+    p.k_scale = ks;
+    p.v_scale = vs;
+    p.bph = bph;
+    p.head_blocks = c.kv_heads * bph;
+    p.tasks = (uint64_t)c.rows * 2u * p.head_blocks;
+    auto al = [](const void* ptr, uintptr_t n) { return reinterpret_cast<uintptr_t>(ptr) % n == 0u; };
+    p.vec_in = (c.k_row_stride % 8u == 0u && c.v_row_stride % 8u == 0u && al(c.k_input, 16) &&
+                al(c.v_input, 16)) ? 1u : 0u;
+    p.vec_out = (al(kc, 8) && al(vc, 8)) ? 1u : 0u;
+    const uint64_t blocks = (p.tasks * 4u + 255u) / 256u;
+    if (blocks == 0u || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    const dim3 grid((uint32_t)blocks);
+    if (psq4) {
+        if (estimator == 1u)
+            hipLaunchKernelGGL((kv_append_psq_kernel<true, true>), grid, dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL((kv_append_psq_kernel<true, false>), grid, dim3(256), 0, stream, p);
+    } else {
+        if (estimator == 1u)
+            hipLaunchKernelGGL((kv_append_psq_kernel<false, true>), grid, dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL((kv_append_psq_kernel<false, false>), grid, dim3(256), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace psk
 
@@ -349,6 +609,24 @@ extern "C" int psk_kv_append_fp8_e4m3(const psk_kv_append_args* a, void* k_pool,
         static_cast<hipStream_t>(stream));
 }
 
+extern "C" int psk_kv_append_psq4(const psk_kv_append_args* a, uint8_t* k_code_pool,
+                                  uint8_t* v_code_pool, uint16_t* k_scale_pool,
+                                  uint16_t* v_scale_pool, uint32_t blocks_per_head,
+                                  uint32_t estimator, void* stream) {
+    if (a == nullptr) return hipErrorInvalidValue;
+    return psk::launch_psq(*a, true, k_code_pool, v_code_pool, k_scale_pool, v_scale_pool,
+                           blocks_per_head, estimator, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int psk_kv_append_psq8(const psk_kv_append_args* a, uint8_t* k_code_pool,
+                                  uint8_t* v_code_pool, uint16_t* k_scale_pool,
+                                  uint16_t* v_scale_pool, uint32_t blocks_per_head,
+                                  uint32_t estimator, void* stream) {
+    if (a == nullptr) return hipErrorInvalidValue;
+    return psk::launch_psq(*a, false, k_code_pool, v_code_pool, k_scale_pool, v_scale_pool,
+                           blocks_per_head, estimator, static_cast<hipStream_t>(stream));
+}
+
 // ------------------------------------------------- reference C++ signatures
 namespace ps::kernel {
 
@@ -366,6 +644,26 @@ hipError_t launch_kv_append_fp8_e4m3(const KvAppendCommonArgs& common,
     return static_cast<hipError_t>(
         psk_kv_append_fp8_e4m3(reinterpret_cast<const psk_kv_append_args*>(&common), k_pool,
                                v_pool, k_scale_pool, v_scale_pool, stream));
+}
+
+hipError_t launch_kv_append_psq4(const KvAppendCommonArgs& common, uint8_t* k_code_pool,
+                                 uint8_t* v_code_pool, bf16_t* k_scale_pool, bf16_t* v_scale_pool,
+                                 uint32_t blocks_per_head,
+                                 ::ps::qwen35::Psq4ScaleEstimator estimator, hipStream_t stream) {
+    return static_cast<hipError_t>(psk_kv_append_psq4(
+        reinterpret_cast<const psk_kv_append_args*>(&common), k_code_pool, v_code_pool,
+        reinterpret_cast<uint16_t*>(k_scale_pool), reinterpret_cast<uint16_t*>(v_scale_pool),
+        blocks_per_head, static_cast<uint32_t>(estimator), stream));
+}
+
+hipError_t launch_kv_append_psq8(const KvAppendCommonArgs& common, uint8_t* k_code_pool,
+                                 uint8_t* v_code_pool, bf16_t* k_scale_pool, bf16_t* v_scale_pool,
+                                 uint32_t blocks_per_head,
+                                 ::ps::qwen35::Psq8ScaleEstimator estimator, hipStream_t stream) {
+    return static_cast<hipError_t>(psk_kv_append_psq8(
+        reinterpret_cast<const psk_kv_append_args*>(&common), k_code_pool, v_code_pool,
+        reinterpret_cast<uint16_t*>(k_scale_pool), reinterpret_cast<uint16_t*>(v_scale_pool),
+        blocks_per_head, static_cast<uint32_t>(estimator), stream));
 }
 
 }  // namespace ps::kernel

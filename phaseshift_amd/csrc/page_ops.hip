@@ -219,6 +219,89 @@ __global__ __launch_bounds__(256) void generic_attention_kernel(const psk_paged_
     }
 }
 
+// PSQ8_W32 / PSQ4_W32 KV, same formulation: every value dequantised as
+// bf16 block scale x codebook value in fp32 (paged_decode.hip:1206-1215,
+// 1667-1673); block index bi = (token, head) slice * D/32 + d/32.
+template <bool kPsq4>
+__global__ __launch_bounds__(256) void generic_attention_psq_kernel(
+    const psk_paged_attention_args a, const uint8_t* kp, const uint8_t* vp, const uint16_t* ksc,
+    const uint16_t* vsc) {
+    const uint64_t task = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    if (task >= (uint64_t)a.rows * a.q_heads) return;
+    const uint32_t row = (uint32_t)(task / a.q_heads);
+    const uint32_t qh = (uint32_t)(task % a.q_heads);
+    const uint32_t kvh = qh / (a.q_heads / a.kv_heads);
+    const uint32_t slot = a.row_sequence_slots[row];
+    if (slot >= a.max_sequences) return;
+    const uint64_t vis64 = (uint64_t)a.row_positions[row] + 1u;
+    if (vis64 > (uint64_t)a.block_table_stride * a.page_tokens) return;
+    const uint32_t visible = (uint32_t)vis64;
+    const uint32_t D = a.head_dim;
+    const uint32_t bph = D / 32u;
+    const uint32_t* bt = a.block_tables + (uint64_t)slot * a.block_table_stride;
+    const uint16_t* q = static_cast<const uint16_t*>(a.q) + (uint64_t)row * a.q_row_stride +
+                        (uint64_t)qh * D;
+    float qv[4], acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t d = lane + 64u * j;
+        qv[j] = d < D ? bf16_bits_to_f32(q[d]) : 0.0f;
+        acc[j] = 0.0f;
+    }
+    auto value = [&](const uint8_t* pool, const uint16_t* scl, uint64_t bi, uint32_t j) {
+        uint32_t c;
+        if constexpr (kPsq4) {
+            const uint32_t byte = pool[bi * 16u + (j & 15u)];
+            c = j < 16u ? (byte & 0xFu) : (byte >> 4);
+            const uint32_t mi = c & 7u;
+            const float mag = mi < 5u ? (float)mi : (float)(2u * mi - 4u);   // 0,1,2,3,4,6,8,10
+            return bf16_bits_to_f32(scl[bi]) * ((c & 8u) ? -mag : mag);
+        } else {
+            c = pool[bi * 32u + j];
+            return bf16_bits_to_f32(scl[bi]) * __builtin_amdgcn_cvt_pk_f32_fp8(c, false)[0];
+        }
+    };
+    float m = -INFINITY, l = 0.0f;
+    const float sl = a.scale * kLog2e;
+    for (uint32_t t = 0; t < visible; ++t) {
+        const uint32_t page = bt[t / a.page_tokens];
+        if (page >= a.num_pages) return;   // output left unwritten
+        const uint64_t tb = ((((uint64_t)a.layer * a.num_pages + page) * a.page_tokens +
+                              t % a.page_tokens) * a.kv_heads + kvh) * bph;
+        float kf[4], vf[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t d = lane + 64u * j;
+            kf[j] = d < D ? value(kp, ksc, tb + d / 32u, d % 32u) : 0.0f;
+            vf[j] = d < D ? value(vp, vsc, tb + d / 32u, d % 32u) : 0.0f;
+        }
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dot += qv[j] * kf[j];
+        dot = wave_sum(dot);
+        const float s = dot * sl;
+        const float mn = __builtin_fmaxf(m, s);
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        const float w = __builtin_amdgcn_exp2f(s - mn);
+        l = l * alpha + w;
+        m = mn;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = acc[j] * alpha + w * vf[j];
+    }
+    const uint64_t ob = (uint64_t)row * a.output_row_stride + (uint64_t)qh * D;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t d = lane + 64u * j;
+        if (d >= D) continue;
+        const float r = acc[j] / l;
+        if (a.output_dtype == PSK_OUT_F32)
+            static_cast<float*>(a.output)[ob + d] = r;
+        else
+            static_cast<uint16_t*>(a.output)[ob + d] = f32_to_bf16_bits(r);
+    }
+}
+
 // ------------------------------------------------- encoder self-test
 // Encodes the floats with bit patterns start .. start+count-1 through the same
 // e4m3_encode_pair the append kernel uses (pairs land in bytes 0-3 of a word
@@ -253,6 +336,23 @@ hipError_t launch_attention_generic(const psk_paged_attention_args& c, int kvb, 
     else
         hipLaunchKernelGGL(generic_attention_kernel<1>, dim3((uint32_t)blocks), dim3(256), 0, stream,
                            c, static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v), ks, vs);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_generic_psq(const psk_paged_attention_args& c, bool psq4, const void* k,
+                                        const void* v, const uint16_t* ks, const uint16_t* vs,
+                                        hipStream_t stream) {
+    const uint64_t waves = (uint64_t)c.rows * c.q_heads;
+    const uint64_t blocks = (waves + 3u) / 4u;
+    if (blocks == 0u || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    if (psq4)
+        hipLaunchKernelGGL(generic_attention_psq_kernel<true>, dim3((uint32_t)blocks), dim3(256), 0,
+                           stream, c, static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v),
+                           ks, vs);
+    else
+        hipLaunchKernelGGL(generic_attention_psq_kernel<false>, dim3((uint32_t)blocks), dim3(256), 0,
+                           stream, c, static_cast<const uint8_t*>(k), static_cast<const uint8_t*>(v),
+                           ks, vs);
     return hipGetLastError();
 }
 

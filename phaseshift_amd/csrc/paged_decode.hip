@@ -1,28 +1,34 @@
-// Paged-attention decode over GQA KV pages, BF16 or FP8 E4M3 KV, gfx950.
+// Paged-attention decode over GQA KV pages, gfx950: BF16, FP8 E4M3, PSQ8_W32
+// or PSQ4_W32 KV.
 //
 // Reference behaviour restated (file:line in the reference repository):
 //   visibility (pos + 1), row skip rules, invalid page  paged_decode.hip:79-97,123-128
 //   BF16 math  s = scale*q.k, online softmax, out = acc/sum   paged_decode.hip:135-205
 //   FP8 math   s = (q.dec(k))*k_scale*scale,
 //              acc += (p*v_scale)*dec(v)                     paged_decode.hip:1064-1090
+//   PSQ math   k, v = bf16 scale of the 32-value block x codebook value,
+//              fp32 attention over the dequantised values   paged_decode.hip:1206-1383,1667-1847
 //   split rule per = ceil(pages/splits), partial (m, P, A)   paged_decode.hip:315-320,413-471
 //   combine g = max m_s, W_s = e^(m_s-g),
 //           out = sum W_s A_s / sum W_s P_s                  paged_decode.hip:474-555
-//   launcher validation                                      paged_decode.hip:228-259,787-817
+//   launcher validation                                      paged_decode.hip:228-259,787-817,
+//                                                            1588-1610,2098-2127
 //
-// MI355X design. One workgroup = (row, kv_head, split), 4 waves. The whole GQA
-// group (q_per_kv <= 16 query heads) is the N=16 side of
-// v_mfma_f32_16x16x32_bf16, so each K/V byte is read from HBM once per
+// MI355X design. The whole GQA group (q_per_kv <= 16 query heads) is the N=16
+// side of v_mfma_f32_16x16x32_bf16, so each K/V byte is read from HBM once per
 // (row, kv_head) instead of once per query head:
 //   S^T[16 tokens x 16 heads] = K[16 x D] * Q^T[D x 16]   (D/32 MFMAs)
 //   O^T[16 dims x 16 heads]  += V^T[16 x 32 tokens] * P^T[32 tokens x 16 heads]
-// Each wave owns 32-token chunks (round robin), keeps its own online-softmax
-// state in log2 units, and the 4 waves merge through LDS at the end. K is read
-// straight into MFMA A-operand registers (lane = token, 16 B per load, every
-// 64 B token segment read whole by 4 lanes); V is transposed through a
-// per-wave LDS tile so that a lane holds 8 tokens of one dim. FP8 codes become
-// bf16 exactly (v_cvt_scalef32_pk_bf16_fp8); k_scale multiplies the score and
-// v_scale is folded into P before PV.
+// A wave owns one kv head of a (row, split) and streams 32-token chunks of K,
+// V and scales into LDS with LDS DMA, two chunks in flight; the K operand is
+// read from LDS row-wise, the V operand with the transposing LDS reads.
+// FP8 codes become bf16 exactly (v_cvt_scalef32_pk_bf16_fp8); k_scale
+// multiplies the score and v_scale is folded into P before PV.
+// PSQ: each K-step of the score product is exactly one 32-value block, so its
+// partial score is multiplied by that block's K scale in fp32; P is multiplied
+// by the V scale of each block before the PV MFMAs of the block's 32 dims.
+// PSQ4 nibbles become E4M3 codes of the same value (v_perm table) and then
+// bf16 exactly, so no product is rounded before the fp32 accumulation.
 #include "device_common.h"
 
 #include <phaseshift_kv/paged_attention.h>
@@ -32,12 +38,24 @@
 namespace psk {
 namespace {
 
+// KV formats of the decode kernel.
+constexpr int kFmtBf16 = 0;   // bf16 values
+constexpr int kFmtFp8 = 1;    // E4M3 codes, one f32 scale per (token, kv head)
+constexpr int kFmtPsq8 = 2;   // E4M3 codes, one bf16 scale per 32-value block
+constexpr int kFmtPsq4 = 3;   // cb10 nibbles, one bf16 scale per 32-value block
+
+template <int FMT>
+constexpr bool fmt_psq() { return FMT == kFmtPsq8 || FMT == kFmtPsq4; }
+// bytes of one (token, kv head) K (or V) slice
+template <int FMT, int D>
+constexpr int code_bytes() { return FMT == kFmtBf16 ? 2 * D : FMT == kFmtPsq4 ? D / 2 : D; }
+
 struct DecodeParams {
     psk_paged_attention_args a;
     const uint8_t* k_pool;
     const uint8_t* v_pool;
-    const float* k_scale;
-    const float* v_scale;
+    const void* k_scale;      // FP8: f32 per (token, head); PSQ: bf16 per block
+    const void* v_scale;
     float* partials;          // nullptr: write the output directly
     uint32_t splits;
     uint32_t pages_per_split; // 0: ceil(pages / splits) per row
@@ -64,8 +82,31 @@ __device__ __forceinline__ bf16x8 load_q8(const uint16_t* q, bool ok) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
-template <int KVB>
-constexpr int chunk_halves() { return KVB == 1 ? 2 : 1; }   // 16-token halves per chunk
+template <int FMT>
+constexpr int chunk_halves() { return FMT == kFmtBf16 ? 1 : 2; }   // 16-token halves per chunk
+
+// Q fragment of a PSQ4 K-step: dims d0..d0+3 and d0+16..d0+19 (the low and
+// high nibbles of 4 code bytes), zeros past the group.
+__device__ __forceinline__ bf16x8 load_q4x2(const uint16_t* q, bool ok) {
+    u32x4 r = {0u, 0u, 0u, 0u};
+    if (ok) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            r[i] = (uint32_t)q[2 * i] | ((uint32_t)q[2 * i + 1] << 16);
+            r[2 + i] = (uint32_t)q[16 + 2 * i] | ((uint32_t)q[16 + 2 * i + 1] << 16);
+        }
+    }
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// The E4M3 codes of the cb10 values of 4 PSQ4 code bytes, low nibbles (hi =
+// false) or high nibbles: magnitude index -> E4M3 code of {0,1,2,3,4,6,8,10}
+// by byte permute, the nibble's sign bit -> bit 7.
+__device__ __forceinline__ uint32_t psq4_e4m3x4(uint32_t x, bool hi) {
+    const uint32_t idx = (hi ? (x >> 4) : x) & 0x07070707u;
+    const uint32_t mag = __builtin_amdgcn_perm(0x52504C48u, 0x44403800u, idx);
+    return mag | ((hi ? x : (x << 4)) & 0x80808080u);
+}
 
 typedef __attribute__((ext_vector_type(2))) int i32x2;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
@@ -175,10 +216,12 @@ __device__ bool find_unit(const psk_paged_attention_args& a, uint32_t splits, ui
 constexpr uint32_t kPageWindow = 1024;   // block-table entries staged in LDS per pass
 
 // LDS bytes of one pipeline stage of one wave: K and V of a chunk (lane-major
-// DMA layout) and, FP8, the k/v scales of its tokens.
-template <int KVB, int D>
+// DMA layout) and, FP8 and PSQ, the k/v scales of its tokens (256 B per
+// 16-token half).
+template <int FMT, int D>
 constexpr int stage_bytes() {
-    return 2 * chunk_halves<KVB>() * (16 * D * KVB + 128) + (KVB == 1 ? 2 * chunk_halves<KVB>() * 256 : 0);
+    return 2 * chunk_halves<FMT>() * (16 * code_bytes<FMT, D>() + 128) +
+           (FMT != kFmtBf16 ? 2 * chunk_halves<FMT>() * 256 : 0);
 }
 
 // kIndep: the 4 waves of a workgroup are 4 independent items, the kv heads
@@ -186,22 +229,28 @@ constexpr int stage_bytes() {
 // head slices of each token row) and need no merge. Otherwise the 4 waves
 // share one (row, kv_head, split) item, take its chunks round robin and merge
 // through LDS at the end (used when the independent grid cannot fill the GPU).
-template <int KVB, int D, bool kIndep, int NW>
+template <int FMT, int D, bool kIndep, int NW>
 __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParams p) {
     constexpr uint32_t NT = NW * 64;   // threads of the workgroup
     static_assert(kIndep || NW == kWaves, "the shared-item merge uses 4 waves");
-    constexpr int H = chunk_halves<KVB>();
+    constexpr int KVB = FMT == kFmtBf16 ? 2 : 1;
+    constexpr bool kPsq = fmt_psq<FMT>();
+    constexpr int CB = code_bytes<FMT, D>();   // K (V) bytes of one token's head slice
+    constexpr int H = chunk_halves<FMT>();
     constexpr int CT = 16 * H;         // tokens per chunk
-    constexpr int NL = D * KVB / 64;   // 16 B loads per lane per 16-token half
+    constexpr int NL = CB / 64;        // 16 B loads per lane per 16-token half
     constexpr int NS = D / 32;         // MFMA K-steps of the score product
     constexpr int NDB = D / 16;        // 16-dim blocks of the output
     // a 16-token half of K (V) in LDS, padded by 128 B so that the two halves
     // of a chunk fall on opposite halves of the 64 LDS banks (the transposing
     // V reads of one instruction touch both)
-    constexpr int HALF_STRIDE = 16 * D * KVB + 128;
+    constexpr int HALF_STRIDE = 16 * CB + 128;
     constexpr int KV_BYTES = H * HALF_STRIDE;               // K (or V) of one chunk
     constexpr int SC_BYTES = KVB == 1 ? H * 256 : 0;       // k (or v) scales of one chunk
-    constexpr int STAGE = stage_bytes<KVB, D>();
+    constexpr int STAGE = stage_bytes<FMT, D>();
+    // PSQ: dwords of block scales per token head (2 bf16 each); the scales of
+    // a 16-token half sit dword-major in LDS: dword w of token t at 64w + 4t
+    constexpr int SW = D / 64;
     constexpr int kWinBytes = (int)kPageWindow * 4;
     // vector-memory operations of one issue(): K and V DMAs and the scale DMAs
     constexpr int kStepOps = H * (2 * NL + (KVB == 1 ? 2 : 0));
@@ -252,8 +301,14 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
                                (uint64_t)(kvh * qpk + (hv ? n : 0u)) * D;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            const int d0 = KVB == 2 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
-            qf[s] = load_q8(qrow + d0, hv);
+            if constexpr (FMT == kFmtPsq4) {
+                qf[s] = load_q4x2(qrow + s * 32 + (int)g * 4, hv);
+            } else {
+                const int d0 = (FMT == kFmtBf16 || FMT == kFmtPsq8)
+                                   ? s * 32 + (int)g * 8
+                                   : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
+                qf[s] = load_q8(qrow + d0, hv);
+            }
         }
     }
 
@@ -313,19 +368,30 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
                 bad |= inv;
                 page = inv ? 0u : page;
                 const uint32_t off = tau % P;
-                const uint64_t elem = layer_base + (uint64_t)page * a.elems_per_page +
-                                      (uint64_t)off * a.elems_per_token + (uint64_t)kvh * D;
-                const uint8_t* ks = p.k_pool + elem * KVB + g * 16;
-                const uint8_t* vs = p.v_pool + elem * KVB + g * 16;
+                // FP8 scale index; PSQ (token, head) slice index
+                const uint64_t si = ((scale_layer + page) * P + off) * a.kv_heads + kvh;
+                const uint64_t cbase =
+                    kPsq ? si * CB
+                         : (layer_base + (uint64_t)page * a.elems_per_page +
+                            (uint64_t)off * a.elems_per_token + (uint64_t)kvh * D) * KVB;
+                const uint8_t* ks = p.k_pool + cbase + g * 16;
+                const uint8_t* vs = p.v_pool + cbase + g * 16;
 #pragma unroll
                 for (int i = 0; i < NL; ++i) load_lds<16>(ks + i * 64, st + hf * HALF_STRIDE + i * 1024);
 #pragma unroll
                 for (int i = 0; i < NL; ++i)
                     load_lds<16>(vs + i * 64, st + KV_BYTES + hf * HALF_STRIDE + i * 1024);
-                if constexpr (KVB == 1) {
-                    const uint64_t si = ((scale_layer + page) * P + off) * a.kv_heads + kvh;
-                    load_lds<4>(p.k_scale + si, st + 2 * KV_BYTES + hf * 256);
-                    load_lds<4>(p.v_scale + si, st + 2 * KV_BYTES + SC_BYTES + hf * 256);
+                if constexpr (FMT == kFmtFp8) {
+                    load_lds<4>(static_cast<const float*>(p.k_scale) + si, st + 2 * KV_BYTES + hf * 256);
+                    load_lds<4>(static_cast<const float*>(p.v_scale) + si,
+                                st + 2 * KV_BYTES + SC_BYTES + hf * 256);
+                } else if constexpr (kPsq) {
+                    // lane (n, g): dword g of token n's block scales (lane
+                    // groups past SW repeat a dword into unused LDS)
+                    const uint64_t sb = si * (uint64_t)(4 * SW) + 4u * (g % (uint32_t)SW);
+                    load_lds<4>(static_cast<const uint8_t*>(p.k_scale) + sb, st + 2 * KV_BYTES + hf * 256);
+                    load_lds<4>(static_cast<const uint8_t*>(p.v_scale) + sb,
+                                st + 2 * KV_BYTES + SC_BYTES + hf * 256);
                 }
             }
         };
@@ -336,17 +402,54 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
 #pragma unroll
             for (int hf = 0; hf < H; ++hf) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                const uint8_t* kb = st + hf * HALF_STRIDE + 16 * lane;
+                if constexpr (kPsq) {
+                    // K-step s = block s: its partial scores times the block's
+                    // K scale of each token 4g + r (bf16 -> f32 by shift).
+                    const uint8_t* kb = st + hf * HALF_STRIDE;
+                    const uint8_t* kscl = st + 2 * KV_BYTES + hf * 256 + 16 * g;
 #pragma unroll
-                for (int s = 0; s < NS; ++s) {
-                    bf16x8 kf;
-                    if constexpr (KVB == 2) {
-                        kf = *reinterpret_cast<const bf16x8*>(kb + 1024 * s);
-                    } else {
-                        const u32x4 w = *reinterpret_cast<const u32x4*>(kb + 1024 * (s >> 1));
-                        kf = (s & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
+                    for (int s = 0; s < NS; ++s) {
+                        bf16x8 kf;
+                        if constexpr (FMT == kFmtPsq8) {
+                            // bytes 32s + 8g .. +8 of token n
+                            const u32x2 w = *reinterpret_cast<const u32x2*>(
+                                kb + 1024 * (s >> 1) + 16 * (16 * (2 * (s & 1) + (int)(g >> 1)) + (int)n) +
+                                8 * (int)(g & 1u));
+                            kf = fp8x8_to_bf16x8(w[0], w[1]);
+                        } else {
+                            // bytes 16s + 4g .. +4 of token n: dims 4g.. (low
+                            // nibbles) and 16 + 4g.. (high nibbles) of block s
+                            const uint32_t x = *reinterpret_cast<const uint32_t*>(kb + 256 * s + 16 * n + 4 * g);
+                            const uint32_t lo = psq4_e4m3x4(x, false), hi = psq4_e4m3x4(x, true);
+                            u32x4 r;
+                            r[0] = fp8x2_to_bf16x2(lo, false);
+                            r[1] = fp8x2_to_bf16x2(lo, true);
+                            r[2] = fp8x2_to_bf16x2(hi, false);
+                            r[3] = fp8x2_to_bf16x2(hi, true);
+                            kf = __builtin_bit_cast(bf16x8, r);
+                        }
+                        const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            kf, qf[s], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        const u32x4 kw = *reinterpret_cast<const u32x4*>(kscl + 64 * (s >> 1));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float ksc = __uint_as_float((s & 1) ? (kw[r] & 0xFFFF0000u) : (kw[r] << 16));
+                            acc[r] = s == 0 ? part[r] * ksc : __builtin_fmaf(part[r], ksc, acc[r]);
+                        }
                     }
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
+                } else {
+                    const uint8_t* kb = st + hf * HALF_STRIDE + 16 * lane;
+#pragma unroll
+                    for (int s = 0; s < NS; ++s) {
+                        bf16x8 kf;
+                        if constexpr (KVB == 2) {
+                            kf = *reinterpret_cast<const bf16x8*>(kb + 1024 * s);
+                        } else {
+                            const u32x4 w = *reinterpret_cast<const u32x4*>(kb + 1024 * (s >> 1));
+                            kf = (s & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
+                        }
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
+                    }
                 }
                 sc[hf] = acc;
             }
@@ -357,7 +460,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
 #pragma unroll
             for (int hf = 0; hf < H; ++hf) {
                 f32x4 kscale = {1.f, 1.f, 1.f, 1.f}, vscale = {1.f, 1.f, 1.f, 1.f};
-                if constexpr (KVB == 1) {
+                if constexpr (FMT == kFmtFp8) {
                     kscale = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + hf * 256 + 16 * g);
                     vscale = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + SC_BYTES + hf * 256 +
                                                              16 * g);
@@ -397,7 +500,45 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
             // two MFMAs keep ~16 mantissa bits of every weight (V and K are
             // exact in bf16).
             const uint8_t* vb = st + KV_BYTES + tr_off;
-            if constexpr (KVB == 1) {
+            if constexpr (kPsq) {
+                // Per block b: P times the block's V scale of each token (the
+                // lane's tokens 4g + r of both halves), one bf16 P operand,
+                // then the MFMAs of the block's two 16-dim output blocks.
+                const uint8_t* vscl = st + 2 * KV_BYTES + SC_BYTES + 16 * g;
+#pragma unroll
+                for (int b = 0; b < NS; ++b) {
+                    const u32x4 w0 = *reinterpret_cast<const u32x4*>(vscl + 64 * (b >> 1));
+                    const u32x4 w1 = *reinterpret_cast<const u32x4*>(vscl + 256 + 64 * (b >> 1));
+                    float f[8];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        f[r] = pv[0][r] * __uint_as_float((b & 1) ? (w0[r] & 0xFFFF0000u) : (w0[r] << 16));
+                        f[4 + r] = pv[1][r] * __uint_as_float((b & 1) ? (w1[r] & 0xFFFF0000u) : (w1[r] << 16));
+                    }
+                    u32x4 ph;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) ph[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+                    const bf16x8 pf = __builtin_bit_cast(bf16x8, ph);
+                    if constexpr (FMT == kFmtPsq8) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const i32x2 w = lds_read_tr8(vb + 256 * (2 * b + h));
+                            const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
+                            o[2 * b + h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[2 * b + h], 0, 0, 0);
+                        }
+                    } else {
+                        // byte i of block b for 8 tokens: dim i (low nibble)
+                        // and dim 16 + i (high nibble)
+                        const i32x2 w = lds_read_tr8(vb + 256 * b);
+                        const bf16x8 vlo = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)w[0], false),
+                                                           psq4_e4m3x4((uint32_t)w[1], false));
+                        const bf16x8 vhi = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)w[0], true),
+                                                           psq4_e4m3x4((uint32_t)w[1], true));
+                        o[2 * b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vlo, pf, o[2 * b], 0, 0, 0);
+                        o[2 * b + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vhi, pf, o[2 * b + 1], 0, 0, 0);
+                    }
+                }
+            } else if constexpr (KVB == 1) {
                 u32x4 ph, pl;
                 { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
                 { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
@@ -656,21 +797,24 @@ bool mfma_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
 
 // LDS bytes of one independent-wave decode workgroup (the split chooser
 // derives workgroups per CU from it).
-size_t decode_workgroup_lds_bytes(int kvb, uint32_t head_dim) {
+// kv_dtype: PSK_KV_*.
+size_t decode_workgroup_lds_bytes(uint32_t kv_dtype, uint32_t head_dim) {
     const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
-    const size_t H = kvb == 1 ? 2 : 1;
-    const size_t stage = 2 * H * (16 * D * kvb + 128) + (kvb == 1 ? 2 * H * 256 : 0);
+    const bool bf16 = kv_dtype == PSK_KV_BF16;
+    const size_t H = bf16 ? 1 : 2;
+    const size_t cb = bf16 ? 2 * D : kv_dtype == PSK_KV_PSQ4_W32 ? D / 2 : D;
+    const size_t stage = 2 * H * (16 * cb + 128) + (bf16 ? 0 : 2 * H * 256);
     return (size_t)kPageWindow * 4 + (size_t)kWaves * 2 * stage;
 }
 
 namespace {
 
-template <int KVB, int D, bool kIndep, int NW>
+template <int FMT, int D, bool kIndep, int NW>
 hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     // block-table window + two pipeline stages per wave; the shared-item merge
     // later reuses the same LDS
-    const size_t v_bytes = (size_t)kPageWindow * 4 + (size_t)NW * 2 * stage_bytes<KVB, D>();
+    const size_t v_bytes = (size_t)kPageWindow * 4 + (size_t)NW * 2 * stage_bytes<FMT, D>();
     const size_t m_bytes = kIndep ? 0 : (size_t)NW * 32 * sizeof(float) +
                                             (size_t)NW * qpk * D * sizeof(float);
     const size_t lds_bytes = v_bytes > m_bytes ? v_bytes : m_bytes;
@@ -678,11 +822,11 @@ hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t st
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_decode_kernel<KVB, D, kIndep, NW>),
+            reinterpret_cast<const void*>(&paged_decode_kernel<FMT, D, kIndep, NW>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((paged_decode_kernel<KVB, D, kIndep, NW>), dim3((uint32_t)grid),
+    hipLaunchKernelGGL((paged_decode_kernel<FMT, D, kIndep, NW>), dim3((uint32_t)grid),
                        dim3(NW * 64), lds_bytes, stream, p);
     return hipGetLastError();
 }
@@ -690,22 +834,24 @@ hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t st
 // Independent waves (one kv head each) when that grid fills at least half of
 // the GPU's 256 CUs; otherwise the 4 waves share each (row, kv_head, split)
 // item. The split chooser assumes the same rule.
-template <int KVB, int D>
+template <int FMT, int D>
 hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
     const uint64_t units = (uint64_t)p.a.rows * p.splits;
     const uint64_t groups = (p.a.kv_heads + kWaves - 1u) / kWaves;
-    if (units * groups >= 128u) return launch_decode_t2<KVB, D, true, kWaves>(p, units * groups, stream);
-    return launch_decode_t2<KVB, D, false, kWaves>(p, units * p.a.kv_heads, stream);
+    if (units * groups >= 128u) return launch_decode_t2<FMT, D, true, kWaves>(p, units * groups, stream);
+    return launch_decode_t2<FMT, D, false, kWaves>(p, units * p.a.kv_heads, stream);
 }
 
-template <int KVB>
+template <int FMT>
 hipError_t launch_decode(const DecodeParams& p, hipStream_t stream) {
     switch (p.a.head_dim) {
-        case 256: return launch_decode_t<KVB, 256>(p, stream);
-        case 128: return launch_decode_t<KVB, 128>(p, stream);
-        case 64: return launch_decode_t<KVB, 64>(p, stream);
+        case 256: return launch_decode_t<FMT, 256>(p, stream);
+        case 128: return launch_decode_t<FMT, 128>(p, stream);
+        case 64:
+            if constexpr (FMT != kFmtPsq4) return launch_decode_t<FMT, 64>(p, stream);
+            return hipErrorNotSupported;
         case 32:
-            if constexpr (KVB == 2) return launch_decode_t<2, 32>(p, stream);
+            if constexpr (FMT == kFmtBf16) return launch_decode_t<kFmtBf16, 32>(p, stream);
             return hipErrorNotSupported;
         default: return hipErrorNotSupported;
     }
@@ -718,8 +864,8 @@ hipError_t launch_reduce(const DecodeParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-DecodeParams make(const psk_paged_attention_args& c, const void* k, const void* v, const float* ks,
-                  const float* vs, float* partials, uint32_t splits, uint32_t pps) {
+DecodeParams make(const psk_paged_attention_args& c, const void* k, const void* v, const void* ks,
+                  const void* vs, float* partials, uint32_t splits, uint32_t pps) {
     DecodeParams p{};
     p.a = c;
     p.k_pool = static_cast<const uint8_t*>(k);
@@ -733,12 +879,53 @@ DecodeParams make(const psk_paged_attention_args& c, const void* k, const void* 
     return p;
 }
 
+// PSQ shapes of the MFMA kernel: q_per_kv <= 16, head_dim 128 or 256 (and
+// 64 for PSQ8), code pools 16 B aligned, scale pools 4 B aligned. Every
+// (token, head) slice is then 16 B aligned (its offset is a multiple of
+// head_dim/2 or head_dim bytes).
+bool psq_mfma_shape_ok(const psk_paged_attention_args& c, bool psq4, const void* kp, const void* vp,
+                       const void* ks, const void* vs) {
+    if (c.q_heads / c.kv_heads > (uint32_t)kMaxQPerKV) return false;
+    const uint32_t D = c.head_dim;
+    if (!(D == 128 || D == 256 || (D == 64 && !psq4))) return false;
+    auto al = [](const void* ptr, uintptr_t n) { return reinterpret_cast<uintptr_t>(ptr) % n == 0u; };
+    return al(kp, 16) && al(vp, 16) && al(ks, 4) && al(vs, 4);
+}
+
+// Validation shared by the PSQ launchers (paged_decode.hip:1597-1609): the
+// common checks, both scale pools, head_dim == 32 * blocks_per_head.
+hipError_t validate_psq(const psk_paged_attention_args* a, const void* kc, const void* vc,
+                        const void* ks, const void* vs, uint32_t blocks_per_head) {
+    if (a == nullptr || kc == nullptr || vc == nullptr || ks == nullptr || vs == nullptr)
+        return hipErrorInvalidValue;
+    const hipError_t e = validate_common(*a);
+    if (e != hipSuccess) return e;
+    if (a->head_dim != 32u * blocks_per_head) return hipErrorNotSupported;
+    return hipSuccess;
+}
+
 }  // namespace
 
-// Generic fallback for shapes outside mfma_shape_ok (defined in page_ops.hip).
+// Generic fallbacks for shapes outside the MFMA kernel (page_ops.hip).
 hipError_t launch_attention_generic(const psk_paged_attention_args& c, int kvb, const void* k,
                                     const void* v, const float* ks, const float* vs,
                                     hipStream_t stream);
+hipError_t launch_attention_generic_psq(const psk_paged_attention_args& c, bool psq4, const void* k,
+                                        const void* v, const uint16_t* ks, const uint16_t* vs,
+                                        hipStream_t stream);
+
+// PSQ attention of every row straight to the output (partials == nullptr)
+// or into split partials.
+hipError_t launch_psq(const psk_paged_attention_args& a, bool psq4, const uint8_t* kc,
+                      const uint8_t* vc, const uint16_t* ks, const uint16_t* vs, float* partials,
+                      uint32_t splits, uint32_t pps, hipStream_t st) {
+    if (!psq_mfma_shape_ok(a, psq4, kc, vc, ks, vs)) {
+        if (partials != nullptr) return hipErrorNotSupported;
+        return launch_attention_generic_psq(a, psq4, kc, vc, ks, vs, st);
+    }
+    const DecodeParams p = make(a, kc, vc, ks, vs, partials, splits, pps);
+    return psq4 ? launch_decode<kFmtPsq4>(p, st) : launch_decode<kFmtPsq8>(p, st);
+}
 
 }  // namespace psk
 
@@ -759,7 +946,7 @@ extern "C" int psk_attention_paged_bf16(const psk_paged_attention_args* a, const
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (!psk::mfma_shape_ok(*a, 2, k_pool, v_pool))
         return psk::launch_attention_generic(*a, 2, k_pool, v_pool, nullptr, nullptr, st);
-    return psk::launch_decode<2>(psk::make(*a, k_pool, v_pool, nullptr, nullptr, nullptr, 1u, 0u), st);
+    return psk::launch_decode<psk::kFmtBf16>(psk::make(*a, k_pool, v_pool, nullptr, nullptr, nullptr, 1u, 0u), st);
 }
 
 extern "C" int psk_attention_paged_fp8_e4m3(const psk_paged_attention_args* a, const void* k_pool,
@@ -773,7 +960,7 @@ extern "C" int psk_attention_paged_fp8_e4m3(const psk_paged_attention_args* a, c
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (!psk::mfma_shape_ok(*a, 1, k_pool, v_pool))
         return psk::launch_attention_generic(*a, 1, k_pool, v_pool, k_scale_pool, v_scale_pool, st);
-    return psk::launch_decode<1>(
+    return psk::launch_decode<psk::kFmtFp8>(
         psk::make(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, nullptr, 1u, 0u), st);
 }
 
@@ -794,7 +981,7 @@ extern "C" int psk_attention_paged_bf16_split_ex(const psk_paged_attention_args*
     int e = split_common(a, k_pool, v_pool, partials, splits);
     if (e != hipSuccess) return e;
     if (!psk::mfma_shape_ok(*a, 2, k_pool, v_pool)) return hipErrorNotSupported;
-    return psk::launch_decode<2>(
+    return psk::launch_decode<psk::kFmtBf16>(
         psk::make(*a, k_pool, v_pool, nullptr, nullptr, partials, splits, pages_per_split),
         static_cast<hipStream_t>(stream));
 }
@@ -817,7 +1004,7 @@ extern "C" int psk_attention_paged_fp8_e4m3_split(const psk_paged_attention_args
     if (e != hipSuccess) return e;
     if (k_scale_pool == nullptr || v_scale_pool == nullptr) return hipErrorInvalidValue;
     if (!psk::mfma_shape_ok(*a, 1, k_pool, v_pool)) return hipErrorNotSupported;
-    return psk::launch_decode<1>(psk::make(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, partials,
+    return psk::launch_decode<psk::kFmtFp8>(psk::make(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, partials,
                                            splits, pages_per_split),
                                  static_cast<hipStream_t>(stream));
 }
@@ -844,6 +1031,87 @@ extern "C" int psk_attention_paged_bf16_split_reduce(const psk_paged_attention_a
                                                      void* stream) {
     if (splits != 2u && splits != 4u && splits != 8u && splits != 16u) return hipErrorInvalidValue;
     return psk_attention_paged_split_reduce_ex(a, partials, splits, 0u, stream);
+}
+
+// ------------------------------------------------------------ PSQ KV
+extern "C" int psk_attention_paged_psq(const psk_paged_attention_args* a, uint32_t kv_dtype,
+                                       const uint8_t* k_code_pool, const uint8_t* v_code_pool,
+                                       const uint16_t* k_scale_pool, const uint16_t* v_scale_pool,
+                                       uint32_t blocks_per_head, void* stream) {
+    if (kv_dtype != PSK_KV_PSQ4_W32 && kv_dtype != PSK_KV_PSQ8_W32) return hipErrorInvalidValue;
+    hipError_t e = psk::validate_psq(a, k_code_pool, v_code_pool, k_scale_pool, v_scale_pool,
+                                     blocks_per_head);
+    if (e != hipSuccess) return e;
+    return psk::launch_psq(*a, kv_dtype == PSK_KV_PSQ4_W32, k_code_pool, v_code_pool, k_scale_pool,
+                           v_scale_pool, nullptr, 1u, 0u, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int psk_attention_paged_psq_split_ex(const psk_paged_attention_args* a, uint32_t kv_dtype,
+                                                const uint8_t* k_code_pool,
+                                                const uint8_t* v_code_pool,
+                                                const uint16_t* k_scale_pool,
+                                                const uint16_t* v_scale_pool,
+                                                uint32_t blocks_per_head, float* partials,
+                                                uint32_t splits, uint32_t pages_per_split,
+                                                void* stream) {
+    if (kv_dtype != PSK_KV_PSQ4_W32 && kv_dtype != PSK_KV_PSQ8_W32) return hipErrorInvalidValue;
+    hipError_t e = psk::validate_psq(a, k_code_pool, v_code_pool, k_scale_pool, v_scale_pool,
+                                     blocks_per_head);
+    if (e != hipSuccess) return e;
+    if (partials == nullptr || splits == 0u || splits > psk::kMaxSplits) return hipErrorInvalidValue;
+    return psk::launch_psq(*a, kv_dtype == PSK_KV_PSQ4_W32, k_code_pool, v_code_pool, k_scale_pool,
+                           v_scale_pool, partials, splits, pages_per_split,
+                           static_cast<hipStream_t>(stream));
+}
+
+// The reference's split launchers accept q_per_kv 4 or 6 and 2, 4, 8 or 16
+// splits (paged_decode.hip:2109-2116, 2172-2179).
+static int psq_split_ref(const psk_paged_attention_args* a, uint32_t kv_dtype, const uint8_t* kc,
+                         const uint8_t* vc, const uint16_t* ks, const uint16_t* vs, uint32_t bph,
+                         float* partials, uint32_t splits, void* stream) {
+    if (a == nullptr) return hipErrorInvalidValue;
+    if (a->kv_heads != 0u && a->q_heads % a->kv_heads == 0u) {
+        const uint32_t qpk = a->q_heads / a->kv_heads;
+        if (qpk != 4u && qpk != 6u) return hipErrorInvalidValue;
+    }
+    if (splits != 2u && splits != 4u && splits != 8u && splits != 16u) return hipErrorInvalidValue;
+    return psk_attention_paged_psq_split_ex(a, kv_dtype, kc, vc, ks, vs, bph, partials, splits, 0u,
+                                            stream);
+}
+
+extern "C" int psk_attention_paged_psq4(const psk_paged_attention_args* a, const uint8_t* kc,
+                                        const uint8_t* vc, const uint16_t* ks, const uint16_t* vs,
+                                        uint32_t bph, void* stream) {
+    return psk_attention_paged_psq(a, PSK_KV_PSQ4_W32, kc, vc, ks, vs, bph, stream);
+}
+extern "C" int psk_attention_paged_psq8(const psk_paged_attention_args* a, const uint8_t* kc,
+                                        const uint8_t* vc, const uint16_t* ks, const uint16_t* vs,
+                                        uint32_t bph, void* stream) {
+    return psk_attention_paged_psq(a, PSK_KV_PSQ8_W32, kc, vc, ks, vs, bph, stream);
+}
+// Prefill rows run as independent decode rows (each sees its own pos + 1
+// tokens, the reference's causal rule).
+extern "C" int psk_attention_paged_prefill_psq4(const psk_paged_attention_args* a, const uint8_t* kc,
+                                                const uint8_t* vc, const uint16_t* ks,
+                                                const uint16_t* vs, uint32_t bph, void* stream) {
+    return psk_attention_paged_psq(a, PSK_KV_PSQ4_W32, kc, vc, ks, vs, bph, stream);
+}
+extern "C" int psk_attention_paged_prefill_psq8(const psk_paged_attention_args* a, const uint8_t* kc,
+                                                const uint8_t* vc, const uint16_t* ks,
+                                                const uint16_t* vs, uint32_t bph, void* stream) {
+    return psk_attention_paged_psq(a, PSK_KV_PSQ8_W32, kc, vc, ks, vs, bph, stream);
+}
+extern "C" int psk_attention_paged_psq4_split(const psk_paged_attention_args* a, const uint8_t* kc,
+                                              const uint8_t* vc, const uint16_t* ks,
+                                              const uint16_t* vs, uint32_t bph, float* partials,
+                                              uint32_t splits, void* stream) {
+    return psq_split_ref(a, PSK_KV_PSQ4_W32, kc, vc, ks, vs, bph, partials, splits, stream);
+}
+extern "C" int psk_attention_paged_psq8_split(const psk_paged_attention_args* a, const uint8_t* kc,
+                                              const uint8_t* vc, const uint16_t* ks,
+                                              const uint16_t* vs, uint32_t bph, float* partials,
+                                              uint32_t splits, void* stream) {
+    return psq_split_ref(a, PSK_KV_PSQ8_W32, kc, vc, ks, vs, bph, partials, splits, stream);
 }
 
 // ------------------------------------------------- reference C++ signatures
@@ -890,6 +1158,52 @@ hipError_t launch_attention_paged_fp8_e4m3_split(
         C(common), k_pool, v_pool, k_scale_pool, v_scale_pool, partials, splits, pages_per_split,
         stream));
 }
+
+// The reference's reduce runs one query head per workgroup in this build.
+uint32_t paged_attention_split_reduce_qh_per_wg() { return 1u; }
+
+#define PSK_PSQ_ARGS(common, k, v, ks, vs)                                                   \
+    C(common), k, v, reinterpret_cast<const uint16_t*>(ks), reinterpret_cast<const uint16_t*>(vs)
+
+hipError_t launch_attention_paged_psq4(const PagedAttentionCommonArgs& common, const uint8_t* k,
+                                       const uint8_t* v, const bf16_t* ks, const bf16_t* vs,
+                                       uint32_t bph, hipStream_t stream) {
+    return static_cast<hipError_t>(
+        psk_attention_paged_psq4(PSK_PSQ_ARGS(common, k, v, ks, vs), bph, stream));
+}
+hipError_t launch_attention_paged_psq8(const PagedAttentionCommonArgs& common, const uint8_t* k,
+                                       const uint8_t* v, const bf16_t* ks, const bf16_t* vs,
+                                       uint32_t bph, hipStream_t stream) {
+    return static_cast<hipError_t>(
+        psk_attention_paged_psq8(PSK_PSQ_ARGS(common, k, v, ks, vs), bph, stream));
+}
+hipError_t launch_attention_paged_prefill_psq4(const PagedAttentionCommonArgs& common,
+                                               const uint8_t* k, const uint8_t* v, const bf16_t* ks,
+                                               const bf16_t* vs, uint32_t bph, hipStream_t stream) {
+    return static_cast<hipError_t>(
+        psk_attention_paged_prefill_psq4(PSK_PSQ_ARGS(common, k, v, ks, vs), bph, stream));
+}
+hipError_t launch_attention_paged_prefill_psq8(const PagedAttentionCommonArgs& common,
+                                               const uint8_t* k, const uint8_t* v, const bf16_t* ks,
+                                               const bf16_t* vs, uint32_t bph, hipStream_t stream) {
+    return static_cast<hipError_t>(
+        psk_attention_paged_prefill_psq8(PSK_PSQ_ARGS(common, k, v, ks, vs), bph, stream));
+}
+hipError_t launch_attention_paged_psq4_split(const PagedAttentionCommonArgs& common, const uint8_t* k,
+                                             const uint8_t* v, const bf16_t* ks, const bf16_t* vs,
+                                             uint32_t bph, float* partials, uint32_t splits,
+                                             hipStream_t stream) {
+    return static_cast<hipError_t>(psk_attention_paged_psq4_split(
+        PSK_PSQ_ARGS(common, k, v, ks, vs), bph, partials, splits, stream));
+}
+hipError_t launch_attention_paged_psq8_split(const PagedAttentionCommonArgs& common, const uint8_t* k,
+                                             const uint8_t* v, const bf16_t* ks, const bf16_t* vs,
+                                             uint32_t bph, float* partials, uint32_t splits,
+                                             hipStream_t stream) {
+    return static_cast<hipError_t>(psk_attention_paged_psq8_split(
+        PSK_PSQ_ARGS(common, k, v, ks, vs), bph, partials, splits, stream));
+}
+#undef PSK_PSQ_ARGS
 
 hipError_t launch_attention_paged_split_reduce_ex(const PagedAttentionCommonArgs& common,
                                                   const float* partials, uint32_t splits,

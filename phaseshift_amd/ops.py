@@ -15,7 +15,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import (KV_BF16, KV_FP8, OUT_BF16, OUT_F32, KvAppendArgs, KvGatherArgs, PageCopyArgs,
+from . import (KV_BF16, KV_FP8, KV_PSQ4, KV_PSQ8, OUT_BF16, OUT_F32, KvAppendArgs, KvGatherArgs, PageCopyArgs,
                PagedAttentionArgs, RequestDescriptor, check, lib)
 
 
@@ -48,6 +48,15 @@ class PoolGeometry:
     @property
     def scale_elems(self) -> int:
         return self.num_layers * self.num_pages * self.page_tokens * self.kv_heads
+
+    # PSQ pools (kv_cache_types.h:16-46): blocks of 32 values of a (token,
+    # head) slice; 16 (PSQ4) or 32 (PSQ8) code bytes and one bf16 scale each.
+    @property
+    def psq_blocks(self) -> int:
+        return self.scale_elems * (self.head_dim // 32)
+
+    def psq_code_bytes(self, fmt: int) -> int:
+        return self.psq_blocks * (16 if fmt == 4 else 32)
 
 
 def _ptr(t) -> int | None:
@@ -181,6 +190,47 @@ def paged_attention(geom: PoolGeometry, layer: int, q, out, slots, positions, bl
     else:
         check("psk_attention_paged_bf16_split_ex", L.psk_attention_paged_bf16_split_ex(
             C.byref(a), _ptr(k_pool), _ptr(v_pool), _ptr(partials), splits, pages_per_split, s))
+    check("psk_attention_paged_split_reduce_ex", L.psk_attention_paged_split_reduce_ex(
+        C.byref(a), _ptr(partials), splits, pages_per_split, s))
+
+
+def kv_append_psq(geom: PoolGeometry, layer: int, k_in, v_in, slots, positions, block_tables,
+                  k_code, v_code, k_scale, v_scale, fmt: int, estimator: int = 0, stream=None,
+                  max_sequences: int | None = None) -> None:
+    """launch_kv_append_psq4 / launch_kv_append_psq8 (kv_append.h:99-123).
+    fmt 4 or 8; estimator 0 = MaxAbs, 1 = Lsq1; scale pools are bf16 bits
+    (int16/uint16/bfloat16 tensors)."""
+    a = append_args(geom, layer, k_in, v_in, slots, positions, block_tables, max_sequences)
+    fn = "psk_kv_append_psq4" if fmt == 4 else "psk_kv_append_psq8"
+    check(fn, getattr(lib(), fn)(C.byref(a), _ptr(k_code), _ptr(v_code), _ptr(k_scale),
+                                 _ptr(v_scale), geom.head_dim // 32, estimator, _stream(stream)))
+
+
+def paged_attention_psq(geom: PoolGeometry, layer: int, q, out, slots, positions, block_tables,
+                        k_code, v_code, k_scale, v_scale, q_heads: int, fmt: int,
+                        scale: float | None = None, splits: int = 1, pages_per_split: int = 0,
+                        partials=None, stream=None, max_sequences: int | None = None,
+                        kind: str = "decode") -> None:
+    """Paged attention over PSQ4/PSQ8 pools (paged_attention.h:202-285).
+    splits == 1: launch_attention_paged_psq{4,8} (kind "prefill":
+    launch_attention_paged_prefill_psq{4,8}); splits > 1: the split kernel
+    into `partials`, then the combine."""
+    a = attention_args(geom, layer, q, out, slots, positions, block_tables, q_heads, scale,
+                       max_sequences)
+    s = _stream(stream)
+    L = lib()
+    bph = geom.head_dim // 32
+    ptrs = (_ptr(k_code), _ptr(v_code), _ptr(k_scale), _ptr(v_scale))
+    if splits <= 1:
+        fn = f"psk_attention_paged_{'prefill_' if kind == 'prefill' else ''}psq{fmt}"
+        check(fn, getattr(L, fn)(C.byref(a), *ptrs, bph, s))
+        return
+    need = split_partials_bytes(q.shape[0], q_heads, geom.kv_heads, splits)
+    if partials is None or partials.numel() * partials.element_size() < need:
+        raise ValueError(f"partials workspace must hold {need} bytes")
+    check("psk_attention_paged_psq_split_ex", L.psk_attention_paged_psq_split_ex(
+        C.byref(a), KV_PSQ4 if fmt == 4 else KV_PSQ8, *ptrs, bph, _ptr(partials), splits,
+        pages_per_split, s))
     check("psk_attention_paged_split_reduce_ex", L.psk_attention_paged_split_reduce_ex(
         C.byref(a), _ptr(partials), splits, pages_per_split, s))
 

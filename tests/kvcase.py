@@ -116,3 +116,28 @@ def oracle_attention_parallel(geom, q, slots, positions, block_tables, kp, vp, k
     with ThreadPoolExecutor(len(bounds) - 1) as ex:
         list(ex.map(job, range(len(bounds) - 1)))
     return out
+
+
+def oracle_attention_psq_parallel(geom, q, slots, positions, block_tables, kc, vc, ks, vs, fmt,
+                                  scale=None, workers=8):
+    """oracle.paged_attention_psq over row chunks in threads."""
+    from concurrent.futures import ThreadPoolExecutor
+    rows = q.shape[0]
+    H, D = geom["q_heads"], geom["head_dim"]
+    out = np.zeros((rows, H * D), np.float32)
+    slots = np.asarray(slots, np.uint32)
+    positions = np.asarray(positions, np.uint32)
+    bounds = np.linspace(0, rows, min(workers, rows) + 1).astype(int)
+
+    def job(i):
+        a, b = bounds[i], bounds[i + 1]
+        if a == b:
+            return
+        o = np.ascontiguousarray(out[a:b])
+        oracle.paged_attention_psq(geom, q[a:b], slots[a:b], positions[a:b], block_tables, kc, vc,
+                                   ks, vs, fmt, scale, out=o)
+        out[a:b] = o
+
+    with ThreadPoolExecutor(len(bounds) - 1) as ex:
+        list(ex.map(job, range(len(bounds) - 1)))
+    return out

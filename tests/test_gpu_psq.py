@@ -1,0 +1,361 @@
+"""PSQ4_W32 / PSQ8_W32 KV on the GPU vs the oracle.
+
+Append: MaxAbs bit-exact and LSQ1 bit-exact against the oracle's
+device-order restatement (the 32-lane xor butterfly of kv_append.hip:293-299,
+no contraction); LSQ1 against the reference host encoder's sequential sums
+to the reference test's "close" bar (test_kv_append.hip:480-520: <= 2% of
+scales and <= 5% of codes differ). Attention: max-abs 5e-2 against the
+oracle's fp32 attention over the same dequantised pools (north-star FP8
+tolerance), on the reference test's PSQ4 geometries
+(test_paged_attention.hip:685-743) plus split-K, head_dim 128/64, the
+generic kernel, and the skip rules.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from phaseshift_amd import HipError, ops
+from tests.kvcase import (INVALID, Layout, bf16_normal, oracle_attention_psq_parallel,
+                          paged_layout, to_dev, to_host)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-2
+
+
+def geom_of(lay):
+    return ops.PoolGeometry(lay.num_layers, lay.num_pages, lay.page_tokens, lay.kv_heads,
+                            lay.head_dim)
+
+
+def dev_pools(lay, fmt, dev, fill=True, seed=0):
+    """Code and scale pools on the device; random codes and positive bf16
+    scales when fill (attention cases), sentinels otherwise (append)."""
+    g = geom_of(lay)
+    nb = g.psq_blocks
+    cb = g.psq_code_bytes(fmt)
+    if not fill:
+        return (torch.full((cb,), 0xA5, dtype=torch.uint8, device=dev),
+                torch.full((cb,), 0x5A, dtype=torch.uint8, device=dev),
+                torch.full((nb,), 0x1234, dtype=torch.int16, device=dev),
+                torch.full((nb,), 0x4321, dtype=torch.int16, device=dev))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    kc = torch.randint(0, 256, (cb,), generator=gen, device=dev, dtype=torch.int32)
+    vc = torch.randint(0, 256, (cb,), generator=gen, device=dev, dtype=torch.int32)
+    if fmt == 8:   # no NaN codes
+        kc = torch.where((kc & 0x7F) == 0x7F, kc ^ 1, kc)
+        vc = torch.where((vc & 0x7F) == 0x7F, vc ^ 1, vc)
+    lo, hi = (0.02, 0.3) if fmt == 4 else (0.0005, 0.007)
+    ks = (torch.rand(nb, generator=gen, device=dev) * (hi - lo) + lo).to(torch.bfloat16).view(torch.int16)
+    vs = (torch.rand(nb, generator=gen, device=dev) * (hi - lo) + lo).to(torch.bfloat16).view(torch.int16)
+    return kc.to(torch.uint8), vc.to(torch.uint8), ks, vs
+
+
+# ------------------------------------------------------------------ append
+def append_case(dev, fmt, lsq1, rows, kv_heads, D, seed, stride_pad=0):
+    rng = np.random.default_rng(seed)
+    lens = [rows // 2 + 3, rows - rows // 2 - 3]
+    lay = paged_layout(rng, lens, 16, kv_heads, D, spare_pages=2)
+    slots = np.repeat(np.arange(2, dtype=np.uint32), lens)
+    pos = np.concatenate([np.arange(n, dtype=np.uint32) for n in lens])
+    W = kv_heads * D + stride_pad
+    k_in = bf16_normal(rng, (rows, W), 0.02)
+    v_in = bf16_normal(rng, (rows, W), 0.02)
+    # the reference test's extreme blocks: all zero, one-hot, tiny, constant
+    k_in[0, :32] = 0
+    k_in[1, 32:64] = 0
+    k_in[1, 40] = oracle.f32_to_bf16(np.array([-5.0], np.float32))[0]
+    v_in[2, :32] = oracle.f32_to_bf16(np.full(32, 1e-30, np.float32))
+    v_in[3, 64:96] = oracle.f32_to_bf16(np.full(32, 3.0, np.float32))
+    return lay, slots, pos, k_in, v_in
+
+
+def run_append(dev, lay, fmt, lsq1, k_in, v_in, slots, pos, bt, max_sequences=None):
+    kc, vc, ks, vs = dev_pools(lay, fmt, dev, fill=False)
+    ops.kv_append_psq(geom_of(lay), 0, to_dev(k_in), to_dev(v_in), to_dev(slots),
+                      to_dev(pos), to_dev(bt), kc, vc, ks, vs, fmt, int(lsq1),
+                      max_sequences=max_sequences)
+    torch.cuda.synchronize()
+    return to_host(kc), to_host(vc), to_host(ks), to_host(vs)
+
+
+def oracle_append(lay, fmt, lsq1, k_in, v_in, slots, pos, bt, device_order=True, max_sequences=None):
+    g = geom_of(lay)
+    kc = np.full(g.psq_code_bytes(fmt), 0xA5, np.uint8)
+    vc = np.full(g.psq_code_bytes(fmt), 0x5A, np.uint8)
+    ks = np.full(g.psq_blocks, 0x1234, np.uint16)
+    vs = np.full(g.psq_blocks, 0x4321, np.uint16)
+    geo = dict(lay.geom, block_table_stride=bt.shape[1],
+               max_sequences=bt.shape[0] if max_sequences is None else max_sequences)
+    oracle.kv_append_psq(geo, k_in, v_in, slots, pos, bt, kc, vc, ks, vs, fmt, lsq1, device_order)
+    return kc, vc, ks, vs
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("lsq1", [False, True])
+@pytest.mark.parametrize("kv_heads,D,rows,pad", [(4, 256, 64, 0), (2, 128, 37, 0), (3, 64, 21, 8),
+                                                 (4, 256, 9, 3)])
+def test_append_bit_exact(dev, fmt, lsq1, kv_heads, D, rows, pad):
+    """pad 3: odd row stride, so the unaligned (element-wise) load path runs."""
+    lay, slots, pos, k_in, v_in = append_case(dev, fmt, lsq1, rows, kv_heads, D,
+                                              fmt * 100 + D + rows + pad, pad)
+    got = run_append(dev, lay, fmt, lsq1, k_in, v_in, slots, pos, lay.block_tables)
+    want = oracle_append(lay, fmt, lsq1, k_in, v_in, slots, pos, lay.block_tables)
+    for name, a, b in zip(("k codes", "v codes", "k scales", "v scales"), got, want):
+        assert np.array_equal(a, b), name
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_append_lsq1_close_to_reference_host_order(dev, fmt):
+    """The reference test's LSQ1 bar against its host encoder's sequential sums."""
+    lay, slots, pos, k_in, v_in = append_case(dev, fmt, True, 256, 4, 256, 77 + fmt)
+    got = run_append(dev, lay, fmt, True, k_in, v_in, slots, pos, lay.block_tables)
+    host = oracle_append(lay, fmt, True, k_in, v_in, slots, pos, lay.block_tables,
+                         device_order=False)
+    written = got[2] != 0x1234
+    scale_mm = np.mean(got[2][written] != host[2][written])
+    code_mm = np.mean(got[0] != host[0])
+    assert scale_mm <= 0.02 and code_mm <= 0.05, (scale_mm, code_mm)
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_append_skip_rules(dev, fmt):
+    rng = np.random.default_rng(5)
+    lay = paged_layout(rng, [40, 40], 16, 4, 256, spare_pages=1)
+    bt = lay.block_tables.copy()
+    bt[1, 1] = INVALID
+    slots = np.array([0, 1, 5, 0, 1], np.uint32)          # slot 5 >= max_sequences
+    pos = np.array([3, 20, 1, 16 * bt.shape[1], 4], np.uint32)   # row 3: past the table
+    k_in = bf16_normal(rng, (5, 1024))
+    v_in = bf16_normal(rng, (5, 1024))
+    got = run_append(dev, lay, fmt, False, k_in, v_in, slots, pos, bt)
+    want = oracle_append(lay, fmt, False, k_in, v_in, slots, pos, bt)
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b)
+    # exactly rows 0 and 4 were written (row 1 hits the invalid page)
+    assert np.sum(got[2] != 0x1234) == 2 * 4 * 8
+
+
+def test_append_psq_full_size_round_trip(dev):
+    """2^16 rows x 4 heads x 256 (the append bench shape): every dequantised
+    value lies within half a codebook step of its input, and a sample of rows
+    matches the oracle bit for bit."""
+    rows, kvh, D = 1 << 16, 4, 256
+    pages = rows // 16
+    lay_bt = np.arange(pages, dtype=np.uint32).reshape(1, pages)
+    g = ops.PoolGeometry(1, pages, 16, kvh, D)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(9)
+    k = torch.randn(rows, kvh * D, generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn(rows, kvh * D, generator=gen, device=dev).to(torch.bfloat16)
+    slots = torch.zeros(rows, dtype=torch.int32, device=dev)
+    pos = torch.arange(rows, dtype=torch.int32, device=dev)
+    bt = to_dev(lay_bt)
+    for fmt in (4, 8):
+        kc = torch.empty(g.psq_code_bytes(fmt), dtype=torch.uint8, device=dev)
+        vc = torch.empty_like(kc)
+        ks = torch.empty(g.psq_blocks, dtype=torch.int16, device=dev)
+        vs = torch.empty_like(ks)
+        ops.kv_append_psq(g, 0, k, v, slots, pos, bt, kc, vc, ks, vs, fmt, 0)
+        torch.cuda.synchronize()
+        # dequantise on the device with torch (codebook lookup x scale)
+        s = (ks.to(torch.int32) << 16).view(torch.float32).view(-1, 1)
+        if fmt == 4:
+            b = kc.view(-1, 16).to(torch.int32)
+            c = torch.cat([b & 15, b >> 4], dim=1)
+            mags = torch.tensor([0, 1, 2, 3, 4, 6, 8, 10], dtype=torch.float32, device=dev)
+            val = mags[c & 7] * torch.where(c >= 8, -1.0, 1.0)
+            step = 1.0   # half of the widest gap (2)
+        else:
+            lut = torch.from_numpy(oracle.e4m3_decode(np.arange(256, dtype=np.uint8))).to(dev)
+            val = lut[kc.view(-1, 32).to(torch.int64)]
+        x = k.float().view(-1, 32)
+        err = (x - val * s).abs()
+        if fmt == 4:
+            bound = s * (1 + 1e-6)   # half of the widest codebook gap (2)
+        else:   # half an E4M3 ulp of x/s: 2^-4 relative, 2^-10 absolute (subnormals)
+            bound = x.abs() * (2.0 ** -4) * (1 + 1e-6) + s * 2.0 ** -10 + 1e-30
+        assert bool((err <= bound).all()), fmt
+        pick = np.array([0, 1, 12345, rows - 1])
+        lay = Layout(1, pages, 16, kvh, D, lay_bt)
+        want = oracle_append(lay, fmt, False, to_host(k[pick]), to_host(v[pick]),
+                             np.zeros(4, np.uint32), pick.astype(np.uint32), lay_bt)
+        for r in pick:
+            blk = slice(r * kvh * 8, (r + 1) * kvh * 8)
+            assert np.array_equal(to_host(ks)[blk], want[2][blk])
+            cbs = 16 if fmt == 4 else 32
+            assert np.array_equal(to_host(kc)[blk.start * cbs:blk.stop * cbs],
+                                  want[0][blk.start * cbs:blk.stop * cbs])
+
+
+def test_append_psq_errors(dev):
+    rng = np.random.default_rng(1)
+    lay = paged_layout(rng, [4], 16, 4, 256)
+    g = geom_of(lay)
+    kc, vc, ks, vs = dev_pools(lay, 4, dev, fill=False)
+    k = to_dev(bf16_normal(rng, (4, 1024)))
+    sl, ps = to_dev(np.zeros(4, np.uint32)), to_dev(np.arange(4, dtype=np.uint32))
+    bt = to_dev(lay.block_tables)
+    bad = ops.PoolGeometry(1, lay.num_pages, 16, 4, 250)
+    with pytest.raises(HipError) as ei:
+        ops.kv_append_psq(bad, 0, k, k, sl, ps, bt, kc, vc, ks, vs, 4, 0)
+    assert ei.value.code == 801   # hipErrorNotSupported, as the reference
+    with pytest.raises(HipError):
+        ops.kv_append_psq(g, 0, k, k, sl, ps, bt, kc, vc, ks, vs, 4, 2)
+    with pytest.raises(HipError):
+        ops.kv_append_psq(g, 0, k, k, sl, ps, bt, kc, vc, None, vs, 8, 0)
+
+
+# --------------------------------------------------------------- attention
+def attn_case(dev, fmt, lens, qh, kvh, D, P=16, seed=0, spare=2):
+    rng = np.random.default_rng(seed)
+    lay = paged_layout(rng, lens, P, kvh, D, spare_pages=spare)
+    pools = dev_pools(lay, fmt, dev, seed=seed)
+    q = bf16_normal(rng, (len(lens), qh * D))
+    slots = np.arange(len(lens), dtype=np.uint32)
+    pos = np.asarray(lens, np.uint32) - 1
+    return rng, lay, pools, q, slots, pos
+
+
+def run_attn(dev, lay, fmt, qh, q, slots, pos, bt, pools, splits=1, pps=0, kind="decode",
+             out_dtype=torch.float32):
+    rows = q.shape[0]
+    out = torch.full((rows, qh * lay.head_dim), 7.0, dtype=out_dtype, device=dev)
+    partials = None
+    if splits > 1:
+        nbytes = ops.split_partials_bytes(rows, qh, lay.kv_heads, splits)
+        partials = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    ops.paged_attention_psq(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                            to_dev(bt), *pools, qh, fmt, splits=splits, pages_per_split=pps,
+                            partials=partials, kind=kind)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def oracle_attn(lay, fmt, qh, q, slots, pos, bt, pools):
+    g = dict(lay.geom, q_heads=qh, block_table_stride=bt.shape[1], max_sequences=bt.shape[0])
+    kc, vc, ks, vs = (to_host(t) for t in pools)
+    return oracle_attention_psq_parallel(g, q, slots, pos, bt, kc, vc, ks, vs, fmt,
+                                         1.0 / math.sqrt(lay.head_dim))
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("qh,kvh,D,lens", [
+    (16, 4, 256, [1, 17, 33, 100, 257, 300, 513, 64]),   # reference: qh 16 kvh 4 rows 8
+    (24, 4, 256, [5, 40, 999, 16]),                      # qh 24 kvh 4 rows 4
+    (16, 4, 256, [2048]),                                # long visible 2048
+    (8, 2, 128, [3, 31, 130]),                           # head_dim 128
+    (8, 4, 64, [1, 70]),                                 # head_dim 64 (PSQ4: generic)
+    (6, 2, 96, [50, 9]),                                 # head_dim 96: generic kernel
+    (20, 1, 128, [70]),                                  # q_per_kv 20: generic kernel
+])
+def test_decode_matches_oracle(dev, fmt, qh, kvh, D, lens):
+    _, lay, pools, q, slots, pos = attn_case(dev, fmt, lens, qh, kvh, D, seed=qh + D + fmt)
+    bt = lay.block_tables
+    want = oracle_attn(lay, fmt, qh, q, slots, pos, bt, pools)
+    got = run_attn(dev, lay, fmt, qh, q, slots, pos, bt, pools)
+    assert np.max(np.abs(got - want)) < TOL
+    mfma = D in (128, 256) or (D == 64 and fmt == 8)
+    if mfma and qh // kvh <= 16 and max(lens) > 64:
+        for splits, pps in ((4, 0), (16, 0), (3, 2), (64, 1)):
+            got_s = run_attn(dev, lay, fmt, qh, q, slots, pos, bt, pools, splits, pps)
+            assert np.max(np.abs(got_s - want)) < TOL, (splits, pps)
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_prefill_rows_are_causal(dev, fmt):
+    """The reference's PSQ prefill cases: 32 and 64 rows of one sequence."""
+    for rows in (32, 64):
+        rng = np.random.default_rng(rows + fmt)
+        lay = paged_layout(rng, [rows + 100], 16, 4, 256, spare_pages=1)
+        pools = dev_pools(lay, fmt, dev, seed=rows)
+        slots = np.zeros(rows, np.uint32)
+        pos = np.arange(100, 100 + rows, dtype=np.uint32)
+        q = bf16_normal(rng, (rows, 16 * 256))
+        want = oracle_attn(lay, fmt, 16, q, slots, pos, lay.block_tables, pools)
+        got = run_attn(dev, lay, fmt, 16, q, slots, pos, lay.block_tables, pools, kind="prefill")
+        assert np.max(np.abs(got - want)) < TOL, rows
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_many_rows_independent_waves_bf16_out(dev, fmt):
+    rng = np.random.default_rng(61 + fmt)
+    lens = rng.integers(1, 600, 200)
+    _, lay, pools, q, slots, pos = attn_case(dev, fmt, lens, 24, 4, 256, seed=61 + fmt)
+    want = oracle_attn(lay, fmt, 24, q, slots, pos, lay.block_tables, pools)
+    got = run_attn(dev, lay, fmt, 24, q, slots, pos, lay.block_tables, pools,
+                   out_dtype=torch.bfloat16)
+    assert np.max(np.abs(got - want)) < TOL
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_reference_split_launchers(dev, fmt):
+    """launch_attention_paged_psq{4,8}_split + bf16_split_reduce, as the
+    reference dispatcher calls them; its argument rules."""
+    _, lay, pools, q, slots, pos = attn_case(dev, fmt, [700, 300], 24, 4, 256, seed=90 + fmt)
+    bt = lay.block_tables
+    want = oracle_attn(lay, fmt, 24, q, slots, pos, bt, pools)
+    from phaseshift_amd import lib
+    import ctypes as C
+    L = lib()
+    for splits in (2, 4, 8, 16):
+        out = torch.full((2, 24 * 256), 7.0, dtype=torch.float32, device=dev)
+        part = torch.empty(ops.split_partials_bytes(2, 24, 4, splits) // 4, device=dev)
+        a = ops.attention_args(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                               to_dev(bt), 24)
+        fn = getattr(L, f"psk_attention_paged_psq{fmt}_split")
+        st = torch.cuda.current_stream().cuda_stream
+        assert fn(C.byref(a), *(t.data_ptr() for t in pools), 8, part.data_ptr(), splits, st) == 0
+        assert L.psk_attention_paged_bf16_split_reduce(C.byref(a), part.data_ptr(), splits, st) == 0
+        torch.cuda.synchronize()
+        assert np.max(np.abs(out.cpu().numpy() - want)) < TOL, splits
+    # splits 3 and q_per_kv 8 are refused, as by the reference
+    assert fn(C.byref(a), *(t.data_ptr() for t in pools), 8, part.data_ptr(), 3, st) != 0
+    a.q_heads = 32
+    assert fn(C.byref(a), *(t.data_ptr() for t in pools), 8, part.data_ptr(), 4, st) != 0
+    # head_dim != 32 * blocks_per_head: hipErrorNotSupported
+    a.q_heads = 24
+    assert L.psk_attention_paged_psq4(C.byref(a), *(t.data_ptr() for t in pools), 4, st) != 0
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("splits", [1, 8])
+def test_invalid_slot_and_page_leave_output_unwritten(dev, fmt, splits):
+    _, lay, pools, q, slots, pos = attn_case(dev, fmt, [600] * 4, 24, 4, 256, seed=12 + fmt)
+    bt = lay.block_tables.copy()
+    bt[1, 20] = INVALID
+    bt[2, 3] = 1 << 30
+    slots = slots.copy()
+    slots[3] = 1000
+    got = run_attn(dev, lay, fmt, 24, q, slots, pos, bt, pools, splits)
+    assert np.all(got[1:] == 7.0)
+    want = oracle_attn(lay, fmt, 24, q[:1], slots[:1], pos[:1], bt, pools)
+    assert np.max(np.abs(got[:1] - want)) < TOL
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_append_then_attend(dev, fmt):
+    """Appended pools attended on the device match the oracle's attention over
+    the oracle's own append (the two halves of the path composed)."""
+    rng = np.random.default_rng(33 + fmt)
+    lens = [300, 45]
+    lay = paged_layout(rng, lens, 16, 4, 256, spare_pages=1)
+    rows = sum(lens)
+    slots = np.repeat(np.arange(2, dtype=np.uint32), lens)
+    pos = np.concatenate([np.arange(n, dtype=np.uint32) for n in lens])
+    k_in = bf16_normal(rng, (rows, 1024), 0.02)
+    v_in = bf16_normal(rng, (rows, 1024), 0.02)
+    kc, vc, ks, vs = dev_pools(lay, fmt, dev, fill=False)
+    ops.kv_append_psq(geom_of(lay), 0, to_dev(k_in), to_dev(v_in), to_dev(slots), to_dev(pos),
+                      to_dev(lay.block_tables), kc, vc, ks, vs, fmt, 1)
+    q = bf16_normal(rng, (2, 24 * 256))
+    qs, qp = np.arange(2, dtype=np.uint32), np.asarray(lens, np.uint32) - 1
+    got = run_attn(dev, lay, fmt, 24, q, qs, qp, lay.block_tables, (kc, vc, ks, vs))
+    okc, ovc, oks, ovs = oracle_append(lay, fmt, True, k_in, v_in, slots, pos, lay.block_tables)
+    g = dict(lay.geom, q_heads=24)
+    want = oracle.paged_attention_psq(g, q, qs, qp, lay.block_tables, okc, ovc, oks, ovs, fmt)
+    assert np.max(np.abs(got - want)) < TOL

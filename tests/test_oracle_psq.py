@@ -1,0 +1,288 @@
+"""Pins the oracle's PSQ4_W32 / PSQ8_W32 codecs, block encoders, append and
+attention.
+
+Evidence, each independent of the oracle's own formulas:
+  * the reference's own header-only host encoders (psq4_kv.h, psq_device.h),
+    compiled from the reference sources into oracle/_ref (skipped when
+    absent): psq_bf16_round, cb10_encode, cb10_code_to_f32, the PSQ4 MaxAbs
+    and LSQ1 block encoders and the nibble packing;
+  * the E4M3 expansion table of the cb10 codebook the reference's codebook
+    test holds (tests/kernels/optimized/test_psq4_codebook.hip:24-28) against
+    the pinned E4M3 decoder;
+  * mathematics: bf16 round-to-nearest-even (torch's float32 -> bfloat16
+    cast), nearest-codebook-point encoding with ties to the smaller
+    magnitude, the least-squares closed form of the LSQ1 scale, and a numpy
+    float64 attention over the dequantised pools.
+PSQ8's block encoder (psq8_kv.h) is not compiled into oracle/_ref (it
+includes hip/hip_fp8.h); its codes are pinned through the E4M3 encoder and
+the shared block logic.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.kvcase import INVALID, bf16_normal, paged_layout
+
+MAGS = np.array([0, 1, 2, 3, 4, 6, 8, 10], np.float64)
+# test_psq4_codebook.hip:24-28: E4M3 codes of the cb10 magnitudes
+CB10_E4M3 = [0x00, 0x38, 0x40, 0x44, 0x48, 0x4C, 0x50, 0x52]
+
+
+def ref_or_skip():
+    r = oracle.ref_lib()
+    if r is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    return r
+
+
+def rand_f32_bits(rng, n):
+    b = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32)
+    x = b.view(np.float32)
+    return x[np.isfinite(x)]
+
+
+# ------------------------------------------------------------- bf16 rounding
+def test_psq_bf16_round_is_rne_for_finite_values():
+    rng = np.random.default_rng(1)
+    x = rand_f32_bits(rng, 1 << 20)
+    # every tie pattern and its neighbours, over many exponents
+    e = rng.integers(1, 254, 4096).astype(np.uint32) << 23
+    m = rng.integers(0, 1 << 7, 4096).astype(np.uint32) << 16
+    ties = (e | m | 0x8000)
+    extra = np.concatenate([ties, ties - 1, ties + 1, ties | 0x10000, ties | 0x80000000])
+    x = np.concatenate([x, extra.view(np.float32)])
+    x = x[np.isfinite(x) & (np.abs(x) < 3.38e38)]   # no overflow to inf
+    got = oracle.psq_bf16_round(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_psq_bf16_round_matches_reference():
+    r = ref_or_skip()
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rand_f32_bits(rng, 1 << 18),
+                        np.array([np.inf, -np.inf, np.nan, 0.0, -0.0], np.float32)])
+    out = np.empty_like(x)
+    r.ref_psq_bf16_round_array(x, out, x.size)
+    got = oracle.psq_bf16_round(x)
+    assert np.array_equal(got.view(np.uint32), out.view(np.uint32))
+
+
+# ------------------------------------------------------------------- cb10
+def test_cb10_decode_table_and_e4m3_expansion():
+    for c in range(16):
+        mag = MAGS[c & 7]
+        want = -mag if c & 8 else mag
+        assert oracle.cb10_decode(np.array([c]))[0] == want
+        # the reference test's E4M3 table decodes to the same value
+        e = CB10_E4M3[c & 7] | (0x80 if c & 8 else 0)
+        assert oracle.e4m3_decode(np.array([e], np.uint8))[0] == want
+
+
+def test_cb10_encode_is_nearest_point_ties_down():
+    rng = np.random.default_rng(3)
+    a = np.concatenate([rng.uniform(0, 12, 20000), rng.uniform(0, 0.6, 2000)]).astype(np.float32)
+    # every midpoint and both its float neighbours
+    mids = np.array([0.5, 1.5, 2.5, 3.5, 5, 7, 9], np.float32)
+    a = np.concatenate([a, mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(20))])
+    x = np.concatenate([a, -a])
+    got = oracle.cb10_encode(x, 1.0)
+    for xi, ci in zip(x.astype(np.float64), got):
+        d = np.abs(abs(xi) - MAGS)
+        want = int(np.flatnonzero(d == d.min())[0])   # ties -> the smaller magnitude
+        assert ci & 7 == want, (xi, ci)
+        assert (ci >> 3) == (1 if xi < 0 else 0)
+    assert oracle.cb10_encode(np.array([np.nan], np.float32), 1.0)[0] == 7
+    assert oracle.cb10_encode(np.array([-0.0], np.float32), 1.0)[0] == 0
+
+
+def test_cb10_matches_reference():
+    r = ref_or_skip()
+    rng = np.random.default_rng(4)
+    x = np.concatenate([rng.standard_normal(1 << 16).astype(np.float32) * 8,
+                        np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0], np.float32)])
+    inv = (1.0 / rng.uniform(0.05, 3, x.size)).astype(np.float32)
+    out = np.empty(x.size, np.uint8)
+    r.ref_cb10_encode_array(x, inv, out, x.size)
+    assert np.array_equal(oracle.cb10_encode(x, inv), out)
+    for c in range(16):
+        assert r.ref_cb10_code_to_f32(c) == oracle.cb10_decode(np.array([c]))[0]
+
+
+# ---------------------------------------------------------- block encoders
+def blocks(rng, n):
+    """Seeded 32-value blocks: normal, outliers, tiny, one-hot, zero, bf16 values."""
+    out = [rng.standard_normal(32) * s for s in rng.uniform(0.01, 30, n)]
+    out += [np.where(rng.random(32) < 0.1, rng.standard_normal(32) * 50, rng.standard_normal(32))
+            for _ in range(n // 4)]
+    out += [rng.standard_normal(32) * 1e-30, np.zeros(32), np.eye(32)[5] * -3.0,
+            np.full(32, 7.25), rng.standard_normal(32) * 1e30]
+    return [oracle.bf16_to_f32(oracle.f32_to_bf16(np.asarray(b, np.float32))) for b in out]
+
+
+def test_psq4_blocks_match_reference_host_encoder():
+    r = ref_or_skip()
+    rng = np.random.default_rng(5)
+    for x in blocks(rng, 400):
+        for lsq1 in (0, 1):
+            s = np.zeros(1, np.float32)
+            c = np.zeros(32, np.uint8)
+            r.ref_psq4_encode_block(x, lsq1, s, c)
+            sb, codes = oracle.psq_encode_block(x, 4, bool(lsq1), device_order=False)
+            assert sb == int(s.view(np.uint32)[0] >> 16), (x, lsq1)
+            assert np.array_equal(codes, c), (x, lsq1)
+
+
+def test_psq4_packing_matches_reference():
+    r = ref_or_skip()
+    rng = np.random.default_rng(6)
+    codes = rng.integers(0, 16, 32, dtype=np.uint8)
+    packed = np.zeros(16, np.uint8)
+    r.ref_psq4_pack_codes(codes, packed)
+    # the oracle's append packs the same way (checked through the pools below)
+    assert np.array_equal(packed, (codes[:16] & 15) | ((codes[16:] & 15) << 4))
+
+
+def test_maxabs_block_properties():
+    rng = np.random.default_rng(7)
+    for x in blocks(rng, 200):
+        amax = float(np.max(np.abs(x)))
+        for fmt in (4, 8):
+            sb, c = oracle.psq_encode_block(x, fmt, False)
+            s = float(np.uint32(sb << 16).view(np.float32))
+            if amax == 0.0 or s == 0.0:
+                assert s == 0.0 and not c.any()
+                continue
+            target = amax / (10.0 if fmt == 4 else 448.0)
+            assert abs(s - target) <= target * 2.0 ** -8 + 1e-45   # one bf16 rounding
+            if fmt == 4:
+                # each code is the nearest codebook point to x/s (ties down),
+                # up to the rounding of |x| * (1/s) in f32
+                a = np.abs(x.astype(np.float64)) / s
+                for ai, ci in zip(a, c):
+                    d = np.abs(ai - MAGS)
+                    assert d[ci & 7] <= d.min() + 1e-5 * max(1.0, ai)
+            else:
+                inv = np.float32(1.0) / np.float32(s)
+                assert np.array_equal(c, oracle.e4m3_encode((x * inv).astype(np.float32)))
+
+
+def test_lsq1_scale_is_least_squares_fit():
+    rng = np.random.default_rng(8)
+    for x in blocks(rng, 200):
+        for fmt in (4, 8):
+            sb0, c0 = oracle.psq_encode_block(x, fmt, False)
+            if sb0 == 0:
+                continue
+            q = (oracle.cb10_decode(c0) if fmt == 4 else oracle.e4m3_decode(c0)).astype(np.float64)
+            num, den = float(np.dot(x.astype(np.float64), q)), float(np.dot(q, q))
+            sb, c = oracle.psq_encode_block(x, fmt, True)
+            s1 = float(np.uint32(sb << 16).view(np.float32))
+            if den == 0 or num <= 0:
+                assert s1 == 0.0 and not c.any()
+                continue
+            ls = num / den
+            # the closed form, rounded to bf16 (f32 sums: a few ulps of slack)
+            assert abs(s1 - ls) <= ls * (2.0 ** -8 + 1e-5)
+            # device (butterfly) and host (sequential) orders agree to a bf16 ulp
+            sbh, _ = oracle.psq_encode_block(x, fmt, True, device_order=False)
+            assert abs(int(sbh) - int(sb)) <= 1
+
+
+# ------------------------------------------------------------------ append
+def psq_pools(lay, fmt):
+    nb = lay.scale_elems * (lay.head_dim // 32)
+    cb = 16 if fmt == 4 else 32
+    return (np.full(nb * cb, 0xA5, np.uint8), np.full(nb * cb, 0x5A, np.uint8),
+            np.full(nb, 0x1234, np.uint16), np.full(nb, 0x4321, np.uint16))
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("lsq1", [False, True])
+def test_append_psq_layout_and_skip_rules(fmt, lsq1):
+    rng = np.random.default_rng(9 + fmt)
+    lay = paged_layout(rng, [40, 17, 5], 16, 2, 64, spare_pages=2)
+    rows = 12
+    slots = np.array([0, 1, 2, 0, 1, 2, 7, 0, 1, 2, 0, 2], np.uint32)   # slot 7: invalid
+    pos = np.array([0, 3, 4, 39, 16, 1, 2, 95, 5, 2, 20, 3], np.uint32)  # 95: past the table
+    bt = lay.block_tables.copy()
+    bt[2, 0] = INVALID   # slot 2 rows hit an invalid page
+    k_in = bf16_normal(rng, (rows, lay.kv_heads * lay.head_dim), 0.05)
+    v_in = bf16_normal(rng, (rows, lay.kv_heads * lay.head_dim), 0.05)
+    kc, vc, ks, vs = psq_pools(lay, fmt)
+    kc0, ks0 = kc.copy(), ks.copy()
+    g = dict(lay.geom, max_sequences=3)
+    oracle.kv_append_psq(g, k_in, v_in, slots, pos, bt, kc, vc, ks, vs, fmt, lsq1)
+    bph, cbytes = lay.head_dim // 32, (16 if fmt == 4 else 32)
+    written = np.zeros(ks.size, bool)
+    for r in range(rows):
+        s, p = int(slots[r]), int(pos[r])
+        if s >= 3 or p // 16 >= bt.shape[1] or bt[s, p // 16] >= lay.num_pages:
+            continue
+        page, off = int(bt[s, p // 16]), p % 16
+        for h in range(lay.kv_heads):
+            for b in range(bph):
+                bi = ((page * 16 + off) * lay.kv_heads + h) * bph + b
+                written[bi] = True
+                x = oracle.bf16_to_f32(k_in[r, h * lay.head_dim + 32 * b:][:32])
+                sb, codes = oracle.psq_encode_block(x, fmt, lsq1)
+                assert ks[bi] == sb
+                blk = kc[bi * cbytes:(bi + 1) * cbytes]
+                if fmt == 4:
+                    assert np.array_equal(blk, (codes[:16] & 15) | ((codes[16:] & 15) << 4))
+                else:
+                    assert np.array_equal(blk, codes)
+    # nothing else was touched
+    assert np.array_equal(ks[~written], ks0[~written])
+    untouched = np.repeat(~written, cbytes)
+    assert np.array_equal(kc[untouched], kc0[untouched])
+    assert written.sum() == 6 * lay.kv_heads * bph   # rows 0,1,3,4,8,10
+
+
+# --------------------------------------------------------------- attention
+def dequant(code, scale, fmt, nb):
+    s = oracle.bf16_to_f32(scale).astype(np.float64)
+    if fmt == 4:
+        b = code.reshape(nb, 16)
+        c = np.concatenate([b & 15, b >> 4], axis=1)
+        v = oracle.cb10_decode(c).astype(np.float64)
+    else:
+        v = oracle.e4m3_decode(code.reshape(nb, 32)).astype(np.float64)
+    return v * s[:, None]   # [nb, 32]
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_attention_psq_matches_float64(fmt):
+    rng = np.random.default_rng(20 + fmt)
+    seq = [37, 16, 1]
+    lay = paged_layout(rng, seq, 16, 2, 64, spare_pages=1)
+    H = 4
+    D = lay.head_dim
+    k_in = bf16_normal(rng, (sum(seq), lay.kv_heads * D), 0.05)
+    v_in = bf16_normal(rng, (sum(seq), lay.kv_heads * D), 0.05)
+    slots = np.repeat(np.arange(3, dtype=np.uint32), seq)
+    pos = np.concatenate([np.arange(n, dtype=np.uint32) for n in seq])
+    kc, vc, ks, vs = psq_pools(lay, fmt)
+    oracle.kv_append_psq(lay.geom, k_in, v_in, slots, pos, lay.block_tables, kc, vc, ks, vs, fmt, False)
+    nb = ks.size
+    K = dequant(kc, ks, fmt, nb).reshape(lay.num_pages, 16, lay.kv_heads, D)
+    V = dequant(vc, vs, fmt, nb).reshape(lay.num_pages, 16, lay.kv_heads, D)
+    q = bf16_normal(rng, (3, H * D))
+    qpos = np.array([36, 15, 0], np.uint32)
+    g = dict(lay.geom, q_heads=H)
+    out = oracle.paged_attention_psq(g, q, np.arange(3), qpos, lay.block_tables, kc, vc, ks, vs, fmt)
+    qf = oracle.bf16_to_f32(q).astype(np.float64)
+    for r in range(3):
+        n = int(qpos[r]) + 1
+        pages = lay.block_tables[r, :(n + 15) // 16]
+        for h in range(H):
+            kvh = h // (H // lay.kv_heads)
+            kk = K[pages, :, kvh].reshape(-1, D)[:n]
+            vv = V[pages, :, kvh].reshape(-1, D)[:n]
+            sc = kk @ qf[r, h * D:(h + 1) * D] / math.sqrt(D)
+            p = np.exp(sc - sc.max())
+            want = p @ vv / p.sum()
+            np.testing.assert_allclose(out[r, h * D:(h + 1) * D], want, rtol=1e-4, atol=1e-5)
