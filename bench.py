@@ -33,6 +33,9 @@ HBM_PEAK_GBPS = 8000.0
 BYTES_PER_TOKEN_FP8 = 2 * 4 * 256 + 2 * 4 * 4 + 4 / 16      # 2080.25
 BYTES_PER_TOKEN_BF16 = 2 * 4 * 256 * 2 + 4 / 16              # 4096.25
 APPEND_BYTES_PER_ROW_FP8 = 2 * 4 * 256 * 2 + 8 + 4 + 2 * 4 * 256 + 2 * 4 * 4   # 6188
+# PSQ: per (token, kv head) K and V codes (hd/2 or hd bytes) + hd/32 bf16 block scales
+BYTES_PER_TOKEN_PSQ = {4: 2 * 4 * (128 + 16) + 4 / 16, 8: 2 * 4 * (256 + 16) + 4 / 16}
+APPEND_BYTES_PER_ROW_PSQ = {f: 2 * 4 * 256 * 2 + 8 + 4 + BYTES_PER_TOKEN_PSQ[f] - 4 / 16 for f in (4, 8)}
 # HBM bytes per main-line decode launch measured with rocprofv3 --pmc on this
 # kernel (FETCH_SIZE 2,139,725 KiB x 2.0 calibration + WRITE_SIZE 6,208 KiB).
 DECODE_TRAFFIC_BYTES = 2139725 * 1024 * 2 + 6208 * 1024
@@ -59,7 +62,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5")
+    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,psq")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times), the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -212,6 +215,109 @@ def run_append(torch, ops, rows, steps, warmup, dev, seed=7):
             launch()
     ms = t.ms() / steps
     return ms, rows * APPEND_BYTES_PER_ROW_FP8
+
+
+def run_psq(torch, ops, steps, warmup, dev):
+    """PSQ4_W32 / PSQ8_W32 KV: decode at the north-star shape (batch 64, ctx
+    32768, 24/4 heads, hd256, page 16; planner-chosen split + combine) and the
+    append of 2^16 rows (MaxAbs and LSQ1)."""
+    import ctypes as C
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8, check, lib
+    L = lib()
+    s = torch.cuda.current_stream().cuda_stream
+    res = {}
+    rows, ctx, QH, H, D, P = 64, 32768, 24, 4, 256, 16
+    for fmt in (4, 8):
+        pages = rows * ctx // P
+        g = ops.PoolGeometry(1, pages, P, H, D)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(fmt)
+        nb, cb = g.psq_blocks, g.psq_code_bytes(fmt)
+        kc = torch.randint(0, 126, (cb,), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
+        vc = torch.randint(0, 126, (cb,), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
+        ks = (torch.rand(nb, generator=gen, device=dev) * 0.01 + 1e-3).to(torch.bfloat16)
+        vs = (torch.rand(nb, generator=gen, device=dev) * 0.01 + 1e-3).to(torch.bfloat16)
+        perm = torch.randperm(pages, generator=torch.Generator().manual_seed(fmt)).to(torch.int32)
+        bt = perm.view(rows, ctx // P).to(dev)
+        q = torch.randn((rows, QH * D), generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty((rows, QH * D), dtype=torch.bfloat16, device=dev)
+        slots = torch.arange(rows, dtype=torch.int32, device=dev)
+        pos = torch.full((rows,), ctx - 1, dtype=torch.int32, device=dev)
+        kvd = KV_PSQ4 if fmt == 4 else KV_PSQ8
+        splits, pps = ops.choose_decode_split(rows, QH, H, D, P, False, [ctx] * rows, 1 << 40,
+                                              kv_dtype=kvd)
+        a = ops.attention_args(g, 0, q, out, slots, pos, bt, QH)
+        part = torch.empty(ops.split_partials_bytes(rows, QH, H, splits) // 4, device=dev)
+        ptrs = (kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr())
+
+        def split_launch():
+            check("psq split", L.psk_attention_paged_psq_split_ex(
+                C.byref(a), kvd, *ptrs, D // 32, part.data_ptr(), splits, pps, s))
+
+        def reduce_launch():
+            check("reduce", L.psk_attention_paged_split_reduce_ex(C.byref(a), part.data_ptr(),
+                                                                  splits, pps, s))
+
+        def step():
+            split_launch()
+            reduce_launch()
+
+        warm(torch, step, warmup)
+        t = Timer(torch)
+        with t:
+            for _ in range(steps):
+                step()
+        step_ms = t.ms() / steps
+        t1 = Timer(torch)
+        with t1:
+            for _ in range(steps):
+                split_launch()
+        k_ms = t1.ms() / steps
+        nbytes = rows * ctx * BYTES_PER_TOKEN_PSQ[fmt] + rows * QH * D * 2
+        res[f"psq{fmt}_decode_b64_ctx32k"] = dict(
+            GBps=round(nbytes / (step_ms * 1e-3) / 1e9, 1), ms_per_step=round(step_ms, 4),
+            split_kernel_ms=round(k_ms, 4),
+            kernel_GBps=round(nbytes / (k_ms * 1e-3) / 1e9, 1),
+            frac_of_peak=round(nbytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            tokens_per_s=round(rows * ctx / (step_ms * 1e-3), 1),
+            bytes_per_step=nbytes, splits=splits, pages_per_split=pps)
+        del kc, vc, ks, vs, part
+        torch.cuda.empty_cache()
+
+        # append: 2^16 rows, one page-slot each (as the FP8 append line)
+        arows = 1 << 16
+        seqs = arows // P
+        ga = ops.PoolGeometry(1, seqs + 16, P, H, D)
+        rng = np.random.default_rng(7)
+        abt = torch.from_numpy(rng.permutation(seqs + 16)[:seqs].astype(np.int32).reshape(seqs, 1)).to(dev)
+        aslots = torch.from_numpy(np.repeat(np.arange(seqs), P).astype(np.int32)).to(dev)
+        apos = torch.from_numpy(np.tile(np.arange(P), seqs).astype(np.int32)).to(dev)
+        prm = torch.from_numpy(rng.permutation(arows)).to(dev)
+        aslots, apos = aslots[prm].contiguous(), apos[prm].contiguous()
+        kin = torch.randn((arows, H * D), generator=gen, device=dev).to(torch.bfloat16)
+        vin = torch.randn((arows, H * D), generator=gen, device=dev).to(torch.bfloat16)
+        akc = torch.empty(ga.psq_code_bytes(fmt), dtype=torch.uint8, device=dev)
+        avc = torch.empty_like(akc)
+        aks = torch.empty(ga.psq_blocks, dtype=torch.int16, device=dev)
+        avs = torch.empty_like(aks)
+        for est, name in ((0, "maxabs"), (1, "lsq1")):
+            def launch():
+                ops.kv_append_psq(ga, 0, kin, vin, aslots, apos, abt, akc, avc, aks, avs, fmt, est)
+
+            warm(torch, launch, warmup)
+            t = Timer(torch)
+            with t:
+                for _ in range(steps):
+                    launch()
+            ms = t.ms() / steps
+            nb_ = arows * APPEND_BYTES_PER_ROW_PSQ[fmt]
+            res[f"psq{fmt}_append_{name}_rows_{arows}"] = dict(
+                tokens_per_s=round(arows / (ms * 1e-3), 1), kernel_ms=round(ms, 5),
+                GBps=round(nb_ / (ms * 1e-3) / 1e9, 1),
+                frac_of_peak=round(nb_ / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+        del kin, vin, akc, avc, aks, avs
+        torch.cuda.empty_cache()
+    return res
 
 
 def run_mixed_step(torch, ops, steps, warmup, dev):
@@ -394,7 +500,7 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 5}))
         return
-    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5"}
+    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5", "psq"}
     extra = {}
 
     # ---- main: north-star point, FP8 batch 64 @ 32k
@@ -438,6 +544,9 @@ def main():
                                       GBps=round(nb / (ms * 1e-3) / 1e9, 1),
                                       frac_of_peak=round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
         extra["kv_append_fp8"] = ap
+
+    if "psq" in only:
+        extra["psq_kv"] = run_psq(torch, ops, args.steps, args.warmup, dev)
 
     if "cfg5" in only:
         extra["cfg5_mixed_step"] = run_mixed_step(torch, ops, max(5, args.steps // 2),

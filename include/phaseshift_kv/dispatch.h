@@ -41,8 +41,8 @@ struct PagedAttentionStep {
     KVCacheDType kv_dtype = KVCacheDType::BF16;
     const void* k_pool = nullptr;
     const void* v_pool = nullptr;
-    const float* k_scale_pool = nullptr;
-    const float* v_scale_pool = nullptr;
+    const void* k_scale_pool = nullptr;                 // FP8: f32; PSQ: bf16 block scales
+    const void* v_scale_pool = nullptr;
     const StepRequest* requests = nullptr;              // host array
     uint32_t num_requests = 0;
     uint32_t max_visible_tokens = 0;
@@ -83,8 +83,9 @@ struct PagedAttentionPlan {
 // whose units finish first under the decode kernel's XCD-aware dispatch, given
 // the rows' visible lengths (row_visible, host array; nullptr: every row at
 // max_visible_tokens) and the partials workspace. splits == 1: do not split.
+// kv_dtype: PSK_KV_* (KVCacheDType value).
 DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_heads,
-                                uint32_t head_dim, uint32_t kv_bytes, uint32_t page_tokens,
+                                uint32_t head_dim, uint32_t kv_dtype, uint32_t page_tokens,
                                 uint32_t max_visible_tokens, const uint32_t* row_visible,
                                 uint64_t partial_bytes);
 Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionPlan& plan);

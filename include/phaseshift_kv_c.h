@@ -400,8 +400,8 @@ typedef struct psk_step_plan_t {
 } psk_step_plan_t;
 
 int psk_paged_attention_step(const psk_paged_attention_args* common, uint32_t kv_dtype,
-                             const void* k_pool, const void* v_pool, const float* k_scale_pool,
-                             const float* v_scale_pool, const psk_step_request* requests,
+                             const void* k_pool, const void* v_pool, const void* k_scale_pool,
+                             const void* v_scale_pool, const psk_step_request* requests,
                              uint32_t num_requests, uint32_t max_visible_tokens, float* partials,
                              uint64_t partial_bytes, psk_step_plan_t* plan_out, void* stream);
 

@@ -173,7 +173,7 @@ extern "C" uint32_t psk_sequence_block_table(const psk_sequence* s, uint32_t* ou
 
 extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, uint32_t kv_dtype,
                                         const void* k_pool, const void* v_pool,
-                                        const float* k_scale_pool, const float* v_scale_pool,
+                                        const void* k_scale_pool, const void* v_scale_pool,
                                         const psk_step_request* requests, uint32_t num_requests,
                                         uint32_t max_visible_tokens, float* partials,
                                         uint64_t partial_bytes, psk_step_plan_t* plan_out,
@@ -182,8 +182,10 @@ extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, 
     if (common == nullptr || (num_requests > 0 && requests == nullptr)) return hipErrorInvalidValue;
     PagedAttentionStep step;
     std::memcpy(&step.common, common, sizeof(step.common));
-    step.kv_dtype = kv_dtype == PSK_KV_FP8_E4M3 ? KVCacheDType::FP8_E4M3 : KVCacheDType::BF16;
-    if (kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_BF16) return hipErrorInvalidValue;
+    if (kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_BF16 && kv_dtype != PSK_KV_PSQ4_W32 &&
+        kv_dtype != PSK_KV_PSQ8_W32)
+        return hipErrorInvalidValue;
+    step.kv_dtype = static_cast<KVCacheDType>(kv_dtype);
     step.k_pool = k_pool;
     step.v_pool = v_pool;
     step.k_scale_pool = k_scale_pool;
@@ -225,9 +227,11 @@ extern "C" int psk_choose_decode_split(const psk_paged_attention_args* a, uint32
     if (a == nullptr || splits == nullptr || pages_per_split == nullptr || a->kv_heads == 0u ||
         a->q_heads % a->kv_heads != 0u || a->page_tokens == 0u)
         return hipErrorInvalidValue;
-    if (kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_BF16) return hipErrorInvalidValue;
+    if (kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_BF16 && kv_dtype != PSK_KV_PSQ4_W32 &&
+        kv_dtype != PSK_KV_PSQ8_W32)
+        return hipErrorInvalidValue;
     const DecodeSplit s = choose_decode_split(a->rows, a->kv_heads, a->q_heads, a->head_dim,
-                                              kv_dtype == PSK_KV_FP8_E4M3 ? 1u : 2u, a->page_tokens,
+                                              kv_dtype, a->page_tokens,
                                               max_visible_tokens, row_visible, partial_bytes);
     *splits = s.splits;
     *pages_per_split = s.pages_per_split;

@@ -88,7 +88,7 @@ double split_makespan(const std::vector<double>& units, uint32_t slots, double c
 }  // namespace
 
 DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_heads,
-                                uint32_t head_dim, uint32_t kv_bytes, uint32_t page_tokens,
+                                uint32_t head_dim, uint32_t kv_dtype, uint32_t page_tokens,
                                 uint32_t max_visible_tokens, const uint32_t* row_visible,
                                 uint64_t partial_bytes) {
     DecodeSplit best;
@@ -101,13 +101,18 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
             pages[r] = std::min(max_pages, (row_visible[r] + page_tokens - 1) / page_tokens);
     const uint32_t q_per_kv = q_heads / kv_heads;
     const uint32_t groups = (kv_heads + 3u) / 4u;   // independent-wave workgroups per unit
-    const size_t lds = psk::decode_workgroup_lds_bytes(kv_bytes == 1 ? PSK_KV_FP8_E4M3 : PSK_KV_BF16, head_dim);
+    const size_t lds = psk::decode_workgroup_lds_bytes(kv_dtype, head_dim);
     const uint32_t per_cu = std::max<uint32_t>(1u, (uint32_t)((160u * 1024u) / lds));
     const uint32_t slots = std::max<uint32_t>(1u, device_cus() / kXcds) * per_cu;
     const uint64_t total_slots = (uint64_t)slots * kXcds;
     // Start-up of a workgroup (unit scan, block-table window, first chunk
     // latency, epilogue), fitted on MI355X: ~8 pages of FP8 hd256 x 4 heads.
-    const double page_bytes = 4.0 * page_tokens * (head_dim * (double)kv_bytes + (kv_bytes == 1 ? 8 : 0));
+    // K bytes of a (token, head) slice plus its scales, per page of 4 heads
+    const double slice = kv_dtype == PSK_KV_BF16        ? 2.0 * head_dim
+                         : kv_dtype == PSK_KV_FP8_E4M3  ? head_dim + 8.0
+                         : kv_dtype == PSK_KV_PSQ4_W32  ? head_dim / 2.0 + head_dim / 16.0
+                                                        : head_dim + head_dim / 16.0;
+    const double page_bytes = 4.0 * page_tokens * slice;
     const double c0 = 8.0 * 16 * 4 * (256 + 8) / page_bytes;
     // Candidates (predicted makespan, splits, pages per split); splits == 1
     // competes when the rows alone fill every slot (it saves the combine pass,
@@ -206,8 +211,9 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
     plan = PagedAttentionPlan{};
     const auto& c = step.common;
     if (c.rows == 0) return Status::make_ok();
-    if (step.kv_dtype != KVCacheDType::BF16 && step.kv_dtype != KVCacheDType::FP8_E4M3)
-        return Status::invalid_argument("KV cache dtype not provided by this build");
+    const bool psq = step.kv_dtype == KVCacheDType::PSQ4_W32 || step.kv_dtype == KVCacheDType::PSQ8_W32;
+    if (step.kv_dtype != KVCacheDType::BF16 && step.kv_dtype != KVCacheDType::FP8_E4M3 && !psq)
+        return Status::invalid_argument("unknown KV cache dtype");
     const uint64_t pbytes = step.partials ? step.partial_bytes : 0;
     auto push = [&](const PlannedKernel& k) -> Status {
         if (plan.count >= kMaxPlannedKernels) return Status::out_of_range("too many launches in a step");
@@ -234,7 +240,7 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
                 row_vis[j - row_begin] = std::min(r.max_visible, step.max_visible_tokens);
         }
         const DecodeSplit s = choose_decode_split(
-            rows, c.kv_heads, c.q_heads, c.head_dim, step.kv_dtype == KVCacheDType::FP8_E4M3 ? 1u : 2u,
+            rows, c.kv_heads, c.q_heads, c.head_dim, static_cast<uint32_t>(step.kv_dtype),
             c.page_tokens, step.max_visible_tokens, row_vis.data(), pbytes);
         k.splits = s.splits;
         k.pages_per_split = s.pages_per_split;
@@ -253,7 +259,9 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         next = r.row_begin + r.row_count;
     }
     if (next != c.rows) partition = false;
-    if (!partition) return add_decode(0, c.rows);
+    // PSQ pools have no tile kernel: every row of the step is a decode row
+    // (each attends to its own prefix, the reference's causal rule).
+    if (!partition || psq) return add_decode(0, c.rows);
 
     // decode launches: maximal runs of consecutive non-tile requests
     for (size_t i = 0; i < reqs.size();) {
@@ -313,6 +321,9 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
                                        hipStream_t stream) {
     using namespace ::ps::kernel;
     const bool fp8 = step.kv_dtype == KVCacheDType::FP8_E4M3;
+    const bool psq = step.kv_dtype == KVCacheDType::PSQ4_W32 || step.kv_dtype == KVCacheDType::PSQ8_W32;
+    const auto* ksf = static_cast<const float*>(step.k_scale_pool);
+    const auto* vsf = static_cast<const float*>(step.v_scale_pool);
     const auto* k8 = static_cast<const ::ps::qwen35::fp8e4m3_storage_t*>(step.k_pool);
     const auto* v8 = static_cast<const ::ps::qwen35::fp8e4m3_storage_t*>(step.v_pool);
     const auto* k16 = static_cast<const bf16_t*>(step.k_pool);
@@ -321,7 +332,24 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
         const PlannedKernel& k = plan.kernels[i];
         const PagedAttentionCommonArgs a = region_args(step.common, k.row_begin, k.rows);
         hipError_t e = hipSuccess;
-        if (k.kind == PlannedKernel::Kind::Tile) {
+        if (psq) {
+            const auto* ca = reinterpret_cast<const psk_paged_attention_args*>(&a);
+            const auto* kc = static_cast<const uint8_t*>(step.k_pool);
+            const auto* vc = static_cast<const uint8_t*>(step.v_pool);
+            const auto* ks = static_cast<const uint16_t*>(step.k_scale_pool);
+            const auto* vs = static_cast<const uint16_t*>(step.v_scale_pool);
+            const uint32_t kvd = static_cast<uint32_t>(step.kv_dtype);
+            const uint32_t bph = a.head_dim / 32u;
+            if (k.splits > 1) {
+                e = static_cast<hipError_t>(psk_attention_paged_psq_split_ex(
+                    ca, kvd, kc, vc, ks, vs, bph, step.partials, k.splits, k.pages_per_split, stream));
+                if (e == hipSuccess)
+                    e = launch_attention_paged_split_reduce_ex(a, step.partials, k.splits,
+                                                               k.pages_per_split, stream);
+            } else {
+                e = static_cast<hipError_t>(psk_attention_paged_psq(ca, kvd, kc, vc, ks, vs, bph, stream));
+            }
+        } else if (k.kind == PlannedKernel::Kind::Tile) {
             // tile rows are relative to the launch region
             std::vector<uint32_t> tb(k.tile_count), tr(k.tile_count);
             for (uint32_t t = 0; t < k.tile_count; ++t) {
@@ -331,8 +359,8 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
             const psk_paged_attention_args* ca = reinterpret_cast<const psk_paged_attention_args*>(&a);
             const uint32_t kvd = fp8 ? PSK_KV_FP8_E4M3 : PSK_KV_BF16;
             if (psk::paged_tiles_supported(*ca, kvd, step.k_pool, step.v_pool)) {
-                e = psk::launch_paged_tiles(*ca, kvd, step.k_pool, step.v_pool, step.k_scale_pool,
-                                            step.v_scale_pool, tb.data(), tr.data(), k.tile_count,
+                e = psk::launch_paged_tiles(*ca, kvd, step.k_pool, step.v_pool, ksf,
+                                            vsf, tb.data(), tr.data(), k.tile_count,
                                             step.partials, k.splits, k.pages_per_split, stream);
                 for (uint32_t q = 0; e == hipSuccess && k.splits > 1 && q < k.req_count; ++q) {
                     const StepRequest& r = plan.combine[k.req_first + q];
@@ -349,14 +377,12 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
                 // shapes outside the tile kernel: every row of each tile on the decode kernel
                 for (uint32_t t = 0; e == hipSuccess && t < k.tile_count; ++t) {
                     const PagedAttentionCommonArgs ta = region_args(a, tb[t], tr[t]);
-                    e = fp8 ? launch_attention_paged_fp8_e4m3(ta, k8, v8, step.k_scale_pool,
-                                                              step.v_scale_pool, stream)
+                    e = fp8 ? launch_attention_paged_fp8_e4m3(ta, k8, v8, ksf, vsf, stream)
                             : launch_attention_paged_bf16(ta, k16, v16, stream);
                 }
             }
         } else if (k.splits > 1) {
-            e = fp8 ? launch_attention_paged_fp8_e4m3_split(a, k8, v8, step.k_scale_pool,
-                                                            step.v_scale_pool, step.partials,
+            e = fp8 ? launch_attention_paged_fp8_e4m3_split(a, k8, v8, ksf, vsf, step.partials,
                                                             k.splits, k.pages_per_split, stream)
                     : static_cast<hipError_t>(psk_attention_paged_bf16_split_ex(
                           reinterpret_cast<const psk_paged_attention_args*>(&a), k16, v16,
@@ -365,8 +391,7 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
                 e = launch_attention_paged_split_reduce_ex(a, step.partials, k.splits,
                                                            k.pages_per_split, stream);
         } else {
-            e = fp8 ? launch_attention_paged_fp8_e4m3(a, k8, v8, step.k_scale_pool,
-                                                      step.v_scale_pool, stream)
+            e = fp8 ? launch_attention_paged_fp8_e4m3(a, k8, v8, ksf, vsf, stream)
                     : launch_attention_paged_bf16(a, k16, v16, stream);
         }
         if (e != hipSuccess) return e;

@@ -137,16 +137,19 @@ def split_partials_bytes(rows: int, q_heads: int, kv_heads: int, splits: int) ->
 
 
 def choose_decode_split(rows: int, q_heads: int, kv_heads: int, head_dim: int, page_tokens: int,
-                        fp8: bool, visible, partial_bytes: int) -> tuple[int, int]:
+                        fp8: bool, visible, partial_bytes: int,
+                        kv_dtype: int | None = None) -> tuple[int, int]:
     """(splits, pages_per_split) the step planner would use for a decode launch
-    over rows with these visible lengths (host sequence of ints)."""
+    over rows with these visible lengths (host sequence of ints). kv_dtype
+    (KV_*) overrides fp8."""
     import numpy as np
     a = PagedAttentionArgs()
     a.rows, a.q_heads, a.kv_heads, a.head_dim, a.page_tokens = rows, q_heads, kv_heads, head_dim, page_tokens
     vis = np.ascontiguousarray(np.asarray(visible, dtype=np.uint32))
     sp, pp = C.c_uint32(0), C.c_uint32(0)
     check("psk_choose_decode_split", lib().psk_choose_decode_split(
-        C.byref(a), KV_FP8 if fp8 else KV_BF16, vis.ctypes.data, int(vis.max()), partial_bytes,
+        C.byref(a), kv_dtype if kv_dtype is not None else (KV_FP8 if fp8 else KV_BF16),
+        vis.ctypes.data, int(vis.max()), partial_bytes,
         C.byref(sp), C.byref(pp)))
     return sp.value, pp.value
 

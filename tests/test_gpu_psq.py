@@ -359,3 +359,29 @@ def test_append_then_attend(dev, fmt):
     g = dict(lay.geom, q_heads=24)
     want = oracle.paged_attention_psq(g, q, qs, qp, lay.block_tables, okc, ovc, oks, ovs, fmt)
     assert np.max(np.abs(got - want)) < TOL
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_planner_step_over_psq_pools(dev, fmt):
+    """psk_paged_attention_step with PSQ pools: decode rows and a 16-row
+    verify block in one step, planned and launched by the library."""
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8, state
+    rng = np.random.default_rng(44 + fmt)
+    lens = [3000, 40, 700, 16 + 900]
+    lay = paged_layout(rng, lens, 16, 4, 256, spare_pages=1)
+    pools = dev_pools(lay, fmt, dev, seed=44 + fmt)
+    slots = np.array([0, 1, 2] + [3] * 16, np.uint32)
+    pos = np.array([2999, 39, 699] + list(range(900, 916)), np.uint32)
+    q = bf16_normal(rng, (19, 24 * 256))
+    out = torch.full((19, 24 * 256), 7.0, dtype=torch.float32, device=dev)
+    a = ops.attention_args(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                           to_dev(lay.block_tables), 24)
+    nbytes = 256 << 20
+    part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    reqs = [(0, 1, 0, 3000), (1, 1, 0, 40), (2, 1, 0, 700), (3, 16, 1, 916)]
+    plan = state.plan_step(a, KV_PSQ4 if fmt == 4 else KV_PSQ8, reqs, 3000, nbytes, part,
+                           *pools, launch=True)
+    torch.cuda.synchronize()
+    assert plan.count == 1 and plan.kernels[0].rows == 19
+    want = oracle_attn(lay, fmt, 24, q, slots, pos, lay.block_tables, pools)
+    assert np.max(np.abs(out.cpu().numpy() - want)) < TOL

@@ -103,3 +103,27 @@ def test_choose_decode_split_export():
     assert sp <= 2
     sp, pp = ops.choose_decode_split(64, 24, 4, 256, 16, True, [1000] * 64, 1 << 40)
     assert sp == 1   # below the reference's 2048-token split threshold
+
+
+def test_psq_steps_run_every_row_on_decode():
+    """PSQ pools have no tile kernel: the config-5 request mix becomes one
+    decode launch over all rows, split by the chooser."""
+    reqs = ([(i, 1, 0) for i in range(48)] + [(48 + 16 * i, 16, 1) for i in range(8)] +
+            [(176 + 512 * i, 512, 2) for i in range(8)])
+    for dt in (P.KV_PSQ4, P.KV_PSQ8):
+        plan = state.plan_step(args(4272), dt, reqs, 16384, 256 << 20)
+        ks = kernels(plan)
+        assert len(ks) == 1 and ks[0][:3] == (0, 0, 4272)
+        plan = state.plan_step(args(64), dt, [(i, 1, 0) for i in range(64)], 32768, 1 << 30)
+        assert kernels(plan)[0][3] > 1
+
+
+def test_psq_choose_decode_split_and_unknown_dtype():
+    from phaseshift_amd import ops
+    import pytest
+    for dt in (P.KV_PSQ4, P.KV_PSQ8):
+        sp, pp = ops.choose_decode_split(64, 24, 4, 256, 16, False, [32768] * 64, 1 << 40,
+                                         kv_dtype=dt)
+        assert sp > 1 and sp * pp >= 2048
+    with pytest.raises(P.HipError):
+        ops.choose_decode_split(64, 24, 4, 256, 16, False, [32768] * 64, 1 << 40, kv_dtype=2)
