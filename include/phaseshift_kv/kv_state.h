@@ -61,7 +61,11 @@ public:
     PagedKVPool& operator=(PagedKVPool&& o) noexcept;
 
     // K/V pools [layers][num_pages][page_tokens][kv_heads][head_dim] (bf16 or
-    // e4m3 bytes) and, for FP8, scale pools [layers][num_pages][page_tokens][kv_heads].
+    // e4m3 bytes) and, for FP8, f32 scale pools [layers][num_pages][page_tokens][kv_heads].
+    // PSQ4_W32 / PSQ8_W32: code pools of 16 / 32 bytes per 32-value block and
+    // bf16 scale pools, one per block, block index
+    // ((((layer*num_pages + page)*page_tokens + off)*kv_heads + head)*head_dim/32 + d/32)
+    // (kv_cache_types.h:16-46; psq4 reserves 1152 B per token at 4 x 256).
     static Status create(PagedKVPool& out, uint32_t num_pages, uint32_t page_tokens,
                          uint32_t num_attention_layers, uint32_t kv_heads, uint32_t head_dim,
                          KVCacheDType dtype);
@@ -95,6 +99,7 @@ public:
 
     void* k_pool() const noexcept { return k_; }
     void* v_pool() const noexcept { return v_; }
+    // FP8: f32 scales; PSQ: the bf16 block scales (bit patterns) at this address
     float* k_scale_pool() const noexcept { return k_scale_; }
     float* v_scale_pool() const noexcept { return v_scale_; }
 

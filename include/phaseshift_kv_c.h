@@ -135,7 +135,7 @@ typedef struct psk_page_copy_pair {
 typedef struct psk_page_copy_args {
     void* dst_k;
     void* dst_v;
-    float* dst_k_scale;                /* FP8 only, else NULL */
+    float* dst_k_scale;                /* FP8: f32 scales; PSQ: bf16 block scales; BF16: NULL */
     float* dst_v_scale;
     const void* src_k;
     const void* src_v;
@@ -149,7 +149,7 @@ typedef struct psk_page_copy_args {
     uint32_t page_tokens;
     uint32_t kv_heads;
     uint32_t head_dim;
-    uint32_t kv_dtype;                 /* PSK_KV_BF16 / PSK_KV_FP8_E4M3 */
+    uint32_t kv_dtype;                 /* PSK_KV_* (PSQ: head_dim % 32 == 0) */
 } psk_page_copy_args;
 
 /* Row metadata descriptor: same layout as ps::runtime::DeviceRequestDescriptor

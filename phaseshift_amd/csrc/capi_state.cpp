@@ -43,13 +43,15 @@ extern "C" int psk_pool_create(psk_kv_pool** out, uint32_t num_pages, uint32_t p
                                uint32_t num_layers, uint32_t kv_heads, uint32_t head_dim,
                                uint32_t kv_dtype) {
     if (out == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    if (kv_dtype != PSK_KV_BF16 && kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_PSQ4_W32 &&
+        kv_dtype != PSK_KV_PSQ8_W32) {
+        g_last_error = "unknown KV cache dtype";
+        return PSK_ERR_INVALID_ARGUMENT;
+    }
     auto* h = new (std::nothrow) psk_kv_pool();
     if (h == nullptr) return PSK_ERR_INSUFFICIENT_MEMORY;
-    const Status st = PagedKVPool::create(
-        h->pool, num_pages, page_tokens, num_layers, kv_heads, head_dim,
-        kv_dtype == PSK_KV_FP8_E4M3 ? KVCacheDType::FP8_E4M3
-                                    : (kv_dtype == PSK_KV_BF16 ? KVCacheDType::BF16
-                                                               : KVCacheDType::PSQ4_W32));
+    const Status st = PagedKVPool::create(h->pool, num_pages, page_tokens, num_layers, kv_heads,
+                                          head_dim, static_cast<KVCacheDType>(kv_dtype));
     if (!st.ok()) {
         delete h;
         return to_code(st);
@@ -72,7 +74,7 @@ extern "C" int psk_pool_info(const psk_kv_pool* p, psk_pool_info_t* out) {
     out->num_layers = q.num_attention_layers();
     out->kv_heads = q.kv_heads();
     out->head_dim = q.head_dim();
-    out->kv_dtype = q.dtype() == KVCacheDType::FP8_E4M3 ? PSK_KV_FP8_E4M3 : PSK_KV_BF16;
+    out->kv_dtype = static_cast<uint32_t>(q.dtype());
     out->free_pages = q.num_free_pages();
     out->used_pages = q.used_count();
     out->reserved_bytes = q.reserved_bytes();

@@ -67,8 +67,12 @@ Status PagedKVPool::create(PagedKVPool& out, uint32_t num_pages, uint32_t page_t
     if (num_attention_layers == 0) return Status::invalid_argument("num_attention_layers must be > 0");
     if (kv_heads == 0) return Status::invalid_argument("kv_heads must be > 0");
     if (head_dim == 0) return Status::invalid_argument("head_dim must be > 0");
-    if (dtype != KVCacheDType::BF16 && dtype != KVCacheDType::FP8_E4M3)
-        return Status::invalid_argument("KV cache dtype not provided by this build");
+    const bool psq = dtype == KVCacheDType::PSQ4_W32 || dtype == KVCacheDType::PSQ8_W32;
+    if (dtype != KVCacheDType::BF16 && dtype != KVCacheDType::FP8_E4M3 && !psq)
+        return Status::invalid_argument("unknown KV cache dtype");
+    // PSQ: blocks of 32 values (kv_cache_types.h:16-46)
+    if (psq && head_dim % 32u != 0u)
+        return Status::invalid_argument("PSQ KV needs head_dim divisible by 32");
     PagedKVPool pool;
     pool.num_pages_ = num_pages;
     pool.page_tokens_ = page_tokens;
@@ -80,19 +84,26 @@ Status PagedKVPool::create(PagedKVPool& out, uint32_t num_pages, uint32_t page_t
     // The launcher structs carry elems_per_layer as uint32 (kv_append.h:40).
     if ((uint64_t)num_pages * page_tokens * kv_heads * head_dim > 0xFFFFFFFFull)
         return Status::invalid_argument("pool layer exceeds 2^32 elements");
-    const uint64_t scales = (uint64_t)num_attention_layers * num_pages * page_tokens * kv_heads;
-    const size_t eb = dtype == KVCacheDType::FP8_E4M3 ? 1 : 2;
-    Status st = alloc256(&pool.k_, elems * eb, "hipMalloc K pool");
+    const uint64_t slices = (uint64_t)num_attention_layers * num_pages * page_tokens * kv_heads;
+    // body bytes (bf16 values, E4M3 codes, PSQ4 nibbles) and scale bytes
+    // (FP8: f32 per slice; PSQ: bf16 per 32-value block)
+    const uint64_t body = dtype == KVCacheDType::BF16             ? elems * 2
+                          : dtype == KVCacheDType::PSQ4_W32       ? elems / 2
+                                                                  : elems;
+    const uint64_t scale_bytes = dtype == KVCacheDType::FP8_E4M3 ? slices * 4
+                                 : psq                           ? elems / 32 * 2
+                                                                 : 0;
+    Status st = alloc256(&pool.k_, body, "hipMalloc K pool");
     if (!st.ok()) return st;
-    st = alloc256(&pool.v_, elems * eb, "hipMalloc V pool");
+    st = alloc256(&pool.v_, body, "hipMalloc V pool");
     if (!st.ok()) return st;
-    pool.reserved_bytes_ = 2 * elems * eb;
-    if (dtype == KVCacheDType::FP8_E4M3) {
-        st = alloc256(reinterpret_cast<void**>(&pool.k_scale_), scales * 4, "hipMalloc K scales");
+    pool.reserved_bytes_ = 2 * body;
+    if (scale_bytes != 0) {
+        st = alloc256(reinterpret_cast<void**>(&pool.k_scale_), scale_bytes, "hipMalloc K scales");
         if (!st.ok()) return st;
-        st = alloc256(reinterpret_cast<void**>(&pool.v_scale_), scales * 4, "hipMalloc V scales");
+        st = alloc256(reinterpret_cast<void**>(&pool.v_scale_), scale_bytes, "hipMalloc V scales");
         if (!st.ok()) return st;
-        pool.reserved_bytes_ += 2 * scales * 4;
+        pool.reserved_bytes_ += 2 * scale_bytes;
     }
     pool.in_use_.assign(num_pages, false);
     pool.free_list_.reserve(num_pages);
@@ -176,7 +187,7 @@ Status PagedKVPool::copy_pages_from(const std::vector<PageId>& dst_pages, const 
     a.page_tokens = page_tokens_;
     a.kv_heads = kv_heads_;
     a.head_dim = head_dim_;
-    a.kv_dtype = dtype_ == KVCacheDType::FP8_E4M3 ? PSK_KV_FP8_E4M3 : PSK_KV_BF16;
+    a.kv_dtype = static_cast<uint32_t>(dtype_);
     const hipError_t e =
         psk::copy_pages_host_pairs(a, pairs.data(), static_cast<uint32_t>(pairs.size()), stream);
     if (e != hipSuccess) return Status::hip_error("copy_page_from", e);

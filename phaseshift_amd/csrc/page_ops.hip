@@ -48,26 +48,42 @@ __global__ __launch_bounds__(256) void gather_kernel(const psk_kv_gather_args a,
 }
 
 // ------------------------------------------------------------- page copy
+// Bytes of one page of one layer: the K (V) body and its scale rows.
+//   BF16  P*H*D*2, no scales        FP8   P*H*D, P*H f32 scales
+//   PSQ4  P*H*D/2, P*H*D/32 bf16    PSQ8  P*H*D, P*H*D/32 bf16
+// (PSQ blocks of a page are contiguous: block index ((layer*num_pages +
+// page)*P + off)*H*D/32 + ..., kv_append.hip:368-372.)
+__host__ __device__ inline void page_bytes(const psk_page_copy_args& a, uint64_t& body,
+                                           uint64_t& scales) {
+    const uint64_t th = (uint64_t)a.page_tokens * a.kv_heads;   // (token, head) slices
+    switch (a.kv_dtype) {
+        case PSK_KV_BF16: body = th * a.head_dim * 2u; scales = 0; break;
+        case PSK_KV_FP8_E4M3: body = th * a.head_dim; scales = th * 4u; break;
+        case PSK_KV_PSQ4_W32: body = th * a.head_dim / 2u; scales = th * (a.head_dim / 32u) * 2u; break;
+        default: body = th * a.head_dim; scales = th * (a.head_dim / 32u) * 2u; break;
+    }
+}
+
 // grid.x = page pairs * layers * 4 tensors (K, V, K-scale, V-scale); every
 // block copies one page body (or one page's scale rows) with 16 B accesses.
-__device__ __forceinline__ void copy_one(const psk_page_copy_args& a, uint32_t eb, uint32_t vec16,
+__device__ __forceinline__ void copy_one(const psk_page_copy_args& a, uint32_t vec16,
                                          uint32_t dst_page, uint32_t src_page, uint32_t layer,
                                          uint32_t tensor) {
     if (dst_page >= a.dst_num_pages || src_page >= a.src_num_pages) return;
-    const uint64_t page_elems = (uint64_t)a.page_tokens * a.kv_heads * a.head_dim;
-    const uint64_t page_scales = (uint64_t)a.page_tokens * a.kv_heads;
+    uint64_t body, scales;
+    page_bytes(a, body, scales);
     const uint8_t* s;
     uint8_t* d;
     uint64_t bytes;
     if (tensor < 2u) {
-        bytes = page_elems * eb;
+        bytes = body;
         const uint64_t so = ((uint64_t)layer * a.src_num_pages + src_page) * bytes;
         const uint64_t dof = ((uint64_t)layer * a.dst_num_pages + dst_page) * bytes;
         s = static_cast<const uint8_t*>(tensor == 0u ? a.src_k : a.src_v) + so;
         d = static_cast<uint8_t*>(tensor == 0u ? a.dst_k : a.dst_v) + dof;
     } else {
-        if (a.kv_dtype != PSK_KV_FP8_E4M3) return;
-        bytes = page_scales * 4u;
+        if (scales == 0u) return;
+        bytes = scales;
         const uint64_t so = ((uint64_t)layer * a.src_num_pages + src_page) * bytes;
         const uint64_t dof = ((uint64_t)layer * a.dst_num_pages + dst_page) * bytes;
         s = reinterpret_cast<const uint8_t*>(tensor == 2u ? a.src_k_scale : a.src_v_scale) + so;
@@ -81,12 +97,12 @@ __device__ __forceinline__ void copy_one(const psk_page_copy_args& a, uint32_t e
     }
 }
 
-__global__ __launch_bounds__(256) void copy_pages_kernel(const psk_page_copy_args a, uint32_t eb,
+__global__ __launch_bounds__(256) void copy_pages_kernel(const psk_page_copy_args a,
                                                          uint32_t vec16) {
     const uint32_t rest = blockIdx.x >> 2;
     const uint32_t pair = rest / a.num_layers;
     if (pair >= a.num_pairs) return;
-    copy_one(a, eb, vec16, a.pairs[pair].dst_page, a.pairs[pair].src_page, rest % a.num_layers,
+    copy_one(a, vec16, a.pairs[pair].dst_page, a.pairs[pair].src_page, rest % a.num_layers,
              blockIdx.x & 3u);
 }
 
@@ -98,12 +114,12 @@ struct InlinePairs {
 };
 
 __global__ __launch_bounds__(256) void copy_pages_inline_kernel(const psk_page_copy_args a,
-                                                                const InlinePairs pairs, uint32_t eb,
+                                                                const InlinePairs pairs,
                                                                 uint32_t vec16) {
     const uint32_t rest = blockIdx.x >> 2;
     const uint32_t pair = rest / a.num_layers;
     if (pair >= a.num_pairs) return;
-    copy_one(a, eb, vec16, pairs.p[pair].dst_page, pairs.p[pair].src_page, rest % a.num_layers,
+    copy_one(a, vec16, pairs.p[pair].dst_page, pairs.p[pair].src_page, rest % a.num_layers,
              blockIdx.x & 3u);
 }
 
@@ -380,20 +396,22 @@ extern "C" int psk_kv_gather(const psk_kv_gather_args* a, const void* pool, void
 
 namespace psk {
 namespace {
-hipError_t copy_validate(const psk_page_copy_args* a, uint32_t& eb, uint32_t& vec16) {
+hipError_t copy_validate(const psk_page_copy_args* a, uint32_t& vec16) {
     if (a == nullptr) return hipErrorInvalidValue;
     if (a->dst_k == nullptr || a->dst_v == nullptr || a->src_k == nullptr || a->src_v == nullptr ||
         a->num_layers == 0u || a->page_tokens == 0u || a->kv_heads == 0u || a->head_dim == 0u)
         return hipErrorInvalidValue;
-    if (a->kv_dtype != PSK_KV_BF16 && a->kv_dtype != PSK_KV_FP8_E4M3) return hipErrorInvalidValue;
-    if (a->kv_dtype == PSK_KV_FP8_E4M3 &&
-        (a->dst_k_scale == nullptr || a->dst_v_scale == nullptr || a->src_k_scale == nullptr ||
-         a->src_v_scale == nullptr))
+    const bool psq = a->kv_dtype == PSK_KV_PSQ4_W32 || a->kv_dtype == PSK_KV_PSQ8_W32;
+    if (a->kv_dtype != PSK_KV_BF16 && a->kv_dtype != PSK_KV_FP8_E4M3 && !psq)
         return hipErrorInvalidValue;
-    eb = a->kv_dtype == PSK_KV_FP8_E4M3 ? 1u : 2u;
+    if (psq && a->head_dim % 32u != 0u) return hipErrorInvalidValue;
+    const bool scaled = a->kv_dtype != PSK_KV_BF16;
+    if (scaled && (a->dst_k_scale == nullptr || a->dst_v_scale == nullptr ||
+                   a->src_k_scale == nullptr || a->src_v_scale == nullptr))
+        return hipErrorInvalidValue;
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16u == 0u; };
     vec16 = al(a->dst_k) && al(a->dst_v) && al(a->src_k) && al(a->src_v) &&
-            (a->kv_dtype != PSK_KV_FP8_E4M3 ||
+            (!scaled ||
              (al(a->dst_k_scale) && al(a->dst_v_scale) && al(a->src_k_scale) && al(a->src_v_scale)));
     return hipSuccess;
 }
@@ -403,8 +421,8 @@ hipError_t copy_validate(const psk_page_copy_args* a, uint32_t& eb, uint32_t& ve
 // go to the kernel by value.
 hipError_t copy_pages_host_pairs(const psk_page_copy_args& args, const psk_page_copy_pair* pairs,
                                  uint32_t n, hipStream_t stream) {
-    uint32_t eb = 0, vec16 = 0;
-    const hipError_t e = copy_validate(&args, eb, vec16);
+    uint32_t vec16 = 0;
+    const hipError_t e = copy_validate(&args, vec16);
     if (e != hipSuccess) return e;
     for (uint32_t b = 0; b < n; b += kInlinePairs) {
         psk_page_copy_args a = args;
@@ -415,7 +433,7 @@ hipError_t copy_pages_host_pairs(const psk_page_copy_args& args, const psk_page_
         const uint64_t blocks = (uint64_t)a.num_pairs * a.num_layers * 4u;
         if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
         hipLaunchKernelGGL(copy_pages_inline_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
-                           a, ip, eb, vec16);
+                           a, ip, vec16);
         const hipError_t le = hipGetLastError();
         if (le != hipSuccess) return le;
     }
@@ -428,13 +446,13 @@ extern "C" int psk_kv_copy_pages(const psk_page_copy_args* a, void* stream) {
     if (a == nullptr) return hipErrorInvalidValue;
     if (a->num_pairs == 0u) return hipSuccess;
     if (a->pairs == nullptr) return hipErrorInvalidValue;
-    uint32_t eb = 0, vec16 = 0;
-    const hipError_t e = psk::copy_validate(a, eb, vec16);
+    uint32_t vec16 = 0;
+    const hipError_t e = psk::copy_validate(a, vec16);
     if (e != hipSuccess) return e;
     const uint64_t blocks = (uint64_t)a->num_pairs * a->num_layers * 4u;
     if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
     hipLaunchKernelGGL(psk::copy_pages_kernel, dim3((uint32_t)blocks), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), *a, eb, vec16);
+                       static_cast<hipStream_t>(stream), *a, vec16);
     return hipGetLastError();
 }
 

@@ -10,19 +10,22 @@ from __future__ import annotations
 
 import ctypes as C
 
-from . import (KV_BF16, KV_FP8, PLAN_ONLY, PoolInfo, SequenceInfo, StepPlan, StepRequest, check,
+from . import (KV_BF16, KV_FP8, KV_PSQ4, KV_PSQ8, PLAN_ONLY, PoolInfo, SequenceInfo, StepPlan, StepRequest, check,
                check_state, lib)
 from .ops import PoolGeometry, _stream
 
 
 class KVPool:
-    def __init__(self, num_pages, page_tokens, num_layers, kv_heads, head_dim, fp8=True):
+    def __init__(self, num_pages, page_tokens, num_layers, kv_heads, head_dim, fp8=True,
+                 kv_dtype=None):
+        """kv_dtype (KV_BF16, KV_FP8, KV_PSQ4, KV_PSQ8) overrides fp8."""
         self._h = C.c_void_p()
+        self.kv_dtype = kv_dtype if kv_dtype is not None else (KV_FP8 if fp8 else KV_BF16)
         check_state("psk_pool_create", lib().psk_pool_create(
             C.byref(self._h), num_pages, page_tokens, num_layers, kv_heads, head_dim,
-            KV_FP8 if fp8 else KV_BF16))
+            self.kv_dtype))
         self.geom = PoolGeometry(num_layers, num_pages, page_tokens, kv_heads, head_dim)
-        self.fp8 = fp8
+        self.fp8 = self.kv_dtype == KV_FP8
 
     def close(self):
         if self._h:
@@ -59,6 +62,13 @@ class KVPool:
         """Views of the pools as torch tensors (no copy)."""
         i = self.info()
         g = self.geom
+        if self.kv_dtype in (KV_PSQ4, KV_PSQ8):
+            fmt = 4 if self.kv_dtype == KV_PSQ4 else 8
+            nc = g.psq_code_bytes(fmt)
+            return {"k": _wrap(torch, i.k_pool, nc, torch.uint8),
+                    "v": _wrap(torch, i.v_pool, nc, torch.uint8),
+                    "k_scale": _wrap(torch, i.k_scale_pool, g.psq_blocks, torch.int16),
+                    "v_scale": _wrap(torch, i.v_scale_pool, g.psq_blocks, torch.int16)}
         n = g.pool_elems
         dt = torch.uint8 if self.fp8 else torch.int16
         out = {"k": _wrap(torch, i.k_pool, n, dt), "v": _wrap(torch, i.v_pool, n, dt)}

@@ -385,3 +385,33 @@ def test_planner_step_over_psq_pools(dev, fmt):
     assert plan.count == 1 and plan.kernels[0].rows == 19
     want = oracle_attn(lay, fmt, 24, q, slots, pos, lay.block_tables, pools)
     assert np.max(np.abs(out.cpu().numpy() - want)) < TOL
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_psq_pool_reserved_bytes_and_page_copy(dev, fmt):
+    """PSQ pools in the host KV state: the reference's byte accounting
+    (test_qwen35_psq_kv_pool.hip: PSQ4 at 4 x 256 reserves 1152 B per token)
+    and byte-exact prefix-cache copies of code pages and block-scale rows."""
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8, state
+    kvd = KV_PSQ4 if fmt == 4 else KV_PSQ8
+    one = state.KVPool(1, 16, 1, 4, 256, kv_dtype=kvd)
+    per_token = 1152 if fmt == 4 else 2176
+    assert one.info().reserved_bytes == 16 * per_token and one.info().kv_dtype == kvd
+    L, NP, Pt, H, D = 2, 24, 16, 4, 256
+    active = state.KVPool(NP, Pt, L, H, D, kv_dtype=kvd)
+    cache = state.KVPool(NP, Pt, L, H, D, kv_dtype=kvd)
+    at, ct = active.tensors(torch), cache.tensors(torch)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    for t in at.values():
+        t.copy_(torch.randint(0, 255, t.shape, generator=gen, device=dev).to(t.dtype))
+    src = [active.allocate() for _ in range(20)]
+    dst = [cache.allocate() for _ in range(20)]
+    cache.copy_pages_from(active, dst, src)
+    torch.cuda.synchronize()
+    for k in ("k", "v", "k_scale", "v_scale"):
+        a = to_host(at[k]).reshape(L, NP, -1)
+        c = to_host(ct[k]).reshape(L, NP, -1)
+        assert np.array_equal(c[:, dst], a[:, src]), k
+    with pytest.raises(Exception):
+        state.KVPool(4, 16, 1, 4, 100, kv_dtype=kvd)   # head_dim not a multiple of 32
