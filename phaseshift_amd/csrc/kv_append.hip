@@ -270,10 +270,11 @@ __global__ __launch_bounds__(256) void kv_append_generic_kernel(const AppendPara
 }
 
 // ---------------------------------------------------------------- PSQ
-// One task = one 32-value block of one (row, K|V, kv head); 4 consecutive
-// lanes hold it, lane k the values 8k..8k+7 (one 16 B load). Tasks are
-// ordered (row, K|V, head, block) so a wave reads 16 consecutive blocks of
-// input and writes 16 consecutive code blocks.
+// One lane = one task = one 32-value block of one (row, K|V, kv head): the
+// block's 64 input bytes are four 16 B loads of that lane, so a wave reads 4
+// KB of consecutive input and every reduction of the block (amax, the LSQ1
+// sums) stays inside the lane. Tasks are ordered (row, K|V, head, block):
+// consecutive lanes read consecutive blocks and write consecutive code blocks.
 struct PsqAppendParams {
     psk_kv_append_args a;
     uint8_t* k_code;
@@ -282,9 +283,9 @@ struct PsqAppendParams {
     uint16_t* v_scale;
     uint32_t bph;           // blocks per head
     uint32_t head_blocks;   // kv_heads * bph
-    uint64_t tasks;         // rows * 2 * head_blocks
+    uint32_t tasks;         // rows * 2 * head_blocks (< 2^31, checked by the launcher)
     uint32_t vec_in;        // 16 B input loads legal
-    uint32_t vec_out;       // 8 B code stores legal
+    uint32_t vec_out;       // 16 B code stores legal
 };
 
 // psq_bf16_round (psq4_kv.h:9-18): round to bf16 by adding 0x7FFF plus the
@@ -295,13 +296,22 @@ __device__ __forceinline__ float psq_bf16_round(float v) {
     return __uint_as_float(u & 0xFFFF0000u);
 }
 
-// cb10_encode (psq_device.h:22-35): magnitude index of |x| * inv against the
-// midpoints 0.5 1.5 2.5 3.5 5 7 9 (NaN -> 7), sign in bit 3.
+// cb10_encode (psq_device.h:22-35): magnitude index of a = |x| * inv against
+// the midpoints 0.5 1.5 2.5 3.5 5 7 9 (7 above 9 and for NaN), sign in bit 3.
+// Computed without comparisons: min(ceil(a - 0.5), 4) counts the midpoints
+// up to 3.5, ceil((a - 5) / 2) clamped to [0, 3] those above 5 (the fma is
+// exact at every boundary), and the clamp written as 3 - clamp(3 - c) turns
+// a NaN into 3 + 4 = 7 (fmin/fmax return the non-NaN operand). Equal to the
+// reference's chain for every float a >= 0, checked exhaustively on the CPU
+// (tests/native/cb10_branchless.c).
 __device__ __forceinline__ uint32_t cb10_code(float x, float inv) {
+#pragma clang fp contract(off)
     const float a = __builtin_fabsf(x) * inv;
-    const uint32_t m = (a <= 0.5f) ? 0u : (a <= 1.5f) ? 1u : (a <= 2.5f) ? 2u : (a <= 3.5f) ? 3u
-                     : (a <= 5.0f) ? 4u : (a <= 7.0f) ? 5u : (a <= 9.0f) ? 6u : 7u;
-    return m | (x < 0.0f ? 8u : 0u);
+    const float t1 = __builtin_fminf(__builtin_ceilf(a - 0.5f), 4.0f);
+    const float c = __builtin_ceilf(__builtin_fmaf(a, 0.5f, -2.5f));
+    const float t2 = 3.0f - __builtin_fminf(__builtin_fmaxf(3.0f - c, 0.0f), 3.0f);
+    const uint32_t m = (uint32_t)(t1 + t2);
+    return m | (x < 0.0f ? 8u : 0u);   // -0.0 and NaN: no sign, as the reference
 }
 
 // cb10 value of a code: magnitudes 0 1 2 3 4 6 8 10.
@@ -311,127 +321,104 @@ __device__ __forceinline__ float cb10_value(uint32_t c) {
     return (c & 8u) ? -mag : mag;
 }
 
-// Lane k of a quad reads lane k^1 (CTRL 0xB1) or k^2 (0x4E).
-template <int CTRL>
-__device__ __forceinline__ float quad_swap(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
-__device__ __forceinline__ uint32_t quad_swap_u(uint32_t x) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
-}
-
+// Codes of the 32 values for scale s (all 0 unless s > 0): PSQ4 cb10 codes of
+// x * (1/s), PSQ8 SATFINITE E4M3 codes of x * (1/s) packed 4 per dword.
 template <bool kPsq4>
-__device__ __forceinline__ void psq_codes(const float (&x)[8], float s, uint32_t (&c)[8]) {
+__device__ __forceinline__ void psq_codes(const float (&x)[32], float s, uint32_t (&c)[32]) {
 #pragma clang fp contract(off)
     const float inv = 1.0f / s;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) c[i] = 0u;
-    if (!(s > 0.0f)) return;
+    const uint32_t keep = s > 0.0f ? 0xFFFFFFFFu : 0u;   // all codes 0 unless s > 0
     if constexpr (kPsq4) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) c[i] = cb10_code(x[i], inv);
+        for (int i = 0; i < 32; ++i) c[i] = cb10_code(x[i], inv) & keep;
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            const uint32_t w = e4m3_encode_pair(x[i] * inv, x[i + 1] * inv, 0u, false);
-            c[i] = w & 0xFFu;
-            c[i + 1] = (w >> 8) & 0xFFu;
+        for (int i = 0; i < 32; i += 4) {
+            const uint32_t w = e4m3_encode_pair(x[i + 2] * inv, x[i + 3] * inv,
+                                                e4m3_encode_pair(x[i] * inv, x[i + 1] * inv, 0u, false),
+                                                true);
+            c[i >> 2] = w & keep;   // c[0..7]: packed dwords
         }
     }
+}
+
+// Sum of v[0..31] in the order of the reference's 32-lane xor butterfly
+// (x += shfl_xor(x, o) for o = 16, 8, 4, 2, 1; kv_append.hip:293-299): the
+// tree (v[j] + v[j^16]), then ^8, ^4, ^2, ^1 on the partial sums.
+__device__ __forceinline__ float butterfly_sum32(float (&v)[32]) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1)
+#pragma unroll
+        for (int j = 0; j < o; ++j) v[j] = v[j] + v[j + o];
+    return v[0];
 }
 
 template <bool kPsq4, bool kLsq1>
 __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParams p) {
 #pragma clang fp contract(off)
     const psk_kv_append_args& a = p.a;
-    const uint64_t task = ((uint64_t)blockIdx.x * 256u + threadIdx.x) >> 2;
-    const uint32_t k = threadIdx.x & 3u;
-    if (task >= p.tasks) return;   // a quad is one task: it leaves whole
-    const uint32_t hb = (uint32_t)(task % p.head_blocks);
-    const uint64_t rest = task / p.head_blocks;
+    const uint32_t task = blockIdx.x * 256u + threadIdx.x;
+    if (task >= p.tasks) return;
+    const uint32_t rest = task / p.head_blocks;
+    const uint32_t hb = task - rest * p.head_blocks;
     const bool is_v = (rest & 1u) != 0u;
-    const uint32_t row = (uint32_t)(rest >> 1);
+    const uint32_t row = rest >> 1;
 
     // row -> (page, offset), the reference skip rules (kv_append.hip:335-360)
     const uint32_t slot = a.row_sequence_slots[row];
-    if (slot >= a.max_sequences) return;
     const uint32_t pos = a.row_positions[row];
+    const uint16_t* src = static_cast<const uint16_t*>(is_v ? a.v_input : a.k_input) +
+                          (uint64_t)row * (is_v ? a.v_row_stride : a.k_row_stride) +
+                          (uint64_t)hb * 32u;
+    // input loads go out before the block-table load, which waits on slot
+    float x[32];
+    if (p.vec_in) {
+        u32x4 w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = reinterpret_cast<const u32x4*>(src)[i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            x[2 * i] = __uint_as_float(w[i >> 2][i & 3] << 16);
+            x[2 * i + 1] = __uint_as_float(w[i >> 2][i & 3] & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = bf16_bits_to_f32(src[i]);
+    }
+    if (slot >= a.max_sequences) return;
     const uint32_t lb = pos / a.page_tokens;
     if (lb >= a.block_table_stride) return;
     const uint32_t page = a.block_tables[(uint64_t)slot * a.block_table_stride + lb];
     if (page >= a.num_pages) return;
     const uint32_t off = pos - lb * a.page_tokens;
 
-    const uint16_t* src = static_cast<const uint16_t*>(is_v ? a.v_input : a.k_input) +
-                          (uint64_t)row * (is_v ? a.v_row_stride : a.k_row_stride) +
-                          (uint64_t)hb * 32u + 8u * k;
-    float x[8];
-    if (p.vec_in) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(src);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[2 * i] = __uint_as_float(w[i] << 16);
-            x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = bf16_bits_to_f32(src[i]);
-    }
-
     // block amax (order-free; fmaxf drops NaN as the reference's does)
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
-    amax = __builtin_fmaxf(amax, quad_swap<0xB1>(amax));
-    amax = __builtin_fmaxf(amax, quad_swap<0x4E>(amax));
+    for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
     float s = amax > 0.0f ? psq_bf16_round(amax * (kPsq4 ? 0.1f : (1.0f / 448.0f))) : 0.0f;
-    uint32_t c[8];
+    uint32_t c[32];
     psq_codes<kPsq4>(x, s, c);
 
     if constexpr (kLsq1) {
-        // num = sum x q, den = sum q q over the block in the order of the
-        // reference's 32-lane xor butterfly (16, 8, 4, 2, 1): value j = 8k + i,
-        // so xor 16 is lane k^2, xor 8 lane k^1, xor 4/2/1 element i^4/^2/^1.
-        float nm[8], dn[8];
-        if constexpr (kPsq4) {
+        // num = sum x q, den = sum q q over the decoded codes, in the
+        // reference's butterfly order; s1 = bf16(num / den), then re-encode
+        float nm[32], dn[32];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float q = cb10_value(c[i]);
-                nm[i] = x[i] * q;
-                dn[i] = q * q;
+        for (int i = 0; i < 32; ++i) {
+            float q;
+            if constexpr (kPsq4) {
+                q = cb10_value(c[i]);
+            } else {
+                const f32x2 q2 = __builtin_amdgcn_cvt_pk_f32_fp8(c[i >> 2] >> (16 * ((i >> 1) & 1)), false);
+                q = (i & 1) ? q2[1] : q2[0];
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i += 2) {
-                const f32x2 q = __builtin_amdgcn_cvt_pk_f32_fp8(c[i] | (c[i + 1] << 8), false);
-                nm[i] = x[i] * q[0];
-                dn[i] = q[0] * q[0];
-                nm[i + 1] = x[i + 1] * q[1];
-                dn[i + 1] = q[1] * q[1];
-            }
+            nm[i] = x[i] * q;
+            dn[i] = q * q;
         }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            nm[i] = nm[i] + quad_swap<0x4E>(nm[i]);
-            dn[i] = dn[i] + quad_swap<0x4E>(dn[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            nm[i] = nm[i] + quad_swap<0xB1>(nm[i]);
-            dn[i] = dn[i] + quad_swap<0xB1>(dn[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            nm[i] = nm[i] + nm[i + 4];
-            dn[i] = dn[i] + dn[i + 4];
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            nm[i] = nm[i] + nm[i + 2];
-            dn[i] = dn[i] + dn[i + 2];
-        }
-        const float num = nm[0] + nm[1], den = dn[0] + dn[1];
+        const float num = butterfly_sum32(nm);
+        const float den = butterfly_sum32(dn);
         const float sl = den > 0.0f ? num / den : 0.0f;
         float s1 = psq_bf16_round(sl);
         if (!(s1 > 0.0f)) s1 = 0.0f;
@@ -443,41 +430,36 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
                          a.kv_heads) * p.bph + hb;
     uint8_t* code = is_v ? p.v_code : p.k_code;
     if constexpr (kPsq4) {
-        // byte j = code j | code j+16 << 4: lanes 0, 1 pair with lanes 2, 3
-        uint32_t own = 0u;
+        // byte j = code j | code j+16 << 4 (psq4_pack_codes, psq4_kv.h:73-77)
+        u32x4 w;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) own |= c[i] << (4 * i);
-        const uint32_t hi = quad_swap_u<0x4E>(own);
-        if (k < 2u) {
-            u32x2 w;
-            w[0] = 0u;
-            w[1] = 0u;
+        for (int d = 0; d < 4; ++d) {
+            uint32_t v = 0u;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t b = ((own >> (4 * i)) & 0xFu) | (((hi >> (4 * i)) & 0xFu) << 4);
-                w[i >> 2] |= b << (8 * (i & 3));
+            for (int b = 0; b < 4; ++b) {
+                const int j = 4 * d + b;
+                v |= ((c[j] & 0xFu) | ((c[j + 16] & 0xFu) << 4)) << (8 * b);
             }
-            uint8_t* dst = code + bi * 16u + 8u * k;
-            if (p.vec_out) {
-                *reinterpret_cast<u32x2*>(dst) = w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) dst[i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
-            }
+            w[d] = v;
         }
-    } else {
-        u32x2 w;
-        w[0] = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-        w[1] = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-        uint8_t* dst = code + bi * 32u + 8u * k;
+        uint8_t* dst = code + bi * 16u;
         if (p.vec_out) {
-            *reinterpret_cast<u32x2*>(dst) = w;
+            *reinterpret_cast<u32x4*>(dst) = w;
         } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) dst[i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+            for (int i = 0; i < 16; ++i) dst[i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+        }
+    } else {
+        uint8_t* dst = code + bi * 32u;
+        if (p.vec_out) {
+            reinterpret_cast<u32x4*>(dst)[0] = (u32x4){c[0], c[1], c[2], c[3]};
+            reinterpret_cast<u32x4*>(dst)[1] = (u32x4){c[4], c[5], c[6], c[7]};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) dst[i] = (uint8_t)(c[i >> 2] >> (8 * (i & 3)));
         }
     }
-    if (k == 0u) (is_v ? p.v_scale : p.k_scale)[bi] = (uint16_t)(__float_as_uint(s) >> 16);
+    (is_v ? p.v_scale : p.k_scale)[bi] = (uint16_t)(__float_as_uint(s) >> 16);
 }
 
 hipError_t validate(const psk_kv_append_args& c, const void* k_pool, const void* v_pool) {
@@ -563,12 +545,14 @@ hipError_t launch_psq(const psk_kv_append_args& c, bool psq4, uint8_t* kc, uint8
     p.v_scale = vs;
     p.bph = bph;
     p.head_blocks = c.kv_heads * bph;
-    p.tasks = (uint64_t)c.rows * 2u * p.head_blocks;
+    const uint64_t tasks = (uint64_t)c.rows * 2u * p.head_blocks;
+    if (tasks >= (1ull << 31)) return hipErrorInvalidValue;
+    p.tasks = (uint32_t)tasks;
     auto al = [](const void* ptr, uintptr_t n) { return reinterpret_cast<uintptr_t>(ptr) % n == 0u; };
     p.vec_in = (c.k_row_stride % 8u == 0u && c.v_row_stride % 8u == 0u && al(c.k_input, 16) &&
                 al(c.v_input, 16)) ? 1u : 0u;
-    p.vec_out = (al(kc, 8) && al(vc, 8)) ? 1u : 0u;
-    const uint64_t blocks = (p.tasks * 4u + 255u) / 256u;
+    p.vec_out = (al(kc, 16) && al(vc, 16)) ? 1u : 0u;
+    const uint64_t blocks = (tasks + 255u) / 256u;
     if (blocks == 0u || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
     const dim3 grid((uint32_t)blocks);
     if (psq4) {

@@ -74,6 +74,8 @@ def to_dev(a, device="cuda"):
     """numpy -> torch device tensor, bit-preserving (u32 -> i32, u16 -> i16)."""
     import torch
     a = np.ascontiguousarray(a)
+    if not a.flags.writeable:
+        a = a.copy()
     if a.dtype == np.uint32:
         a = a.view(np.int32)
     elif a.dtype == np.uint16:
