@@ -215,6 +215,14 @@ __device__ bool find_unit(const psk_paged_attention_args& a, uint32_t splits, ui
 
 constexpr uint32_t kPageWindow = 1024;   // block-table entries staged in LDS per pass
 
+// PSQ4 workgroups are VALU-bound (nibble expansion, per-block scales), so two
+// of them share a CU: a 512-entry window keeps the LDS of one under 80 KB and
+// the register budget is 256 per wave. Every other format runs one per CU.
+template <int FMT>
+constexpr uint32_t page_window() { return FMT == kFmtPsq4 ? 512u : kPageWindow; }
+template <int FMT>
+constexpr int waves_per_simd() { return FMT == kFmtPsq4 ? 2 : 1; }
+
 // LDS bytes of one pipeline stage of one wave: K and V of a chunk (lane-major
 // DMA layout) and, FP8 and PSQ, the k/v scales of its tokens (256 B per
 // 16-token half).
@@ -230,7 +238,7 @@ constexpr int stage_bytes() {
 // share one (row, kv_head, split) item, take its chunks round robin and merge
 // through LDS at the end (used when the independent grid cannot fill the GPU).
 template <int FMT, int D, bool kIndep, int NW>
-__global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_kernel(const DecodeParams p) {
     constexpr uint32_t NT = NW * 64;   // threads of the workgroup
     static_assert(kIndep || NW == kWaves, "the shared-item merge uses 4 waves");
     constexpr int KVB = FMT == kFmtBf16 ? 2 : 1;
@@ -251,7 +259,8 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
     // PSQ: dwords of block scales per token head (2 bf16 each); the scales of
     // a 16-token half sit dword-major in LDS: dword w of token t at 64w + 4t
     constexpr int SW = D / 64;
-    constexpr int kWinBytes = (int)kPageWindow * 4;
+    constexpr uint32_t kWin = page_window<FMT>();
+    constexpr int kWinBytes = (int)kWin * 4;
     // vector-memory operations of one issue(): K and V DMAs and the scale DMAs
     constexpr int kStepOps = H * (2 * NL + (KVB == 1 ? 2 : 0));
     constexpr uint32_t kStride = kIndep ? CT : NW * CT;   // a wave's chunk stride
@@ -340,10 +349,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(const DecodeParam
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    // One pass per window of kPageWindow pages (a single pass unless the
+    // One pass per window of kWin pages (a single pass unless the
     // split holds more pages than that).
-    for (uint32_t wp = pb; wp < pe; wp += kPageWindow) {
-        const uint32_t wp_end = min(pe, wp + kPageWindow);
+    for (uint32_t wp = pb; wp < pe; wp += kWin) {
+        const uint32_t wp_end = min(pe, wp + kWin);
         __syncthreads();
         for (uint32_t i = tid; i < wp_end - wp; i += NT) win[i] = bt[wp + i];
         __syncthreads();
@@ -804,7 +813,8 @@ size_t decode_workgroup_lds_bytes(uint32_t kv_dtype, uint32_t head_dim) {
     const size_t H = bf16 ? 1 : 2;
     const size_t cb = bf16 ? 2 * D : kv_dtype == PSK_KV_PSQ4_W32 ? D / 2 : D;
     const size_t stage = 2 * H * (16 * cb + 128) + (bf16 ? 0 : 2 * H * 256);
-    return (size_t)kPageWindow * 4 + (size_t)kWaves * 2 * stage;
+    const size_t win = kv_dtype == PSK_KV_PSQ4_W32 ? page_window<kFmtPsq4>() : kPageWindow;
+    return win * 4 + (size_t)kWaves * 2 * stage;
 }
 
 namespace {
@@ -814,7 +824,7 @@ hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t st
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     // block-table window + two pipeline stages per wave; the shared-item merge
     // later reuses the same LDS
-    const size_t v_bytes = (size_t)kPageWindow * 4 + (size_t)NW * 2 * stage_bytes<FMT, D>();
+    const size_t v_bytes = (size_t)page_window<FMT>() * 4 + (size_t)NW * 2 * stage_bytes<FMT, D>();
     const size_t m_bytes = kIndep ? 0 : (size_t)NW * 32 * sizeof(float) +
                                             (size_t)NW * qpk * D * sizeof(float);
     const size_t lds_bytes = v_bytes > m_bytes ? v_bytes : m_bytes;
