@@ -14,6 +14,7 @@
 // page copies of any number of pages and layers run as one kernel launch.
 #pragma once
 #include <phaseshift_kv/types.h>
+#include <phaseshift_kv_c.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -85,6 +86,14 @@ public:
     // Any number of (dst, src) page pairs in one launch per 32 pairs.
     Status copy_pages_from(const std::vector<PageId>& dst_pages, const PagedKVPool& src,
                            const std::vector<PageId>& src_pages, hipStream_t stream);
+    // The checked copy arguments and pairs of such a copy, for callers that
+    // batch it with other copies into one launch.
+    Status copy_pairs_from(const std::vector<PageId>& dst_pages, const PagedKVPool& src,
+                           const std::vector<PageId>& src_pages, psk_page_copy_args& args,
+                           std::vector<psk_page_copy_pair>& pairs) const;
+    // Bytes of one page of one layer: K (or V) body and scale rows.
+    uint64_t page_body_bytes() const noexcept;
+    uint64_t page_scale_bytes() const noexcept;
 
     uint32_t num_pages() const noexcept { return num_pages_; }
     uint32_t page_tokens() const noexcept { return page_tokens_; }

@@ -367,6 +367,89 @@ int psk_sequence_commit(psk_sequence* seq, uint32_t tokens);
 int psk_sequence_info(const psk_sequence* seq, psk_sequence_info_t* out);
 uint32_t psk_sequence_block_table(const psk_sequence* seq, uint32_t* out, uint32_t cap);
 
+/* ---- GDN recurrent-state pool [state/gdn_state_pool.h:41-200] ------------
+ * Per slot: bf16 conv history [states][conv_history][conv_history_stride]
+ * and f32 recurrent state [states][v_heads][head_k][head_v]. The prefix
+ * cache copies a sequence's slot (slot id = its sequence slot). */
+typedef struct psk_gdn_pool psk_gdn_pool;
+typedef struct psk_gdn_layout {
+    uint32_t num_gdn_states;
+    uint32_t conv_dim;
+    uint32_t conv_dim_padded;
+    uint32_t conv_history;
+    uint32_t conv_history_stride;
+    uint32_t num_v_heads;
+    uint32_t head_k;
+    uint32_t head_v;
+} psk_gdn_layout;
+typedef struct psk_gdn_pool_info_t {
+    void* conv_base;
+    void* recurrent_base;
+    uint64_t conv_slot_bytes;
+    uint64_t recurrent_slot_bytes;
+    uint64_t reserved_bytes;
+    uint32_t max_sequences;
+    uint32_t used_slots;
+} psk_gdn_pool_info_t;
+/* GdnStatePoolLayout::make [gdn_state_pool.h:52-66]: conv_dim padded to 8. */
+int psk_gdn_layout_make(uint32_t gdn_layers, uint32_t conv_dim, uint32_t conv_history,
+                        uint32_t num_v_heads, uint32_t head_k, uint32_t head_v,
+                        psk_gdn_layout* out);
+int psk_gdn_pool_create(psk_gdn_pool** out, uint32_t max_sequences, const psk_gdn_layout* layout);
+void psk_gdn_pool_destroy(psk_gdn_pool* pool);
+int psk_gdn_pool_info(const psk_gdn_pool* pool, psk_gdn_pool_info_t* out);
+int psk_gdn_pool_initialize(psk_gdn_pool* pool, uint32_t slot, void* stream);
+int psk_gdn_pool_reset(psk_gdn_pool* pool, uint32_t slot, void* stream);
+int psk_gdn_pool_release(psk_gdn_pool* pool, uint32_t slot);
+int psk_gdn_pool_copy_slot(psk_gdn_pool* dst, uint32_t dst_slot, const psk_gdn_pool* src,
+                           uint32_t src_slot, void* stream);
+
+/* ---- Prefix cache [runtime/prefix_cache.h:24-150, prefix_cache.cpp:84-486] -
+ * LRU checkpoints of (KV pages, GDN slot, optional DFlash ring) in cache-owned
+ * pools. save/restore move all of a checkpoint's bytes in one batched copy
+ * launch. Checkpoints are named by a stable id (0 = none). */
+typedef struct psk_prefix_cache psk_prefix_cache;
+/* The drafter's DFlash2 context ring [dflash2/context_state.h:15-27]. */
+typedef struct psk_dflash_context {
+    void* k_ring;
+    void* v_ring;
+    uint64_t ring_bytes;
+    uint32_t length;
+    uint32_t next_position;
+} psk_dflash_context;
+typedef struct psk_prefix_checkpoint_info {
+    uint64_t id;                       /* 0: no checkpoint */
+    uint64_t last_used;
+    uint32_t position;
+    uint32_t num_pages;
+    uint32_t cache_state_slot;
+    uint32_t dflash;
+} psk_prefix_checkpoint_info;
+typedef struct psk_prefix_cache_stats_t {
+    uint64_t lookups, hits, misses, inserts, duplicate_hits, evictions, skipped_too_large;
+    uint64_t restored_tokens, saved_tokens, save_d2d_bytes, restore_d2d_bytes, copy_launches;
+    uint64_t cache_kv_bytes, cache_gdn_bytes, dflash_ring_bytes;
+    uint32_t size, cache_pages, cache_free_pages, cache_free_slots, max_entries, capacity_tokens;
+} psk_prefix_cache_stats_t;
+int psk_prefix_cache_create(psk_prefix_cache** out, const psk_kv_pool* active_kv,
+                            const psk_gdn_pool* active_gdn, uint32_t capacity_tokens,
+                            uint32_t max_entries, uint32_t min_prefix_tokens);
+void psk_prefix_cache_destroy(psk_prefix_cache* cache);
+int psk_prefix_cache_enable_dflash_ring(psk_prefix_cache* cache, uint64_t ring_bytes);
+/* Longest cached prefix of tokens[0..n) (strictly shorter if asked); out->id
+ * is 0 on a miss. */
+int psk_prefix_cache_find_longest(psk_prefix_cache* cache, const int32_t* tokens, uint32_t n,
+                                  uint32_t strictly_shorter, psk_prefix_checkpoint_info* out);
+int psk_prefix_cache_save(psk_prefix_cache* cache, const psk_sequence* seq,
+                          const psk_gdn_pool* gdn, const psk_kv_pool* kv, const int32_t* tokens,
+                          uint32_t n, uint32_t prompt_boundary, const psk_dflash_context* dflash,
+                          void* stream);
+int psk_prefix_cache_restore(psk_prefix_cache* cache, psk_sequence* seq, psk_gdn_pool* gdn,
+                             psk_kv_pool* kv, uint64_t checkpoint_id, psk_dflash_context* dflash,
+                             void* stream);
+int psk_prefix_cache_clear(psk_prefix_cache* cache);
+int psk_prefix_cache_stats(const psk_prefix_cache* cache, psk_prefix_cache_stats_t* out);
+
 /* ---- Step planner (paged_attention_dispatch.hip:437-894) -------------------
  * Plans and launches the PAGED_ATTENTION binding of one mixed step. Requests
  * must partition [0, rows) in order (else the whole step is one decode

@@ -89,6 +89,39 @@ class StepPlan(C.Structure):
     _fields_ = [("count", C.c_uint32), ("kernels", PlannedKernel * 16)]
 
 
+class GdnLayout(C.Structure):
+    """psk_gdn_layout == GdnStatePoolLayout (gdn_state_pool.h:41-50)."""
+    _fields_ = [(n, C.c_uint32) for n in ("num_gdn_states", "conv_dim", "conv_dim_padded",
+                                          "conv_history", "conv_history_stride", "num_v_heads",
+                                          "head_k", "head_v")]
+
+
+class GdnPoolInfo(C.Structure):
+    _fields_ = [("conv_base", C.c_void_p), ("recurrent_base", C.c_void_p),
+                ("conv_slot_bytes", C.c_uint64), ("recurrent_slot_bytes", C.c_uint64),
+                ("reserved_bytes", C.c_uint64), ("max_sequences", C.c_uint32),
+                ("used_slots", C.c_uint32)]
+
+
+class DFlashContext(C.Structure):
+    _fields_ = [("k_ring", C.c_void_p), ("v_ring", C.c_void_p), ("ring_bytes", C.c_uint64),
+                ("length", C.c_uint32), ("next_position", C.c_uint32)]
+
+
+class CheckpointInfo(C.Structure):
+    _fields_ = [("id", C.c_uint64), ("last_used", C.c_uint64)] + [
+        (n, C.c_uint32) for n in ("position", "num_pages", "cache_state_slot", "dflash")]
+
+
+class PrefixCacheStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "lookups", "hits", "misses", "inserts", "duplicate_hits", "evictions", "skipped_too_large",
+        "restored_tokens", "saved_tokens", "save_d2d_bytes", "restore_d2d_bytes", "copy_launches",
+        "cache_kv_bytes", "cache_gdn_bytes", "dflash_ring_bytes")] + [
+        (n, C.c_uint32) for n in ("size", "cache_pages", "cache_free_pages", "cache_free_slots",
+                                  "max_entries", "capacity_tokens")]
+
+
 PSK_ERR = {1001: "invalid_argument", 1002: "out_of_range", 1003: "invalid_state",
            1004: "insufficient_memory", 1005: "hip_error"}
 PLAN_ONLY = C.c_void_p(~0 & 0xFFFFFFFFFFFFFFFF)
@@ -157,6 +190,22 @@ SIGNATURES = {
     "psk_sequence_commit": [_P, _U32],
     "psk_sequence_info": [_P, _P],
     "psk_sequence_block_table": [_P, _P, _U32],
+    "psk_gdn_layout_make": [_U32, _U32, _U32, _U32, _U32, _U32, _P],
+    "psk_gdn_pool_create": [_P, _U32, _P],
+    "psk_gdn_pool_destroy": [_P],
+    "psk_gdn_pool_info": [_P, _P],
+    "psk_gdn_pool_initialize": [_P, _U32, _P],
+    "psk_gdn_pool_reset": [_P, _U32, _P],
+    "psk_gdn_pool_release": [_P, _U32],
+    "psk_gdn_pool_copy_slot": [_P, _U32, _P, _U32, _P],
+    "psk_prefix_cache_create": [_P, _P, _P, _U32, _U32, _U32],
+    "psk_prefix_cache_destroy": [_P],
+    "psk_prefix_cache_enable_dflash_ring": [_P, C.c_uint64],
+    "psk_prefix_cache_find_longest": [_P, _P, _U32, _U32, _P],
+    "psk_prefix_cache_save": [_P, _P, _P, _P, _P, _U32, _U32, _P, _P],
+    "psk_prefix_cache_restore": [_P, _P, _P, _P, C.c_uint64, _P, _P],
+    "psk_prefix_cache_clear": [_P],
+    "psk_prefix_cache_stats": [_P, _P],
     "psk_paged_attention_step": [_P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _P, C.c_uint64, _P, _P],
     "psk_choose_decode_split": [_P, _U32, _P, _U32, C.c_uint64, _P, _P],
     "psk_selftest_e4m3_encode_range": [_U32, _U32, _P, _P],
@@ -168,6 +217,8 @@ SIGNATURES = {
 _RESTYPE = {
     "psk_last_error_message": C.c_char_p,
     "psk_pool_destroy": None,
+    "psk_gdn_pool_destroy": None,
+    "psk_prefix_cache_destroy": None,
     "psk_slot_pool_destroy": None,
     "psk_slot_pool_block_tables": C.c_void_p,
     "psk_sequence_block_table": C.c_uint32,

@@ -1,6 +1,7 @@
 // C-ABI over the host KV state and the step planner (opaque handles).
 #include <phaseshift_kv/dispatch.h>
 #include <phaseshift_kv/kv_state.h>
+#include <phaseshift_kv/prefix_cache.h>
 #include <phaseshift_kv_c.h>
 
 #include <cstring>
@@ -18,6 +19,12 @@ struct psk_slot_pool {
 };
 struct psk_sequence {
     PagedSequenceState seq;
+};
+struct psk_gdn_pool {
+    GdnStatePool pool;
+};
+struct psk_prefix_cache {
+    PrefixCache cache;
 };
 
 namespace {
@@ -238,4 +245,201 @@ extern "C" int psk_choose_decode_split(const psk_paged_attention_args* a, uint32
     *splits = s.splits;
     *pages_per_split = s.pages_per_split;
     return hipSuccess;
+}
+
+// ------------------------------------------------------------ GDN pool
+static GdnStatePoolLayout from_c(const psk_gdn_layout& l) {
+    GdnStatePoolLayout o;
+    o.num_gdn_states = l.num_gdn_states;
+    o.conv_dim = l.conv_dim;
+    o.conv_dim_padded = l.conv_dim_padded;
+    o.conv_history = l.conv_history;
+    o.conv_history_stride = l.conv_history_stride;
+    o.num_v_heads = l.num_v_heads;
+    o.head_k = l.head_k;
+    o.head_v = l.head_v;
+    return o;
+}
+
+extern "C" int psk_gdn_layout_make(uint32_t gdn_layers, uint32_t conv_dim, uint32_t conv_history,
+                                   uint32_t num_v_heads, uint32_t head_k, uint32_t head_v,
+                                   psk_gdn_layout* out) {
+    if (out == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    const GdnStatePoolLayout l =
+        GdnStatePoolLayout::make(gdn_layers, conv_dim, conv_history, num_v_heads, head_k, head_v);
+    *out = {l.num_gdn_states, l.conv_dim,    l.conv_dim_padded, l.conv_history,
+            l.conv_history_stride, l.num_v_heads, l.head_k, l.head_v};
+    return 0;
+}
+
+extern "C" int psk_gdn_pool_create(psk_gdn_pool** out, uint32_t max_sequences,
+                                   const psk_gdn_layout* layout) {
+    if (out == nullptr || layout == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    auto* h = new (std::nothrow) psk_gdn_pool();
+    if (h == nullptr) return PSK_ERR_INSUFFICIENT_MEMORY;
+    const Status st = GdnStatePool::create(h->pool, max_sequences, from_c(*layout));
+    if (!st.ok()) {
+        delete h;
+        return to_code(st);
+    }
+    *out = h;
+    return 0;
+}
+
+extern "C" void psk_gdn_pool_destroy(psk_gdn_pool* p) { delete p; }
+
+extern "C" int psk_gdn_pool_info(const psk_gdn_pool* p, psk_gdn_pool_info_t* out) {
+    if (p == nullptr || out == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    out->conv_base = p->pool.conv_base();
+    out->recurrent_base = p->pool.recurrent_base();
+    out->conv_slot_bytes = p->pool.layout().conv_slot_bytes();
+    out->recurrent_slot_bytes = p->pool.layout().recurrent_slot_bytes();
+    out->reserved_bytes = p->pool.reserved_bytes();
+    out->max_sequences = p->pool.max_sequences();
+    out->used_slots = p->pool.num_used_slots();
+    return 0;
+}
+
+extern "C" int psk_gdn_pool_initialize(psk_gdn_pool* p, uint32_t slot, void* stream) {
+    if (p == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(p->pool.initialize(slot, S(stream)));
+}
+
+extern "C" int psk_gdn_pool_reset(psk_gdn_pool* p, uint32_t slot, void* stream) {
+    if (p == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(p->pool.reset(slot, S(stream)));
+}
+
+extern "C" int psk_gdn_pool_release(psk_gdn_pool* p, uint32_t slot) {
+    if (p == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(p->pool.release(slot));
+}
+
+extern "C" int psk_gdn_pool_copy_slot(psk_gdn_pool* dst, uint32_t dst_slot, const psk_gdn_pool* src,
+                                      uint32_t src_slot, void* stream) {
+    if (dst == nullptr || src == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(dst->pool.copy_slot_from(dst_slot, src->pool, src_slot, S(stream)));
+}
+
+// --------------------------------------------------------- prefix cache
+extern "C" int psk_prefix_cache_create(psk_prefix_cache** out, const psk_kv_pool* active_kv,
+                                       const psk_gdn_pool* active_gdn, uint32_t capacity_tokens,
+                                       uint32_t max_entries, uint32_t min_prefix_tokens) {
+    if (out == nullptr || active_kv == nullptr || active_gdn == nullptr)
+        return PSK_ERR_INVALID_ARGUMENT;
+    auto* h = new (std::nothrow) psk_prefix_cache();
+    if (h == nullptr) return PSK_ERR_INSUFFICIENT_MEMORY;
+    const Status st = PrefixCache::create(h->cache, active_kv->pool, active_gdn->pool,
+                                          capacity_tokens, max_entries, min_prefix_tokens);
+    if (!st.ok()) {
+        delete h;
+        return to_code(st);
+    }
+    *out = h;
+    return 0;
+}
+
+extern "C" void psk_prefix_cache_destroy(psk_prefix_cache* c) { delete c; }
+
+extern "C" int psk_prefix_cache_enable_dflash_ring(psk_prefix_cache* c, uint64_t ring_bytes) {
+    if (c == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    return to_code(c->cache.enable_dflash_ring(ring_bytes));
+}
+
+static void info_of(const PrefixCheckpoint* cp, psk_prefix_checkpoint_info* out) {
+    *out = psk_prefix_checkpoint_info{};
+    if (cp == nullptr) return;
+    out->id = cp->id;
+    out->last_used = cp->last_used;
+    out->position = cp->position;
+    out->num_pages = static_cast<uint32_t>(cp->cache_pages.size());
+    out->cache_state_slot = cp->cache_state_slot;
+    out->dflash = cp->dflash ? 1u : 0u;
+}
+
+extern "C" int psk_prefix_cache_find_longest(psk_prefix_cache* c, const int32_t* tokens, uint32_t n,
+                                             uint32_t strictly_shorter,
+                                             psk_prefix_checkpoint_info* out) {
+    if (c == nullptr || out == nullptr || (n > 0 && tokens == nullptr)) return PSK_ERR_INVALID_ARGUMENT;
+    info_of(c->cache.find_longest(std::vector<int32_t>(tokens, tokens + n), strictly_shorter != 0u),
+            out);
+    return 0;
+}
+
+static DFlashContextView view_of(const psk_dflash_context& d) {
+    DFlashContextView v;
+    v.k_ring = d.k_ring;
+    v.v_ring = d.v_ring;
+    v.ring_bytes = d.ring_bytes;
+    v.length = d.length;
+    v.next_position = d.next_position;
+    return v;
+}
+
+extern "C" int psk_prefix_cache_save(psk_prefix_cache* c, const psk_sequence* seq,
+                                     const psk_gdn_pool* gdn, const psk_kv_pool* kv,
+                                     const int32_t* tokens, uint32_t n, uint32_t prompt_boundary,
+                                     const psk_dflash_context* dflash, void* stream) {
+    if (c == nullptr || seq == nullptr || gdn == nullptr || kv == nullptr ||
+        (n > 0 && tokens == nullptr))
+        return PSK_ERR_INVALID_ARGUMENT;
+    DFlashContextView v;
+    if (dflash != nullptr) v = view_of(*dflash);
+    return to_code(c->cache.save(seq->seq, gdn->pool, kv->pool, std::vector<int32_t>(tokens, tokens + n),
+                                 S(stream), prompt_boundary != 0u, dflash ? &v : nullptr));
+}
+
+extern "C" int psk_prefix_cache_restore(psk_prefix_cache* c, psk_sequence* seq, psk_gdn_pool* gdn,
+                                        psk_kv_pool* kv, uint64_t checkpoint_id,
+                                        psk_dflash_context* dflash, void* stream) {
+    if (c == nullptr || seq == nullptr || gdn == nullptr || kv == nullptr)
+        return PSK_ERR_INVALID_ARGUMENT;
+    const PrefixCheckpoint* cp = c->cache.find_id(checkpoint_id);
+    if (cp == nullptr) {
+        g_last_error = "prefix restore: no checkpoint with this id";
+        return PSK_ERR_INVALID_ARGUMENT;
+    }
+    DFlashContextView v;
+    if (dflash != nullptr) v = view_of(*dflash);
+    const int rc = to_code(c->cache.restore(seq->seq, gdn->pool, kv->pool, *cp, S(stream),
+                                            dflash ? &v : nullptr));
+    if (rc == 0 && dflash != nullptr) {
+        dflash->length = v.length;
+        dflash->next_position = v.next_position;
+    }
+    return rc;
+}
+
+extern "C" int psk_prefix_cache_clear(psk_prefix_cache* c) {
+    if (c == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    c->cache.clear();
+    return 0;
+}
+
+extern "C" int psk_prefix_cache_stats(const psk_prefix_cache* c, psk_prefix_cache_stats_t* out) {
+    if (c == nullptr || out == nullptr) return PSK_ERR_INVALID_ARGUMENT;
+    const PrefixCacheStats& s = c->cache.stats();
+    *out = psk_prefix_cache_stats_t{};
+    out->lookups = s.lookups;
+    out->hits = s.hits;
+    out->misses = s.misses;
+    out->inserts = s.inserts;
+    out->duplicate_hits = s.duplicate_hits;
+    out->evictions = s.evictions;
+    out->skipped_too_large = s.skipped_too_large;
+    out->restored_tokens = s.restored_tokens;
+    out->saved_tokens = s.saved_tokens;
+    out->save_d2d_bytes = s.save_d2d_bytes;
+    out->restore_d2d_bytes = s.restore_d2d_bytes;
+    out->copy_launches = s.copy_launches;
+    out->cache_kv_bytes = c->cache.cache_kv_bytes();
+    out->cache_gdn_bytes = c->cache.cache_gdn_bytes();
+    out->dflash_ring_bytes = c->cache.dflash_ring_bytes();
+    out->size = static_cast<uint32_t>(c->cache.size());
+    out->cache_pages = c->cache.cache_pages();
+    out->cache_free_pages = c->cache.cache_free_pages();
+    out->cache_free_slots = c->cache.cache_free_slots();
+    out->max_entries = c->cache.max_entries();
+    out->capacity_tokens = c->cache.capacity_tokens();
+    return 0;
 }

@@ -8,13 +8,10 @@
 #include <phaseshift_kv/kv_state.h>
 #include <phaseshift_kv_c.h>
 
+#include "page_ops.h"
+
 #include <algorithm>
 #include <utility>
-
-namespace psk {
-hipError_t copy_pages_host_pairs(const psk_page_copy_args& args, const psk_page_copy_pair* pairs,
-                                 uint32_t n, hipStream_t stream);
-}
 
 namespace ps::qwen35 {
 
@@ -112,6 +109,25 @@ Status PagedKVPool::create(PagedKVPool& out, uint32_t num_pages, uint32_t page_t
     return Status::make_ok();
 }
 
+uint64_t PagedKVPool::page_body_bytes() const noexcept {
+    const uint64_t e = (uint64_t)page_tokens_ * kv_heads_ * head_dim_;
+    switch (dtype_) {
+        case KVCacheDType::BF16: return e * 2;
+        case KVCacheDType::PSQ4_W32: return e / 2;
+        default: return e;
+    }
+}
+
+uint64_t PagedKVPool::page_scale_bytes() const noexcept {
+    const uint64_t th = (uint64_t)page_tokens_ * kv_heads_;
+    switch (dtype_) {
+        case KVCacheDType::FP8_E4M3: return th * 4;
+        case KVCacheDType::PSQ4_W32:
+        case KVCacheDType::PSQ8_W32: return th * (head_dim_ / 32) * 2;
+        default: return 0;
+    }
+}
+
 Status PagedKVPool::allocate(PageId& page) {
     if (free_list_.empty()) return Status::insufficient_memory("KV page pool exhausted");
     page = free_list_.back();
@@ -155,15 +171,16 @@ Status PagedKVPool::copy_page_from(PageId dst_page, const PagedKVPool& src, Page
     return copy_pages_from({dst_page}, src, {src_page}, stream);
 }
 
-Status PagedKVPool::copy_pages_from(const std::vector<PageId>& dst_pages, const PagedKVPool& src,
-                                    const std::vector<PageId>& src_pages, hipStream_t stream) {
+Status PagedKVPool::copy_pairs_from(const std::vector<PageId>& dst_pages, const PagedKVPool& src,
+                                    const std::vector<PageId>& src_pages, psk_page_copy_args& a,
+                                    std::vector<psk_page_copy_pair>& pairs) const {
     if (dtype_ != src.dtype_) return Status::invalid_argument("KV page copy dtype mismatch");
     if (page_tokens_ != src.page_tokens_ || num_attention_layers_ != src.num_attention_layers_ ||
         kv_heads_ != src.kv_heads_ || head_dim_ != src.head_dim_)
         return Status::invalid_argument("KV page copy layout mismatch");
     if (dst_pages.size() != src_pages.size())
         return Status::invalid_argument("KV page copy list sizes differ");
-    std::vector<psk_page_copy_pair> pairs(dst_pages.size());
+    pairs.resize(dst_pages.size());
     for (size_t i = 0; i < dst_pages.size(); ++i) {
         if (dst_pages[i] >= num_pages_)
             return Status::invalid_argument("KV page copy destination out of range");
@@ -171,8 +188,7 @@ Status PagedKVPool::copy_pages_from(const std::vector<PageId>& dst_pages, const 
             return Status::invalid_argument("KV page copy source out of range");
         pairs[i] = {dst_pages[i], src_pages[i]};
     }
-    if (pairs.empty()) return Status::make_ok();
-    psk_page_copy_args a{};
+    a = psk_page_copy_args{};
     a.dst_k = k_;
     a.dst_v = v_;
     a.dst_k_scale = k_scale_;
@@ -188,6 +204,15 @@ Status PagedKVPool::copy_pages_from(const std::vector<PageId>& dst_pages, const 
     a.kv_heads = kv_heads_;
     a.head_dim = head_dim_;
     a.kv_dtype = static_cast<uint32_t>(dtype_);
+    return Status::make_ok();
+}
+
+Status PagedKVPool::copy_pages_from(const std::vector<PageId>& dst_pages, const PagedKVPool& src,
+                                    const std::vector<PageId>& src_pages, hipStream_t stream) {
+    psk_page_copy_args a{};
+    std::vector<psk_page_copy_pair> pairs;
+    Status st = copy_pairs_from(dst_pages, src, src_pages, a, pairs);
+    if (!st.ok() || pairs.empty()) return st;
     const hipError_t e =
         psk::copy_pages_host_pairs(a, pairs.data(), static_cast<uint32_t>(pairs.size()), stream);
     if (e != hipSuccess) return Status::hip_error("copy_page_from", e);

@@ -3,6 +3,7 @@
 //   u32 fill (block-table truncation), row metadata from request descriptors,
 //   the generic any-shape attention kernel, and the E4M3 encoder self-test.
 #include "device_common.h"
+#include "page_ops.h"
 
 #include <phaseshift_kv/paged_attention.h>
 
@@ -121,6 +122,47 @@ __global__ __launch_bounds__(256) void copy_pages_inline_kernel(const psk_page_c
     if (pair >= a.num_pairs) return;
     copy_one(a, vec16, pairs.p[pair].dst_page, pairs.p[pair].src_page, rest % a.num_layers,
              blockIdx.x & 3u);
+}
+
+// ------------------------------------------------------------ copy plan
+// One launch for a whole prefix-cache save or restore: the KV page pairs
+// above (blocks [0, page_blocks)) and up to kMaxCopySegments contiguous
+// segments (GDN state slots, DFlash rings), each cut into kSegmentBlockBytes
+// per workgroup.
+constexpr uint64_t kSegmentBlockBytes = 64u * 1024u;
+struct InlineSegments {
+    CopySegment s[kMaxCopySegments];
+    uint64_t first_block[kMaxCopySegments + 1];
+};
+
+__global__ __launch_bounds__(256) void copy_plan_kernel(const psk_page_copy_args a,
+                                                        const InlinePairs pairs,
+                                                        const InlineSegments segs, uint32_t nseg,
+                                                        uint32_t vec16, uint32_t page_blocks) {
+    if (blockIdx.x < page_blocks) {
+        const uint32_t rest = blockIdx.x >> 2;
+        const uint32_t pair = rest / a.num_layers;
+        if (pair >= a.num_pairs) return;
+        copy_one(a, vec16, pairs.p[pair].dst_page, pairs.p[pair].src_page, rest % a.num_layers,
+                 blockIdx.x & 3u);
+        return;
+    }
+    const uint64_t b = blockIdx.x - page_blocks;
+    uint32_t i = 0;
+    while (i + 1u < nseg && segs.first_block[i + 1] <= b) ++i;
+    if (i >= nseg || b >= segs.first_block[nseg]) return;
+    const CopySegment sg = segs.s[i];
+    const uint64_t off = (b - segs.first_block[i]) * kSegmentBlockBytes;
+    const uint64_t n = min(kSegmentBlockBytes, sg.bytes - off);
+    const uint8_t* src = static_cast<const uint8_t*>(sg.src) + off;
+    uint8_t* dst = static_cast<uint8_t*>(sg.dst) + off;
+    const bool al = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | n) & 15u) == 0u;
+    if (al) {
+        for (uint64_t o = (uint64_t)threadIdx.x * 16u; o < n; o += 256u * 16u)
+            *reinterpret_cast<u32x4*>(dst + o) = *reinterpret_cast<const u32x4*>(src + o);
+    } else {
+        for (uint64_t o = threadIdx.x; o < n; o += 256u) dst[o] = src[o];
+    }
 }
 
 // ------------------------------------------------------------------ fill
@@ -421,23 +463,61 @@ hipError_t copy_validate(const psk_page_copy_args* a, uint32_t& vec16) {
 // go to the kernel by value.
 hipError_t copy_pages_host_pairs(const psk_page_copy_args& args, const psk_page_copy_pair* pairs,
                                  uint32_t n, hipStream_t stream) {
+    return copy_plan_host(&args, pairs, n, nullptr, 0, stream);
+}
+
+// Page pairs (kv == nullptr or n == 0: none) and segments in as few launches
+// as the inline pair limit allows: the first launch carries every segment and
+// the first kInlinePairs pairs.
+hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair* pairs, uint32_t n,
+                          const CopySegment* segs, uint32_t nseg, hipStream_t stream) {
+    if (nseg > kMaxCopySegments) return hipErrorInvalidValue;
     uint32_t vec16 = 0;
-    const hipError_t e = copy_validate(&args, vec16);
-    if (e != hipSuccess) return e;
-    for (uint32_t b = 0; b < n; b += kInlinePairs) {
-        psk_page_copy_args a = args;
+    psk_page_copy_args base{};
+    if (kv != nullptr && n > 0) {
+        const hipError_t e = copy_validate(kv, vec16);
+        if (e != hipSuccess) return e;
+        base = *kv;
+    } else {
+        n = 0;
+        base.num_layers = 1;
+    }
+    InlineSegments is{};
+    uint64_t seg_blocks = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        if (segs[i].bytes != 0 && (segs[i].dst == nullptr || segs[i].src == nullptr))
+            return hipErrorInvalidValue;
+        is.s[i] = segs[i];
+        is.first_block[i] = seg_blocks;
+        seg_blocks += (segs[i].bytes + kSegmentBlockBytes - 1) / kSegmentBlockBytes;
+    }
+    is.first_block[nseg] = seg_blocks;
+    uint32_t b = 0;
+    do {
+        psk_page_copy_args a = base;
         a.num_pairs = n - b < kInlinePairs ? n - b : kInlinePairs;
         a.pairs = nullptr;
         InlinePairs ip{};
         for (uint32_t i = 0; i < a.num_pairs; ++i) ip.p[i] = pairs[b + i];
-        const uint64_t blocks = (uint64_t)a.num_pairs * a.num_layers * 4u;
+        const uint64_t page_blocks = (uint64_t)a.num_pairs * a.num_layers * 4u;
+        const uint32_t ns = b == 0 ? nseg : 0u;
+        const uint64_t blocks = page_blocks + (b == 0 ? seg_blocks : 0u);
         if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(copy_pages_inline_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream,
-                           a, ip, vec16);
-        const hipError_t le = hipGetLastError();
-        if (le != hipSuccess) return le;
-    }
+        if (blocks > 0) {
+            hipLaunchKernelGGL(copy_plan_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a, ip,
+                               is, ns, vec16, (uint32_t)page_blocks);
+            const hipError_t le = hipGetLastError();
+            if (le != hipSuccess) return le;
+        }
+        b += a.num_pairs;
+    } while (b < n);
     return hipSuccess;
+}
+
+// Zero `bytes` (a multiple of 4) at dst without hipMemsetAsync.
+hipError_t zero_fill(void* dst, uint64_t bytes, hipStream_t stream) {
+    if (bytes % 4u) return hipErrorInvalidValue;
+    return static_cast<hipError_t>(psk_fill_u32(static_cast<uint32_t*>(dst), 0u, bytes / 4u, stream));
 }
 
 }  // namespace psk

@@ -10,7 +10,8 @@ from __future__ import annotations
 
 import ctypes as C
 
-from . import (KV_BF16, KV_FP8, KV_PSQ4, KV_PSQ8, PLAN_ONLY, PoolInfo, SequenceInfo, StepPlan, StepRequest, check,
+from . import (CheckpointInfo, DFlashContext, GdnLayout, GdnPoolInfo, PrefixCacheStats,
+               KV_BF16, KV_FP8, KV_PSQ4, KV_PSQ8, PLAN_ONLY, PoolInfo, SequenceInfo, StepPlan, StepRequest, check,
                check_state, lib)
 from .ops import PoolGeometry, _stream
 
@@ -157,6 +158,113 @@ class Sequence:
         if self._h:
             h, self._h = self._h, C.c_void_p()
             check_state("psk_sequence_release", lib().psk_sequence_release(h, _stream(stream)))
+
+
+class GdnPool:
+    """GdnStatePool (gdn_state_pool.h:41-200): per-slot bf16 conv history and
+    f32 recurrent state."""
+
+    def __init__(self, max_sequences, gdn_layers, conv_dim, conv_history, num_v_heads, head_k,
+                 head_v):
+        self.layout = GdnLayout()
+        check_state("psk_gdn_layout_make", lib().psk_gdn_layout_make(
+            gdn_layers, conv_dim, conv_history, num_v_heads, head_k, head_v, C.byref(self.layout)))
+        self._h = C.c_void_p()
+        check_state("psk_gdn_pool_create", lib().psk_gdn_pool_create(
+            C.byref(self._h), max_sequences, C.byref(self.layout)))
+
+    def close(self):
+        if self._h:
+            lib().psk_gdn_pool_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self) -> GdnPoolInfo:
+        i = GdnPoolInfo()
+        check_state("psk_gdn_pool_info", lib().psk_gdn_pool_info(self._h, C.byref(i)))
+        return i
+
+    def initialize(self, slot, stream=None):
+        check_state("psk_gdn_pool_initialize", lib().psk_gdn_pool_initialize(
+            self._h, slot, _stream(stream)))
+
+    def reset(self, slot, stream=None):
+        check_state("psk_gdn_pool_reset", lib().psk_gdn_pool_reset(self._h, slot, _stream(stream)))
+
+    def release(self, slot):
+        check_state("psk_gdn_pool_release", lib().psk_gdn_pool_release(self._h, slot))
+
+    def copy_slot_from(self, dst_slot, src: "GdnPool", src_slot, stream=None):
+        check_state("psk_gdn_pool_copy_slot", lib().psk_gdn_pool_copy_slot(
+            self._h, dst_slot, src._h, src_slot, _stream(stream)))
+
+    def tensors(self, torch):
+        """(conv uint8 view, recurrent uint8 view) of the whole pool."""
+        i = self.info()
+        return (_wrap(torch, i.conv_base, i.conv_slot_bytes * i.max_sequences, torch.uint8),
+                _wrap(torch, i.recurrent_base, i.recurrent_slot_bytes * i.max_sequences,
+                      torch.uint8))
+
+
+class PrefixCache:
+    """PrefixCache (runtime/prefix_cache.h): LRU checkpoints of KV pages, the
+    GDN slot and an optional DFlash ring; one batched copy launch per save or
+    restore."""
+
+    def __init__(self, active_kv: KVPool, active_gdn: GdnPool, capacity_tokens, max_entries,
+                 min_prefix_tokens=64):
+        self._h = C.c_void_p()
+        check_state("psk_prefix_cache_create", lib().psk_prefix_cache_create(
+            C.byref(self._h), active_kv._h, active_gdn._h, capacity_tokens, max_entries,
+            min_prefix_tokens))
+
+    def close(self):
+        if self._h:
+            lib().psk_prefix_cache_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def enable_dflash_ring(self, ring_bytes):
+        check_state("psk_prefix_cache_enable_dflash_ring",
+                    lib().psk_prefix_cache_enable_dflash_ring(self._h, ring_bytes))
+
+    def find_longest(self, tokens, strictly_shorter=False) -> CheckpointInfo | None:
+        t = (C.c_int32 * max(len(tokens), 1))(*tokens)
+        out = CheckpointInfo()
+        check_state("psk_prefix_cache_find_longest", lib().psk_prefix_cache_find_longest(
+            self._h, t, len(tokens), int(strictly_shorter), C.byref(out)))
+        return out if out.id != 0 else None
+
+    def save(self, seq: "Sequence", gdn: GdnPool, kv: KVPool, tokens, stream=None,
+             prompt_boundary=False, dflash: DFlashContext | None = None):
+        t = (C.c_int32 * max(len(tokens), 1))(*tokens)
+        check_state("psk_prefix_cache_save", lib().psk_prefix_cache_save(
+            self._h, seq._h, gdn._h, kv._h, t, len(tokens), int(prompt_boundary),
+            C.byref(dflash) if dflash is not None else None, _stream(stream)))
+
+    def restore(self, seq: "Sequence", gdn: GdnPool, kv: KVPool, checkpoint_id: int, stream=None,
+                dflash: DFlashContext | None = None):
+        check_state("psk_prefix_cache_restore", lib().psk_prefix_cache_restore(
+            self._h, seq._h, gdn._h, kv._h, checkpoint_id,
+            C.byref(dflash) if dflash is not None else None, _stream(stream)))
+
+    def clear(self):
+        check_state("psk_prefix_cache_clear", lib().psk_prefix_cache_clear(self._h))
+
+    def stats(self) -> PrefixCacheStats:
+        s = PrefixCacheStats()
+        check_state("psk_prefix_cache_stats", lib().psk_prefix_cache_stats(self._h, C.byref(s)))
+        return s
 
 
 def plan_step(args, kv_dtype: int, requests, max_visible_tokens: int, partial_bytes: int,
