@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,psq")
+    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,psq,prefix")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times), the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -320,6 +320,62 @@ def run_psq(torch, ops, steps, warmup, dev):
     return res
 
 
+def run_prefix_cache(torch, steps, warmup, dev):
+    """Prefix-cache save and restore of a 4096-token prefix: FP8 KV, 6
+    attention layers x 4 kv heads x hd 256, page 16 (256 pages), plus the GDN
+    slot of the reference's qwen35-0.8B layout (18 states, conv 6144 x 3,
+    16 x 128 x 128 recurrent). Each is one batched copy launch per 32 pages."""
+    from phaseshift_amd import state
+    L, P, H, D, tokens = 6, 16, 4, 256, 4096
+    kv = state.KVPool(2 * tokens // P + 8, P, L, H, D, fp8=True)
+    slots = state.SlotPool(4, tokens // P)
+    gdn = state.GdnPool(4, 18, 6144, 3, 16, 128, 128)
+    cache = state.PrefixCache(kv, gdn, tokens, 2, 64)
+    seq = state.Sequence(slots, kv, tokens)
+    gdn.initialize(seq.slot)
+    seq.reserve(tokens)
+    seq.commit(tokens)
+    toks = np.arange(tokens, dtype=np.int32)
+    gi = gdn.info()
+    moved = (tokens // P) * L * 2 * (P * H * D + P * H * 4) + gi.conv_slot_bytes + gi.recurrent_slot_bytes
+    save_ms, restore_ms = [], []
+
+    def once(record):
+        cache.clear()
+        t = Timer(torch)
+        with t:
+            cache.save(seq, gdn, kv, toks)
+        r = state.Sequence(slots, kv, tokens)
+        gdn.initialize(r.slot)
+        cid = cache.find_longest(toks).id
+        t2 = Timer(torch)
+        with t2:
+            cache.restore(r, gdn, kv, cid)
+        if record:
+            save_ms.append(t.ms())
+            restore_ms.append(t2.ms())
+        gdn.release(r.slot)
+        r.release()
+
+    for _ in range(max(warmup, 3)):
+        once(False)
+    for _ in range(steps):
+        once(True)
+    st = cache.stats()
+    s_ms, r_ms = float(np.median(save_ms)), float(np.median(restore_ms))
+    res = dict(prefix_tokens=tokens, pages=tokens // P, layers=L, copied_bytes=moved,
+               save_ms=round(s_ms, 4), restore_ms=round(r_ms, 4),
+               save_GBps_read_plus_write=round(2 * moved / (s_ms * 1e-3) / 1e9, 1),
+               restore_GBps_read_plus_write=round(2 * moved / (r_ms * 1e-3) / 1e9, 1),
+               launches_per_save=int(st.copy_launches // max(1, 2 * (steps + max(warmup, 3)))),
+               reference_copies_per_save=(tokens // P) * L * 4 + 4)
+    gdn.release(seq.slot)
+    seq.release()
+    cache.close()
+    del st
+    return res
+
+
 def run_mixed_step(torch, ops, steps, warmup, dev):
     """BASELINE config 5, one continuous-batching step on the device: row
     metadata from the request descriptors, KV append (fused FP8 quantization) of
@@ -500,7 +556,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 5}))
         return
-    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5", "psq"}
+    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5", "psq",
+                                                     "prefix"}
     extra = {}
 
     # ---- main: north-star point, FP8 batch 64 @ 32k
@@ -547,6 +604,9 @@ def main():
 
     if "psq" in only:
         extra["psq_kv"] = run_psq(torch, ops, args.steps, args.warmup, dev)
+
+    if "prefix" in only:
+        extra["prefix_cache_fp8"] = run_prefix_cache(torch, args.steps, args.warmup, dev)
 
     if "cfg5" in only:
         extra["cfg5_mixed_step"] = run_mixed_step(torch, ops, max(5, args.steps // 2),

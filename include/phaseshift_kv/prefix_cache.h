@@ -198,12 +198,24 @@ private:
     void evict_lru();
     void release_checkpoint(PrefixCheckpoint& entry) noexcept;
     void destroy_rings() noexcept;
+    void destroy_staging() noexcept;
+    // The page pairs of one save / restore, copied to the device so that the
+    // whole copy is one launch: a pinned host staging buffer (reused once the
+    // previous upload from it has completed) and a device buffer (reused in
+    // stream order; one stream per cache).
+    Status launch_copy(const psk_page_copy_args& kv, const std::vector<psk_page_copy_pair>& pairs,
+                       const void* segs, uint32_t nseg, hipStream_t stream);
 
     std::optional<PagedKVPool> cache_kv_;
     std::optional<GdnStatePool> cache_gdn_;
     std::vector<void*> k_rings_, v_rings_;
     std::vector<uint32_t> free_ring_slots_;
     uint64_t ring_bytes_ = 0;
+    psk_page_copy_pair* pairs_host_ = nullptr;   // pinned
+    psk_page_copy_pair* pairs_dev_ = nullptr;
+    uint32_t pairs_cap_ = 0;
+    hipEvent_t pairs_ev_ = nullptr;
+    bool pairs_ev_pending_ = false;
     uint32_t capacity_tokens_ = 0;
     uint32_t max_entries_ = 0;
     uint32_t min_prefix_tokens_ = 64;

@@ -488,6 +488,45 @@ int psk_paged_attention_step(const psk_paged_attention_args* common, uint32_t kv
                              uint32_t num_requests, uint32_t max_visible_tokens, float* partials,
                              uint64_t partial_bytes, psk_step_plan_t* plan_out, void* stream);
 
+/* HIP-graph capture of planned steps (additive; the reference keys its batch
+ * graphs with a plan signature, paged_attention_dispatch.hip:896-908, and
+ * captures warm buckets, executor.hip:990-1075). The signature covers the
+ * plan's launches (kinds, regions, splits, tile and combine tables), the
+ * KV dtype, the argument bytes and the pool / scale / workspace pointers; the
+ * contents of those buffers may change between replays. A key's first step
+ * launches eagerly, the second captures and launches the graph, later ones
+ * replay it. *how: 0 eager, 1 captured, 2 replayed. Least recently used
+ * graphs beyond `capacity` keys are destroyed. Not thread-safe; one cache per
+ * stream. */
+typedef struct psk_step_graph_cache psk_step_graph_cache;
+typedef struct psk_step_graph_stats_t {
+    uint64_t eager;
+    uint64_t captures;
+    uint64_t replays;
+    uint64_t evictions;
+    uint32_t entries;
+    uint32_t graphs;
+} psk_step_graph_stats_t;
+int psk_step_graph_cache_create(psk_step_graph_cache** out, uint32_t capacity);
+void psk_step_graph_cache_destroy(psk_step_graph_cache* cache);
+int psk_step_graph_cache_stats(const psk_step_graph_cache* cache, psk_step_graph_stats_t* out);
+int psk_paged_attention_step_graphed(psk_step_graph_cache* cache,
+                                     const psk_paged_attention_args* common, uint32_t kv_dtype,
+                                     const void* k_pool, const void* v_pool,
+                                     const void* k_scale_pool, const void* v_scale_pool,
+                                     const psk_step_request* requests, uint32_t num_requests,
+                                     uint32_t max_visible_tokens, float* partials,
+                                     uint64_t partial_bytes, psk_step_plan_t* plan_out,
+                                     void* stream, uint32_t* how);
+/* 64-bit FNV-1a of the plan signature (0 if the step does not plan). */
+uint64_t psk_paged_attention_plan_signature(const psk_paged_attention_args* common,
+                                            uint32_t kv_dtype, const void* k_pool,
+                                            const void* v_pool, const void* k_scale_pool,
+                                            const void* v_scale_pool,
+                                            const psk_step_request* requests,
+                                            uint32_t num_requests, uint32_t max_visible_tokens,
+                                            float* partials, uint64_t partial_bytes);
+
 /* Split-K sizing the planner uses for a decode launch (additive, no reference
  * counterpart): the split count and pages per split that finish first under
  * the decode kernel's XCD-aware dispatch on this device. row_visible is an

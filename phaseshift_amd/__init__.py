@@ -122,6 +122,11 @@ class PrefixCacheStats(C.Structure):
                                   "max_entries", "capacity_tokens")]
 
 
+class StepGraphStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("eager", "captures", "replays", "evictions")] + [
+        ("entries", C.c_uint32), ("graphs", C.c_uint32)]
+
+
 PSK_ERR = {1001: "invalid_argument", 1002: "out_of_range", 1003: "invalid_state",
            1004: "insufficient_memory", 1005: "hip_error"}
 PLAN_ONLY = C.c_void_p(~0 & 0xFFFFFFFFFFFFFFFF)
@@ -207,6 +212,13 @@ SIGNATURES = {
     "psk_prefix_cache_clear": [_P],
     "psk_prefix_cache_stats": [_P, _P],
     "psk_paged_attention_step": [_P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _P, C.c_uint64, _P, _P],
+    "psk_step_graph_cache_create": [_P, _U32],
+    "psk_step_graph_cache_destroy": [_P],
+    "psk_step_graph_cache_stats": [_P, _P],
+    "psk_paged_attention_step_graphed": [_P, _P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _P,
+                                         C.c_uint64, _P, _P, _P],
+    "psk_paged_attention_plan_signature": [_P, _U32, _P, _P, _P, _P, _P, _U32, _U32, _P,
+                                           C.c_uint64],
     "psk_choose_decode_split": [_P, _U32, _P, _U32, C.c_uint64, _P, _P],
     "psk_selftest_e4m3_encode_range": [_U32, _U32, _P, _P],
     "psk_selftest_e4m3_decode_all": [_P, _P],
@@ -219,6 +231,8 @@ _RESTYPE = {
     "psk_pool_destroy": None,
     "psk_gdn_pool_destroy": None,
     "psk_prefix_cache_destroy": None,
+    "psk_step_graph_cache_destroy": None,
+    "psk_paged_attention_plan_signature": C.c_uint64,
     "psk_slot_pool_destroy": None,
     "psk_slot_pool_block_tables": C.c_void_p,
     "psk_sequence_block_table": C.c_uint32,

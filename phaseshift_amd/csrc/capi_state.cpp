@@ -180,16 +180,17 @@ extern "C" uint32_t psk_sequence_block_table(const psk_sequence* s, uint32_t* ou
     return n;
 }
 
-extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, uint32_t kv_dtype,
-                                        const void* k_pool, const void* v_pool,
-                                        const void* k_scale_pool, const void* v_scale_pool,
-                                        const psk_step_request* requests, uint32_t num_requests,
-                                        uint32_t max_visible_tokens, float* partials,
-                                        uint64_t partial_bytes, psk_step_plan_t* plan_out,
-                                        void* stream) {
+// The step and its plan from the C arguments (shared with the graphed step,
+// step_graph.cpp).
+int psk_build_step(const psk_paged_attention_args* common, uint32_t kv_dtype, const void* k_pool,
+                   const void* v_pool, const void* k_scale_pool, const void* v_scale_pool,
+                   const psk_step_request* requests, uint32_t num_requests,
+                   uint32_t max_visible_tokens, float* partials, uint64_t partial_bytes,
+                   ps::qwen35::runtime::PagedAttentionStep& step,
+                   std::vector<ps::qwen35::runtime::StepRequest>& reqs,
+                   ps::qwen35::runtime::PagedAttentionPlan& plan, psk_step_plan_t* plan_out) {
     using namespace ps::qwen35::runtime;
     if (common == nullptr || (num_requests > 0 && requests == nullptr)) return hipErrorInvalidValue;
-    PagedAttentionStep step;
     std::memcpy(&step.common, common, sizeof(step.common));
     if (kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_BF16 && kv_dtype != PSK_KV_PSQ4_W32 &&
         kv_dtype != PSK_KV_PSQ8_W32)
@@ -199,7 +200,7 @@ extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, 
     step.v_pool = v_pool;
     step.k_scale_pool = k_scale_pool;
     step.v_scale_pool = v_scale_pool;
-    std::vector<StepRequest> reqs(num_requests);
+    reqs.assign(num_requests, StepRequest{});
     for (uint32_t i = 0; i < num_requests; ++i)
         reqs[i] = {requests[i].row_begin, requests[i].row_count, requests[i].execution_class,
                    requests[i].max_visible};
@@ -208,7 +209,6 @@ extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, 
     step.max_visible_tokens = max_visible_tokens;
     step.partials = partials;
     step.partial_bytes = partial_bytes;
-    PagedAttentionPlan plan;
     const Status st = plan_paged_attention_step(step, plan);
     if (!st.ok()) {
         g_last_error = st.message;
@@ -224,6 +224,24 @@ extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, 
             plan_out->kernels[i].pages_per_split = plan.kernels[i].pages_per_split;
         }
     }
+    return hipSuccess;
+}
+
+extern "C" int psk_paged_attention_step(const psk_paged_attention_args* common, uint32_t kv_dtype,
+                                        const void* k_pool, const void* v_pool,
+                                        const void* k_scale_pool, const void* v_scale_pool,
+                                        const psk_step_request* requests, uint32_t num_requests,
+                                        uint32_t max_visible_tokens, float* partials,
+                                        uint64_t partial_bytes, psk_step_plan_t* plan_out,
+                                        void* stream) {
+    using namespace ps::qwen35::runtime;
+    PagedAttentionStep step;
+    std::vector<StepRequest> reqs;
+    PagedAttentionPlan plan;
+    const int rc = psk_build_step(common, kv_dtype, k_pool, v_pool, k_scale_pool, v_scale_pool,
+                                  requests, num_requests, max_visible_tokens, partials,
+                                  partial_bytes, step, reqs, plan, plan_out);
+    if (rc != hipSuccess) return rc;
     if (stream == reinterpret_cast<void*>(~uintptr_t(0))) return hipSuccess;   // plan only
     return launch_paged_attention_plan(step, plan, S(stream));
 }

@@ -21,9 +21,12 @@ constexpr uint32_t kMaxCopySegments = 8;
 hipError_t copy_pages_host_pairs(const psk_page_copy_args& args, const psk_page_copy_pair* pairs,
                                  uint32_t n, hipStream_t stream);
 // Page pairs (kv may be null when n == 0) and up to kMaxCopySegments segments;
-// one launch when n <= 32.
+// one launch when n <= 32 or when device_pairs (room for n pairs, owned by
+// the caller, reused only after this launch in stream order) is given, else
+// one launch per 32 pairs.
 hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair* pairs, uint32_t n,
-                          const CopySegment* segs, uint32_t nseg, hipStream_t stream);
+                          const CopySegment* segs, uint32_t nseg, hipStream_t stream,
+                          psk_page_copy_pair* device_pairs = nullptr);
 // Zero `bytes` (a multiple of 4) with a fill kernel (no hipMemsetAsync).
 hipError_t zero_fill(void* dst, uint64_t bytes, hipStream_t stream);
 

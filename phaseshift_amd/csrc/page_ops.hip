@@ -135,6 +135,7 @@ struct InlineSegments {
     uint64_t first_block[kMaxCopySegments + 1];
 };
 
+// Pairs inline (kernel arguments) or, when a.pairs is set, from device memory.
 __global__ __launch_bounds__(256) void copy_plan_kernel(const psk_page_copy_args a,
                                                         const InlinePairs pairs,
                                                         const InlineSegments segs, uint32_t nseg,
@@ -143,8 +144,8 @@ __global__ __launch_bounds__(256) void copy_plan_kernel(const psk_page_copy_args
         const uint32_t rest = blockIdx.x >> 2;
         const uint32_t pair = rest / a.num_layers;
         if (pair >= a.num_pairs) return;
-        copy_one(a, vec16, pairs.p[pair].dst_page, pairs.p[pair].src_page, rest % a.num_layers,
-                 blockIdx.x & 3u);
+        const psk_page_copy_pair pp = a.pairs != nullptr ? a.pairs[pair] : pairs.p[pair];
+        copy_one(a, vec16, pp.dst_page, pp.src_page, rest % a.num_layers, blockIdx.x & 3u);
         return;
     }
     const uint64_t b = blockIdx.x - page_blocks;
@@ -463,14 +464,15 @@ hipError_t copy_validate(const psk_page_copy_args* a, uint32_t& vec16) {
 // go to the kernel by value.
 hipError_t copy_pages_host_pairs(const psk_page_copy_args& args, const psk_page_copy_pair* pairs,
                                  uint32_t n, hipStream_t stream) {
-    return copy_plan_host(&args, pairs, n, nullptr, 0, stream);
+    return copy_plan_host(&args, pairs, n, nullptr, 0, stream, nullptr);
 }
 
 // Page pairs (kv == nullptr or n == 0: none) and segments in as few launches
 // as the inline pair limit allows: the first launch carries every segment and
 // the first kInlinePairs pairs.
 hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair* pairs, uint32_t n,
-                          const CopySegment* segs, uint32_t nseg, hipStream_t stream) {
+                          const CopySegment* segs, uint32_t nseg, hipStream_t stream,
+                          psk_page_copy_pair* device_pairs) {
     if (nseg > kMaxCopySegments) return hipErrorInvalidValue;
     uint32_t vec16 = 0;
     psk_page_copy_args base{};
@@ -492,6 +494,22 @@ hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair
         seg_blocks += (segs[i].bytes + kSegmentBlockBytes - 1) / kSegmentBlockBytes;
     }
     is.first_block[nseg] = seg_blocks;
+    if (device_pairs != nullptr && n > kInlinePairs) {
+        // one launch: the pair list goes to the caller's device buffer first
+        // (a pageable-source copy returns once the data is staged)
+        hipError_t e = hipMemcpyAsync(device_pairs, pairs, (size_t)n * sizeof(psk_page_copy_pair),
+                                      hipMemcpyHostToDevice, stream);
+        if (e != hipSuccess) return e;
+        psk_page_copy_args a = base;
+        a.num_pairs = n;
+        a.pairs = device_pairs;
+        const uint64_t page_blocks = (uint64_t)n * a.num_layers * 4u;
+        const uint64_t blocks = page_blocks + seg_blocks;
+        if (page_blocks > 0x7FFFFFFFull || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(copy_plan_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a,
+                           InlinePairs{}, is, nseg, vec16, (uint32_t)page_blocks);
+        return hipGetLastError();
+    }
     uint32_t b = 0;
     do {
         psk_page_copy_args a = base;

@@ -124,7 +124,49 @@ Status GdnStatePool::copy_slot_from(SequenceSlotId dst_slot, const GdnStatePool&
 }
 
 // ------------------------------------------------------------- PrefixCache
-PrefixCache::~PrefixCache() { destroy_rings(); }
+PrefixCache::~PrefixCache() {
+    destroy_rings();
+    destroy_staging();
+}
+
+void PrefixCache::destroy_staging() noexcept {
+    if (pairs_ev_) {
+        (void)hipEventSynchronize(pairs_ev_);
+        (void)hipEventDestroy(pairs_ev_);
+    }
+    if (pairs_host_) (void)hipHostFree(pairs_host_);
+    if (pairs_dev_) (void)hipFree(pairs_dev_);
+    pairs_ev_ = nullptr;
+    pairs_host_ = nullptr;
+    pairs_dev_ = nullptr;
+    pairs_cap_ = 0;
+    pairs_ev_pending_ = false;
+}
+
+Status PrefixCache::launch_copy(const psk_page_copy_args& kv,
+                                const std::vector<psk_page_copy_pair>& pairs, const void* segs,
+                                uint32_t nseg, hipStream_t stream) {
+    const auto* sg = static_cast<const psk::CopySegment*>(segs);
+    const uint32_t n = static_cast<uint32_t>(pairs.size());
+    psk::CopySegment none{};
+    if (n <= 32u || pairs_cap_ < n) {
+        const hipError_t e = psk::copy_plan_host(&kv, pairs.data(), n, nseg ? sg : &none, nseg, stream);
+        if (e != hipSuccess) return Status::hip_error("prefix cache copy", e);
+        stats_.copy_launches += std::max<uint64_t>(1, (n + 31) / 32);
+        return Status::make_ok();
+    }
+    if (pairs_ev_pending_) {
+        const hipError_t w = hipEventSynchronize(pairs_ev_);
+        if (w != hipSuccess) return Status::hip_error("prefix cache staging wait", w);
+    }
+    std::copy(pairs.begin(), pairs.end(), pairs_host_);
+    hipError_t e = psk::copy_plan_host(&kv, pairs_host_, n, sg, nseg, stream, pairs_dev_);
+    if (e == hipSuccess) e = hipEventRecord(pairs_ev_, stream);
+    if (e != hipSuccess) return Status::hip_error("prefix cache copy", e);
+    pairs_ev_pending_ = true;
+    ++stats_.copy_launches;
+    return Status::make_ok();
+}
 
 void PrefixCache::destroy_rings() noexcept {
     for (void* p : k_rings_) (void)hipFree(p);
@@ -153,6 +195,19 @@ Status PrefixCache::create(PrefixCache& out, const PagedKVPool& active_kv,
     if (!st.ok()) return st;
     out.clear();
     out.destroy_rings();
+    out.destroy_staging();
+    // staging for one launch per save / restore (up to every cache page)
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&out.pairs_host_),
+                                 (size_t)cache_pages * sizeof(psk_page_copy_pair), 0);
+    if (e == hipSuccess)
+        e = hipMalloc(reinterpret_cast<void**>(&out.pairs_dev_),
+                      (size_t)cache_pages * sizeof(psk_page_copy_pair));
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&out.pairs_ev_, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        out.destroy_staging();
+        return Status::hip_error("prefix cache staging", e);
+    }
+    out.pairs_cap_ = cache_pages;
     out.cache_kv_.emplace(std::move(kv));
     out.cache_gdn_.emplace(std::move(gdn));
     out.capacity_tokens_ = capacity_tokens;
@@ -342,13 +397,11 @@ Status PrefixCache::save(const PagedSequenceState& sequence, const GdnStatePool&
         segs[nseg++] = {k_rings_[ring], dflash_context->k_ring, ring_bytes_};
         segs[nseg++] = {v_rings_[ring], dflash_context->v_ring, ring_bytes_};
     }
-    const hipError_t e = psk::copy_plan_host(&kv, pairs.data(), (uint32_t)pairs.size(), segs, nseg,
-                                             stream);
-    if (e != hipSuccess) {
+    st = launch_copy(kv, pairs, segs, nseg, stream);
+    if (!st.ok()) {
         release_checkpoint(cp);
-        return Status::hip_error("prefix save copy", e);
+        return st;
     }
-    stats_.copy_launches += std::max<uint64_t>(1, (pairs.size() + 31) / 32);
     // the reference's accounting (prefix_cache.cpp:340-344): K+V pages of every
     // layer with their scale rows, plus twice the GDN slot
     const uint64_t per_page = (kv_pool.page_body_bytes() + kv_pool.page_scale_bytes()) * 2u *
@@ -408,10 +461,8 @@ Status PrefixCache::restore(PagedSequenceState& sequence, GdnStatePool& gdn_pool
         segs[nseg++] = {dflash_context->k_ring, k_rings_[checkpoint.dflash_slot], ring_bytes_};
         segs[nseg++] = {dflash_context->v_ring, v_rings_[checkpoint.dflash_slot], ring_bytes_};
     }
-    const hipError_t e = psk::copy_plan_host(&kv, pairs.data(), (uint32_t)pairs.size(), segs, nseg,
-                                             stream);
-    if (e != hipSuccess) return Status::hip_error("prefix restore copy", e);
-    stats_.copy_launches += std::max<uint64_t>(1, (pairs.size() + 31) / 32);
+    st = launch_copy(kv, pairs, segs, nseg, stream);
+    if (!st.ok()) return st;
     if (dflash_context != nullptr) {
         dflash_context->length = checkpoint.dflash_length;
         dflash_context->next_position = checkpoint.dflash_next_position;

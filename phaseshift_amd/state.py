@@ -11,6 +11,7 @@ from __future__ import annotations
 import ctypes as C
 
 from . import (CheckpointInfo, DFlashContext, GdnLayout, GdnPoolInfo, PrefixCacheStats,
+               StepGraphStats,
                KV_BF16, KV_FP8, KV_PSQ4, KV_PSQ8, PLAN_ONLY, PoolInfo, SequenceInfo, StepPlan, StepRequest, check,
                check_state, lib)
 from .ops import PoolGeometry, _stream
@@ -238,18 +239,28 @@ class PrefixCache:
         check_state("psk_prefix_cache_enable_dflash_ring",
                     lib().psk_prefix_cache_enable_dflash_ring(self._h, ring_bytes))
 
+    @staticmethod
+    def _tokens(tokens):
+        """(pointer, count) of int32 tokens: a C-contiguous int32 numpy array
+        is passed as is, anything else converted."""
+        import numpy as np
+        if not (isinstance(tokens, np.ndarray) and tokens.dtype == np.int32
+                and tokens.flags.c_contiguous):
+            tokens = np.ascontiguousarray(np.asarray(tokens, dtype=np.int64).astype(np.int32))
+        return tokens, tokens.ctypes.data if tokens.size else None, int(tokens.size)
+
     def find_longest(self, tokens, strictly_shorter=False) -> CheckpointInfo | None:
-        t = (C.c_int32 * max(len(tokens), 1))(*tokens)
+        keep, t, n = self._tokens(tokens)
         out = CheckpointInfo()
         check_state("psk_prefix_cache_find_longest", lib().psk_prefix_cache_find_longest(
-            self._h, t, len(tokens), int(strictly_shorter), C.byref(out)))
+            self._h, t, n, int(strictly_shorter), C.byref(out)))
         return out if out.id != 0 else None
 
     def save(self, seq: "Sequence", gdn: GdnPool, kv: KVPool, tokens, stream=None,
              prompt_boundary=False, dflash: DFlashContext | None = None):
-        t = (C.c_int32 * max(len(tokens), 1))(*tokens)
+        keep, t, n = self._tokens(tokens)
         check_state("psk_prefix_cache_save", lib().psk_prefix_cache_save(
-            self._h, seq._h, gdn._h, kv._h, t, len(tokens), int(prompt_boundary),
+            self._h, seq._h, gdn._h, kv._h, t, n, int(prompt_boundary),
             C.byref(dflash) if dflash is not None else None, _stream(stream)))
 
     def restore(self, seq: "Sequence", gdn: GdnPool, kv: KVPool, checkpoint_id: int, stream=None,
@@ -288,3 +299,60 @@ def plan_step(args, kv_dtype: int, requests, max_visible_tokens: int, partial_by
         _stream(stream) if launch else PLAN_ONLY)
     check("psk_paged_attention_step", rc)
     return plan
+
+
+class StepGraphCache:
+    """HIP graphs of planned PAGED_ATTENTION steps keyed by the plan signature
+    (psk_paged_attention_step_graphed): first sighting eager, second captured,
+    then replayed."""
+
+    def __init__(self, capacity=8):
+        self._h = C.c_void_p()
+        check("psk_step_graph_cache_create", lib().psk_step_graph_cache_create(
+            C.byref(self._h), capacity))
+
+    def close(self):
+        if self._h:
+            lib().psk_step_graph_cache_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def step(self, args, kv_dtype, requests, max_visible_tokens, partial_bytes, partials,
+             k_pool, v_pool, k_scale=None, v_scale=None, stream=None):
+        """Returns (plan, how) with how 0 eager, 1 captured, 2 replayed."""
+        n = len(requests)
+        reqs = (StepRequest * max(n, 1))()
+        for i, r in enumerate(requests):
+            reqs[i].row_begin, reqs[i].row_count, reqs[i].execution_class = r[0], r[1], r[2]
+            reqs[i].max_visible = r[3] if len(r) > 3 else 0
+        plan = StepPlan()
+        how = C.c_uint32(99)
+        p = lambda t: None if t is None else (t if isinstance(t, int) else t.data_ptr())
+        check("psk_paged_attention_step_graphed", lib().psk_paged_attention_step_graphed(
+            self._h, C.byref(args), kv_dtype, p(k_pool), p(v_pool), p(k_scale), p(v_scale), reqs,
+            n, max_visible_tokens, p(partials), partial_bytes, C.byref(plan), _stream(stream),
+            C.byref(how)))
+        return plan, how.value
+
+    def stats(self) -> StepGraphStats:
+        st = StepGraphStats()
+        check("psk_step_graph_cache_stats", lib().psk_step_graph_cache_stats(self._h, C.byref(st)))
+        return st
+
+
+def plan_signature(args, kv_dtype, requests, max_visible_tokens, partial_bytes, partials,
+                   k_pool, v_pool, k_scale=None, v_scale=None) -> int:
+    n = len(requests)
+    reqs = (StepRequest * max(n, 1))()
+    for i, r in enumerate(requests):
+        reqs[i].row_begin, reqs[i].row_count, reqs[i].execution_class = r[0], r[1], r[2]
+        reqs[i].max_visible = r[3] if len(r) > 3 else 0
+    p = lambda t: None if t is None else (t if isinstance(t, int) else t.data_ptr())
+    return int(lib().psk_paged_attention_plan_signature(
+        C.byref(args), kv_dtype, p(k_pool), p(v_pool), p(k_scale), p(v_scale), reqs, n,
+        max_visible_tokens, p(partials), partial_bytes))
