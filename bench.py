@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,psq,prefix")
+    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,psq,prefix,graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times), the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -376,6 +376,91 @@ def run_prefix_cache(torch, steps, warmup, dev):
     return res
 
 
+def run_step_graph(torch, ops, steps, warmup, dev):
+    """Planned PAGED_ATTENTION steps with FP8 KV launched eagerly
+    (psk_paged_attention_step: plan + launches) and as a captured HIP graph
+    (psk_paged_attention_step_graphed: plan + signature + one graph launch).
+    "mixed": 8 decode rows at 2.2k-3.6k tokens (split-K + combine), two 16-row
+    verify blocks, a 128-row prefill chunk. "verify32": 32 verify blocks of 16
+    rows at 1k context, whose split tiles need one combine launch per block
+    (34 launches a step). GPU time per step (events around back-to-back steps)
+    and host time to enqueue a step."""
+    import time
+    from phaseshift_amd import KV_FP8, state
+    QH, H, D, P = 24, 4, 256, 16
+
+    def workload(kind, seed):
+        rng = np.random.default_rng(seed)
+        if kind == "mixed":
+            ctx = [int(x) for x in rng.integers(2200, 3600, 8)]
+            lens = ctx + [1016, 1016, 328]
+            slot_l = list(range(8)) + [8] * 16 + [9] * 16 + [10] * 128
+            pos_l = [c - 1 for c in ctx] + list(range(1000, 1016)) * 2 + list(range(200, 328))
+            reqs = [(i, 1, 0, ctx[i]) for i in range(8)] + [(8, 16, 1, 1016), (24, 16, 1, 1016),
+                                                            (40, 128, 2, 328)]
+            maxvis = 3600
+        else:
+            lens = [1016] * 32
+            slot_l = [b for b in range(32) for _ in range(16)]
+            pos_l = list(range(1000, 1016)) * 32
+            reqs = [(16 * b, 16, 1, 1016) for b in range(32)]
+            maxvis = 2048
+        need = [(n + P - 1) // P for n in lens]
+        pages = sum(need) + 2
+        perm = rng.permutation(pages).astype(np.int32)
+        bt = np.full((len(lens), max(need)), -1, np.int32)
+        k = 0
+        for r, n in enumerate(need):
+            bt[r, :n] = perm[k:k + n]
+            k += n
+        g = ops.PoolGeometry(1, pages, P, H, D)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        pools = (torch.randint(0, 126, (g.pool_elems,), generator=gen, device=dev).to(torch.uint8),
+                 torch.randint(0, 126, (g.pool_elems,), generator=gen, device=dev).to(torch.uint8),
+                 torch.rand(g.scale_elems, generator=gen, device=dev) * 0.02 + 1e-3,
+                 torch.rand(g.scale_elems, generator=gen, device=dev) * 0.02 + 1e-3)
+        slots = torch.tensor(slot_l, dtype=torch.int32, device=dev)
+        pos = torch.tensor(pos_l, dtype=torch.int32, device=dev)
+        rows = slots.numel()
+        q = torch.randn((rows, QH * D), generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty((rows, QH * D), dtype=torch.float32, device=dev)
+        a = ops.attention_args(g, 0, q, out, slots, pos, torch.from_numpy(bt).to(dev), QH)
+        return a, pools, reqs, maxvis, (q, out, slots, pos)
+
+    res = {}
+    nbytes = 64 << 20
+    part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    for kind in ("mixed", "verify32"):
+        a, pools, reqs, maxvis, keep = workload(kind, 5)
+        cache = state.StepGraphCache(4)
+
+        def eager():
+            state.plan_step(a, KV_FP8, reqs, maxvis, nbytes, part, *pools, launch=True)
+
+        def graphed():
+            cache.step(a, KV_FP8, reqs, maxvis, nbytes, part, *pools)
+
+        r = {}
+        for name, fn in (("eager", eager), ("graph", graphed)):
+            warm(torch, fn, max(warmup, 3))
+            t = Timer(torch)
+            h0 = time.perf_counter()
+            with t:
+                for _ in range(steps):
+                    fn()
+            host_ms = (time.perf_counter() - h0) * 1e3 / steps
+            r[name + "_gpu_ms_per_step"] = round(t.ms() / steps, 4)
+            r[name + "_host_ms_per_step"] = round(host_ms, 4)
+        plan, how = cache.step(a, KV_FP8, reqs, maxvis, nbytes, part, *pools)
+        torch.cuda.synchronize()
+        r.update(planned_kernels=int(plan.count), replayed=bool(how == 2),
+                 gpu_speedup=round(r["eager_gpu_ms_per_step"] / r["graph_gpu_ms_per_step"], 3))
+        res[kind] = r
+        cache.close()
+    return res
+
+
 def run_mixed_step(torch, ops, steps, warmup, dev):
     """BASELINE config 5, one continuous-batching step on the device: row
     metadata from the request descriptors, KV append (fused FP8 quantization) of
@@ -557,7 +642,7 @@ def main():
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 5}))
         return
     only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5", "psq",
-                                                     "prefix"}
+                                                     "prefix", "graph"}
     extra = {}
 
     # ---- main: north-star point, FP8 batch 64 @ 32k
@@ -607,6 +692,9 @@ def main():
 
     if "prefix" in only:
         extra["prefix_cache_fp8"] = run_prefix_cache(torch, args.steps, args.warmup, dev)
+
+    if "graph" in only:
+        extra["step_graph_fp8"] = run_step_graph(torch, ops, args.steps, args.warmup, dev)
 
     if "cfg5" in only:
         extra["cfg5_mixed_step"] = run_mixed_step(torch, ops, max(5, args.steps // 2),
