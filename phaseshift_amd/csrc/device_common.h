@@ -88,6 +88,29 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float r, bool fa
     return x / s;
 }
 
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+// 8 FP8 codes in two dwords -> 8 f16 (exact: every E4M3 value is an f16 value).
+__device__ __forceinline__ f16x8 fp8x8_to_f16x8(uint32_t w0, uint32_t w1) {
+    u32x4 r;
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true));
+    return __builtin_bit_cast(f16x8, r);
+}
+
+// Two floats -> f16 pair (round to nearest even).
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+}
+
+// Online softmax with a lazily moved reference: the running reference max
+// (log2 units) moves only when a new score exceeds it by more than this, so
+// the accumulator rescale is rare; exponentials stay below 2^kLazyMaxSlack.
+constexpr float kLazyMaxSlack = 8.0f;
+
 template <int W>
 __device__ __forceinline__ float group_max(float x) {
 #pragma unroll

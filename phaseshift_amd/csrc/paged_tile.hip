@@ -308,9 +308,12 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
             }
             mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = __builtin_fmaxf(m_run, mx);
+            // m_run is the row's softmax reference: it moves only when a score
+            // exceeds it by more than kLazyMaxSlack (then P <= 2^slack)
+            const bool moved = mx > m_run + kLazyMaxSlack;
+            const float m_new = moved ? mx : m_run;
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+            const float alpha = moved ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
             float pv[H][4], psum = 0.0f;
 #pragma unroll
             for (int hf = 0; hf < H; ++hf)
@@ -322,11 +325,31 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
                 }
             l_run = l_run * alpha + psum;
             m_run = m_new;
-            if (__any(alpha != 1.0f)) {
+            if (__any(moved)) {
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) o[db] *= alpha;
             }
-            // P as hi + lo bf16 pairs (two MFMAs, ~16 mantissa bits per weight)
+            const uint8_t* vb = st + KV_BYTES + tr_off;
+            if constexpr (KVB == 1) {
+                // FP8: P (v_scale folded in) as one f16 operand (11 mantissa
+                // bits) and V as f16 (E4M3 values are exact in f16): one
+                // MFMA per output block
+                u32x4 pf;
+                pf[0] = pack_f16x2(pv[0][0], pv[0][1]);
+                pf[1] = pack_f16x2(pv[0][2], pv[0][3]);
+                pf[2] = pack_f16x2(pv[1][0], pv[1][1]);
+                pf[3] = pack_f16x2(pv[1][2], pv[1][3]);
+                const f16x8 pfh = __builtin_bit_cast(f16x8, pf);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    if (db % 2 == 0) __builtin_amdgcn_sched_barrier(0);
+                    const i32x2 x = tr8(vb + 256 * db);
+                    const f16x8 vf = fp8x8_to_f16x8((uint32_t)x[0], (uint32_t)x[1]);
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pfh, o[db], 0, 0, 0);
+                }
+                return;
+            }
+            // BF16: P as hi + lo bf16 pairs (two MFMAs, ~16 mantissa bits per weight)
             u32x4 ph, pl;
             { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
             { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
@@ -335,7 +358,6 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
             const bf16x8 pfh = __builtin_bit_cast(bf16x8, ph);
             const bf16x8 pfl = __builtin_bit_cast(bf16x8, pl);
             // O^T += V^T P^T
-            const uint8_t* vb = st + KV_BYTES + tr_off;
             // Blocks of 4 output-dim groups: the scheduling barriers keep the
             // compiler from hoisting every V read of the chunk at once, which
             // would need more registers than 3 waves per SIMD leave.
