@@ -8,13 +8,14 @@
 //                                                        paged_prefill.hip:586-825
 //   launcher validation                                  paged_prefill.hip:437-459
 //
-// MI355X design. Workgroup = (16-row tile, kv_head, split); one wave per query
-// head of the GQA group. The 16 rows of the tile are the N=16 side of
-// v_mfma_f32_16x16x32_bf16, so each lane owns one row's causal limit and
-// softmax state; K/V chunks (32 tokens) are staged once in LDS and read by all
-// q_per_kv waves. Waves own disjoint (row, head) outputs, so there is no
-// cross-wave merge; split-K writes the decode kernel's partial layout and the
-// same combine kernel finishes it.
+// MI355X design. Workgroup = (16-row tile, kv_head, split); each wave owns HPW
+// query heads of the GQA group. The 16 rows of the tile are the N=16 side of
+// v_mfma_f32_16x16x32, so each lane owns one row's causal limit and softmax
+// state; K/V chunks (32 tokens) are staged once in LDS and read by all waves,
+// and every K (V) fragment a wave converts feeds the MFMAs of all its heads.
+// Waves own disjoint (row, head) outputs, so there is no cross-wave merge;
+// split-K writes the decode kernel's partial layout and the same combine
+// kernel finishes it.
 #include "device_common.h"
 
 #include <phaseshift_kv/paged_attention.h>
@@ -25,7 +26,7 @@ namespace {
 using ps::kernel::kPagedAttentionHeadLimit;
 
 constexpr int kTileRows = 16;
-constexpr int kMaxTileWaves = 8;   // q_per_kv <= 8 (one head per wave)
+constexpr int kMaxTileHeads = 8;   // q_per_kv <= 8
 constexpr uint32_t kMaxTileSplits = 1024;
 
 // Explicit tiles (row start, row count <= 16) passed by value in the kernel
@@ -80,8 +81,12 @@ constexpr int kTileStages = 4;
 
 // kAl16: page_tokens % 16 == 0, so every page-aligned 16-token half lies in one
 // page and its page id, base address and in-page offset are wave-uniform.
-template <int KVB, int D, int NW, bool kAl16>
-__global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams p) {
+// Waves per SIMD the register budget targets: 3 with one head per wave, 2
+// with two (the accumulators of 2 heads take 128 registers at D=256).
+constexpr int tile_waves_per_simd(int hpw) { return hpw == 1 ? 3 : 2; }
+
+template <int KVB, int D, int NW, int HPW, bool kAl16>
+__global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_kernel(const TileParams p) {
     constexpr int H = 2;                 // 16-token halves per chunk
     constexpr int CT = 16 * H;           // tokens per chunk
     constexpr int NL = D * KVB / 64;     // 16 B DMA pieces per lane per half
@@ -157,27 +162,38 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
     // Everything above is uniform over the workgroup, so all waves reach the
     // barriers below; a wave past the last query head of the group only
     // issues its share of the DMAs.
-    const bool computes = w < qpk;
+    const bool computes = w * HPW < qpk;
 
     if (tid == 0) bad_lds = 0u;
 
     // this wave's query head; Q fragments of the 16 rows (column n = row n)
-    const uint32_t head = kv_head * qpk + (computes ? w : 0u);
-    bf16x8 qf[NS];
-    {
+    // this wave's query heads (group index w*HPW + i); heads past the group
+    // compute on zero Q and are never written
+    bool hv[HPW];
+    bf16x8 qf[HPW][NS];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+        const uint32_t gh = w * HPW + (uint32_t)i;
+        hv[i] = gh < qpk;
+        const uint32_t head = kv_head * qpk + (hv[i] ? gh : 0u);
         const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
                                (uint64_t)(row_ok ? row : r0) * a.q_row_stride + (uint64_t)head * D;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const int d0 = KVB == 2 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
-            qf[s] = q8(qrow + d0, row_ok && computes);
+            qf[i][s] = q8(qrow + d0, row_ok && hv[i]);
         }
     }
 
-    float m_run = -INFINITY, l_run = 0.0f;
-    f32x4 o[NDB];
+    float m_run[HPW], l_run[HPW];
+    f32x4 o[HPW][NDB];
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < HPW; ++i) {
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[i][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
 
     // tr-read offsets of this lane inside the V part of a stage. Lane r of a
     // 16-lane block names row r of the transpose; in the DMA layout byte b of
@@ -265,10 +281,12 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
 
         // Scores, causal online softmax and PV of the chunk at c in stage st.
         auto consume = [&](uint32_t c, const uint8_t* st) __attribute__((always_inline)) {
-            f32x4 sc[H];
+            f32x4 sc[HPW][H];
 #pragma unroll
             for (int hf = 0; hf < H; ++hf) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                f32x4 acc[HPW];
+#pragma unroll
+                for (int i = 0; i < HPW; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
                 const uint8_t* kb = st + hf * HALF_STRIDE + 16 * lane;
 #pragma unroll
                 for (int s = 0; s < NS; ++s) {
@@ -281,93 +299,98 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
                         const u32x4 wv = *reinterpret_cast<const u32x4*>(kb + 1024 * (s >> 1));
                         kf = (s & 1) ? fp8x8_to_bf16x8(wv[2], wv[3]) : fp8x8_to_bf16x8(wv[0], wv[1]);
                     }
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i)
+                        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[i][s], acc[i], 0, 0, 0);
                 }
-                sc[hf] = acc;
+#pragma unroll
+                for (int i = 0; i < HPW; ++i) sc[i][hf] = acc[i];
             }
             __builtin_amdgcn_sched_barrier(0);
             // lane (n, g): row n, tokens c + 16*hf + 4*g + r; causal per row
-            float s2[H][4], vsc[H][4];
-            float mx = -INFINITY;
+            f32x4 kscale[H], vscale[H];
+            bool tok_ok[H][4];
 #pragma unroll
             for (int hf = 0; hf < H; ++hf) {
-                f32x4 kscale = {1.f, 1.f, 1.f, 1.f}, vscale = {1.f, 1.f, 1.f, 1.f};
+                kscale[hf] = (f32x4){1.f, 1.f, 1.f, 1.f};
+                vscale[hf] = (f32x4){1.f, 1.f, 1.f, 1.f};
                 if constexpr (KVB == 1) {
-                    kscale = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + hf * 256 + 16 * g);
-                    vscale = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + SC_BYTES + hf * 256 +
-                                                             16 * g);
+                    kscale[hf] = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + hf * 256 + 16 * g);
+                    vscale[hf] = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + SC_BYTES +
+                                                                 hf * 256 + 16 * g);
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t tau = c + hf * 16 + 4 * g + r;
-                    s2[hf][r] = (tau < vis && tau < te) ? sc[hf][r] * (p.scale_log2 * kscale[r])
-                                                        : -INFINITY;
-                    vsc[hf][r] = vscale[r];
-                    mx = __builtin_fmaxf(mx, s2[hf][r]);
+                    tok_ok[hf][r] = tau < vis && tau < te;
                 }
             }
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-            // m_run is the row's softmax reference: it moves only when a score
-            // exceeds it by more than kLazyMaxSlack (then P <= 2^slack)
-            const bool moved = mx > m_run + kLazyMaxSlack;
-            const float m_new = moved ? mx : m_run;
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = moved ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
-            float pv[H][4], psum = 0.0f;
+            u32x4 pf[HPW], pl[HPW];
 #pragma unroll
-            for (int hf = 0; hf < H; ++hf)
+            for (int i = 0; i < HPW; ++i) {
+                float s2[H][4];
+                float mx = -INFINITY;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
-                    psum += e;
-                    pv[hf][r] = e * vsc[hf][r];
+                for (int hf = 0; hf < H; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        s2[hf][r] = tok_ok[hf][r] ? sc[i][hf][r] * (p.scale_log2 * kscale[hf][r]) : -INFINITY;
+                        mx = __builtin_fmaxf(mx, s2[hf][r]);
+                    }
+                mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+                // m_run is the row's softmax reference: it moves only when a
+                // score exceeds it by more than kLazyMaxSlack (then P <= 2^slack)
+                const bool moved = mx > m_run[i] + kLazyMaxSlack;
+                const float m_new = moved ? mx : m_run[i];
+                const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+                const float alpha = moved ? __builtin_amdgcn_exp2f(m_run[i] - m_use) : 1.0f;
+                float pv[H][4], psum = 0.0f;
+#pragma unroll
+                for (int hf = 0; hf < H; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
+                        psum += e;
+                        pv[hf][r] = e * vscale[hf][r];
+                    }
+                l_run[i] = l_run[i] * alpha + psum;
+                m_run[i] = m_new;
+                if (__any(moved)) {
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) o[i][db] *= alpha;
                 }
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
-            if (__any(moved)) {
+                if constexpr (KVB == 1) {
+                    // FP8: P (v_scale folded in) as one f16 operand (11 mantissa
+                    // bits); V as f16 (E4M3 values are exact in f16)
+                    pf[i][0] = pack_f16x2(pv[0][0], pv[0][1]);
+                    pf[i][1] = pack_f16x2(pv[0][2], pv[0][3]);
+                    pf[i][2] = pack_f16x2(pv[1][0], pv[1][1]);
+                    pf[i][3] = pack_f16x2(pv[1][2], pv[1][3]);
+                } else {
+                    // BF16: P as hi + lo bf16 pairs (two MFMAs, ~16 mantissa bits)
 #pragma unroll
-                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+                    for (int j = 0; j < 4; ++j) {
+                        const u32x2 t_ = split_bf16x2(pv[j >> 1][2 * (j & 1)], pv[j >> 1][2 * (j & 1) + 1]);
+                        pf[i][j] = t_[0];
+                        pl[i][j] = t_[1];
+                    }
+                }
             }
+            // O^T += V^T P^T, one V fragment per output block for all heads.
+            // The scheduling barriers keep the compiler from hoisting every V
+            // read of the chunk at once.
             const uint8_t* vb = st + KV_BYTES + tr_off;
-            if constexpr (KVB == 1) {
-                // FP8: P (v_scale folded in) as one f16 operand (11 mantissa
-                // bits) and V as f16 (E4M3 values are exact in f16): one
-                // MFMA per output block
-                u32x4 pf;
-                pf[0] = pack_f16x2(pv[0][0], pv[0][1]);
-                pf[1] = pack_f16x2(pv[0][2], pv[0][3]);
-                pf[2] = pack_f16x2(pv[1][0], pv[1][1]);
-                pf[3] = pack_f16x2(pv[1][2], pv[1][3]);
-                const f16x8 pfh = __builtin_bit_cast(f16x8, pf);
-#pragma unroll
-                for (int db = 0; db < NDB; ++db) {
-                    if (db % 2 == 0) __builtin_amdgcn_sched_barrier(0);
-                    const i32x2 x = tr8(vb + 256 * db);
-                    const f16x8 vf = fp8x8_to_f16x8((uint32_t)x[0], (uint32_t)x[1]);
-                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pfh, o[db], 0, 0, 0);
-                }
-                return;
-            }
-            // BF16: P as hi + lo bf16 pairs (two MFMAs, ~16 mantissa bits per weight)
-            u32x4 ph, pl;
-            { const u32x2 t_ = split_bf16x2(pv[0][0], pv[0][1]); ph[0] = t_[0]; pl[0] = t_[1]; }
-            { const u32x2 t_ = split_bf16x2(pv[0][2], pv[0][3]); ph[1] = t_[0]; pl[1] = t_[1]; }
-            { const u32x2 t_ = split_bf16x2(pv[1][0], pv[1][1]); ph[2] = t_[0]; pl[2] = t_[1]; }
-            { const u32x2 t_ = split_bf16x2(pv[1][2], pv[1][3]); ph[3] = t_[0]; pl[3] = t_[1]; }
-            const bf16x8 pfh = __builtin_bit_cast(bf16x8, ph);
-            const bf16x8 pfl = __builtin_bit_cast(bf16x8, pl);
-            // O^T += V^T P^T
-            // Blocks of 4 output-dim groups: the scheduling barriers keep the
-            // compiler from hoisting every V read of the chunk at once, which
-            // would need more registers than 3 waves per SIMD leave.
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
                 if (db % 2 == 0) __builtin_amdgcn_sched_barrier(0);
-                bf16x8 vf;
                 if constexpr (KVB == 1) {
                     const i32x2 x = tr8(vb + 256 * db);
-                    vf = fp8x8_to_bf16x8((uint32_t)x[0], (uint32_t)x[1]);
+                    const f16x8 vf = fp8x8_to_f16x8((uint32_t)x[0], (uint32_t)x[1]);
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i)
+                        o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            vf, __builtin_bit_cast(f16x8, pf[i]), o[i][db], 0, 0, 0);
                 } else {
                     const i16x4 x0 = tr16(vb + 512 * db);
                     const i16x4 x1 = tr16(vb + HALF_STRIDE + 512 * db);
@@ -376,10 +399,15 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
                     u[1] = __builtin_bit_cast(u32x2, x0)[1];
                     u[2] = __builtin_bit_cast(u32x2, x1)[0];
                     u[3] = __builtin_bit_cast(u32x2, x1)[1];
-                    vf = __builtin_bit_cast(bf16x8, u);
+                    const bf16x8 vf = __builtin_bit_cast(bf16x8, u);
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i) {
+                        o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            vf, __builtin_bit_cast(bf16x8, pf[i]), o[i][db], 0, 0, 0);
+                        o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            vf, __builtin_bit_cast(bf16x8, pl[i]), o[i][db], 0, 0, 0);
+                    }
                 }
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfh, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfl, o[db], 0, 0, 0);
             }
         };
 
@@ -413,49 +441,61 @@ __global__ __launch_bounds__(NW * 64, 3) void paged_tile_kernel(const TileParams
     }
     __syncthreads();
     if (!computes) return;
-    const float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-    const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
-    float* part = nullptr;
+    float* part_row = nullptr;
     if (p.partials != nullptr)
-        part = p.partials + ((uint64_t)(row * a.kv_heads + kv_head) * p.splits + split) *
-                                (uint64_t)(qpk * (2u + kPagedAttentionHeadLimit));
+        part_row = p.partials + ((uint64_t)(row * a.kv_heads + kv_head) * p.splits + split) *
+                                    (uint64_t)(qpk * (2u + kPagedAttentionHeadLimit));
     if (bad_lds != 0u) {
         // an invalid page on the way leaves the tile's outputs unwritten
-        if (part != nullptr && row_ok && g == 0) part[w] = __builtin_nanf("");
+        if (part_row != nullptr && row_ok && g == 0) {
+#pragma unroll
+            for (int i = 0; i < HPW; ++i)
+                if (hv[i]) part_row[w * HPW + i] = __builtin_nanf("");
+        }
         return;
     }
     // rows without tokens in this split (tau >= vis for all of them) are not
     // read by the combine (it uses ceil(pages(row) / per) splits)
     if (!row_ok || t_begin >= vis) return;
-    if (part == nullptr) {
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-            const uint64_t oi = (uint64_t)row * a.output_row_stride + (uint64_t)head * D + db * 16 + 4 * g;
-            if (a.output_dtype == PSK_OUT_F32) {
-                f32x4 v = o[db] / l_all;
-                *reinterpret_cast<f32x4*>(static_cast<float*>(a.output) + oi) = v;
-            } else {
-                uint16_t* dst = static_cast<uint16_t*>(a.output) + oi;
-                u32x2 pk;
-                pk[0] = pack_bf16x2(o[db][0] / l_all, o[db][1] / l_all);
-                pk[1] = pack_bf16x2(o[db][2] / l_all, o[db][3] / l_all);
-                *reinterpret_cast<u32x2*>(dst) = pk;
+    for (int i = 0; i < HPW; ++i) {
+        if (!hv[i]) continue;
+        const uint32_t gh = w * HPW + (uint32_t)i;
+        const uint32_t head = kv_head * qpk + gh;
+        const float l_tot = l_run[i] + __shfl_xor(l_run[i], 16, 64);
+        const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
+        if (part_row == nullptr) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const uint64_t oi =
+                    (uint64_t)row * a.output_row_stride + (uint64_t)head * D + db * 16 + 4 * g;
+                if (a.output_dtype == PSK_OUT_F32) {
+                    f32x4 v = o[i][db] / l_all;
+                    *reinterpret_cast<f32x4*>(static_cast<float*>(a.output) + oi) = v;
+                } else {
+                    uint16_t* dst = static_cast<uint16_t*>(a.output) + oi;
+                    u32x2 pk;
+                    pk[0] = pack_bf16x2(o[i][db][0] / l_all, o[i][db][1] / l_all);
+                    pk[1] = pack_bf16x2(o[i][db][2] / l_all, o[i][db][3] / l_all);
+                    *reinterpret_cast<u32x2*>(dst) = pk;
+                }
             }
-        }
-    } else {
-        if (g == 0) {
-            part[w] = m_run * 0.69314718055994531f;
-            part[qpk + w] = l_all;
-        }
+        } else {
+            if (g == 0) {
+                part_row[gh] = m_run[i] * 0.69314718055994531f;
+                part_row[qpk + gh] = l_all;
+            }
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-            *reinterpret_cast<f32x4*>(part + 2u * qpk + w * kPagedAttentionHeadLimit + db * 16 + 4 * g) = o[db];
+            for (int db = 0; db < NDB; ++db)
+                *reinterpret_cast<f32x4*>(part_row + 2u * qpk + gh * kPagedAttentionHeadLimit +
+                                          db * 16 + 4 * g) = o[i][db];
+        }
     }
 }
 
 bool tile_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, const void* vp) {
     const uint32_t qpk = c.q_heads / c.kv_heads;
-    if (qpk == 0u || qpk > (uint32_t)kMaxTileWaves) return false;
+    if (qpk == 0u || qpk > (uint32_t)kMaxTileHeads) return false;
     const uint32_t D = c.head_dim;
     if (!(D == 64 || D == 128 || D == 256 || (D == 32 && kvb == 2))) return false;
     const uint32_t al = 16u / (uint32_t)kvb;
@@ -467,38 +507,41 @@ bool tile_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
     return true;
 }
 
-template <int KVB, int D, int NW, bool kAl16>
+template <int KVB, int D, int NW, int HPW, bool kAl16>
 hipError_t launch_tile_t3(const TileParams& p, uint64_t grid, hipStream_t stream) {
     const size_t lds_bytes = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * tile_stage_bytes<KVB, D>();
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_tile_kernel<KVB, D, NW, kAl16>),
+            reinterpret_cast<const void*>(&paged_tile_kernel<KVB, D, NW, HPW, kAl16>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((paged_tile_kernel<KVB, D, NW, kAl16>), dim3((uint32_t)grid), dim3(NW * 64),
+    hipLaunchKernelGGL((paged_tile_kernel<KVB, D, NW, HPW, kAl16>), dim3((uint32_t)grid), dim3(NW * 64),
                        lds_bytes, stream, p);
     return hipGetLastError();
 }
 
-template <int KVB, int D, int NW>
+template <int KVB, int D, int NW, int HPW>
 hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream) {
-    return (p.a.page_tokens & 15u) == 0u ? launch_tile_t3<KVB, D, NW, true>(p, grid, stream)
-                                         : launch_tile_t3<KVB, D, NW, false>(p, grid, stream);
+    return (p.a.page_tokens & 15u) == 0u ? launch_tile_t3<KVB, D, NW, HPW, true>(p, grid, stream)
+                                         : launch_tile_t3<KVB, D, NW, HPW, false>(p, grid, stream);
 }
 
-// One wave per query head of the GQA group (at least 4 waves, so every SIMD
-// issues part of the DMAs).
+// Waves and heads per wave by group size: up to 4 heads one per wave (4
+// waves, so every SIMD issues part of the DMAs); 5-8 heads two per wave, so
+// each converted K/V fragment feeds two MFMAs and the LDS reads of a chunk
+// halve (measured on the 6-head group at D=256: 3 waves of two heads beat 6
+// waves of one by 12% in spite of a few spilled registers at 2 waves/SIMD).
 template <int KVB, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     const uint64_t tiles = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1) / kTileRows;
     const uint64_t grid = tiles * p.a.kv_heads * p.splits;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    if (qpk <= 4u) return launch_tile_t2<KVB, D, 4>(p, grid, stream);
-    if (qpk <= 6u) return launch_tile_t2<KVB, D, 6>(p, grid, stream);
-    return launch_tile_t2<KVB, D, 8>(p, grid, stream);
+    if (qpk <= 4u) return launch_tile_t2<KVB, D, 4, 1>(p, grid, stream);
+    if (qpk <= 6u) return launch_tile_t2<KVB, D, 3, 2>(p, grid, stream);
+    return launch_tile_t2<KVB, D, 4, 2>(p, grid, stream);
 }
 
 template <int KVB>
@@ -576,14 +619,15 @@ hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dty
 }
 
 // Tile workgroups that fit one CU: LDS (block-table window + pipeline
-// stages) and waves (at most 3 per SIMD at the kernel's register budget).
+// stages) and waves (3 per SIMD with one head per wave, 2 with two).
 uint32_t tile_workgroups_per_cu(int kvb, uint32_t head_dim, uint32_t q_per_kv) {
     const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
     const size_t stage = 2 * 2 * (16 * D * kvb + 128) + (kvb == 1 ? 2 * 2 * 256 : 0);
     const size_t lds = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * stage + 64;
     const uint32_t by_lds = (uint32_t)((160u * 1024u) / lds);
-    const uint32_t nw = q_per_kv <= 4u ? 4u : q_per_kv <= 6u ? 6u : 8u;
-    const uint32_t by_waves = 12u / nw;
+    const uint32_t hpw = q_per_kv <= 4u ? 1u : 2u;
+    const uint32_t nw = q_per_kv <= 4u ? 4u : (q_per_kv + hpw - 1u) / hpw;
+    const uint32_t by_waves = 4u * (uint32_t)tile_waves_per_simd((int)hpw) / nw;
     const uint32_t n = by_lds < by_waves ? by_lds : by_waves;
     return n == 0u ? 1u : n;
 }
