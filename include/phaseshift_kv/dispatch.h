@@ -63,13 +63,14 @@ struct PlannedKernel {
     uint32_t pages_per_split = 0;
     uint32_t tile_first = 0;      // Tile: range in PagedAttentionPlan::tiles
     uint32_t tile_count = 0;
+    uint32_t tiles_per_group = 1; // Tile: consecutive tiles per workgroup (rows == 0 pads)
     uint32_t req_first = 0;       // Tile with splits > 1: combine ranges
     uint32_t req_count = 0;
 };
 
 struct PlannedTile {
     uint32_t row_begin;   // absolute step row
-    uint32_t rows;        // 1..16, one sequence
+    uint32_t rows;        // 1..16, one sequence; 0: padding of a tile group
 };
 
 struct PagedAttentionPlan {

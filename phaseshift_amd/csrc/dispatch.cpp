@@ -19,8 +19,11 @@ uint32_t tile_workgroups_per_cu(int kvb, uint32_t head_dim, uint32_t q_per_kv);
 hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
                               const void* v, const float* ks, const float* vs,
                               const uint32_t* tile_begin, const uint32_t* tile_rows,
-                              uint32_t n_tiles, float* partials, uint32_t splits,
-                              uint32_t pages_per_split, hipStream_t stream);
+                              uint32_t n_tiles, uint32_t tiles_per_group, float* partials,
+                              uint32_t splits, uint32_t pages_per_split, hipStream_t stream);
+uint32_t tile_group_size(uint32_t q_per_kv);
+uint64_t tile_launch_workgroups(uint64_t n_tiles, uint32_t tiles_per_group, uint32_t q_per_kv,
+                                uint32_t kv_heads);
 bool paged_tiles_supported(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
                            const void* v);
 }  // namespace psk
@@ -173,16 +176,16 @@ namespace {
 // Tile launches: split only until the grid fills the GPU's tile workgroup
 // slots (prefill chunks of 512 rows usually fill them unsplit; a few verify
 // blocks over long contexts need splits to occupy the CUs).
-DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t region_rows, uint32_t kv_heads,
-                              uint32_t q_heads, uint32_t head_dim, uint32_t kv_bytes,
-                              uint32_t page_tokens, uint32_t max_visible_tokens,
-                              uint64_t partial_bytes) {
+DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t tiles_per_group, uint32_t region_rows,
+                              uint32_t kv_heads, uint32_t q_heads, uint32_t head_dim,
+                              uint32_t kv_bytes, uint32_t page_tokens,
+                              uint32_t max_visible_tokens, uint64_t partial_bytes) {
     DecodeSplit s;
     if (max_visible_tokens < kSplitMinVisible || n_tiles == 0 || kv_heads == 0) return s;
     const uint32_t q_per_kv = q_heads / kv_heads;
     const uint64_t slots = (uint64_t)device_cus() *
                            psk::tile_workgroups_per_cu(kv_bytes == 1 ? 1 : 2, head_dim, q_per_kv);
-    const uint64_t wgs = (uint64_t)n_tiles * kv_heads;
+    const uint64_t wgs = psk::tile_launch_workgroups(n_tiles, tiles_per_group, q_per_kv, kv_heads);
     if (wgs >= slots) return s;
     const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
     uint64_t splits = std::min<uint64_t>((slots + wgs - 1) / wgs, max_pages / kMinPagesPerSplit);
@@ -282,31 +285,49 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         k.tile_first = static_cast<uint32_t>(plan.tiles.size());
         k.req_first = static_cast<uint32_t>(plan.combine.size());
         uint32_t lo = UINT32_MAX, hi = 0;
-        std::vector<std::pair<uint32_t, PlannedTile>> tiles;   // (visible bound, tile)
+        // prefill tiles go in groups of consecutive tiles of one request (the
+        // kernel stages each K/V chunk once for the group); rows == 0 pads
+        const uint32_t group =
+            cls == kExecPrefill ? psk::tile_group_size(c.kv_heads ? c.q_heads / c.kv_heads : 0u) : 1u;
+        // (visible bound, first tile of the group in `flat`)
+        std::vector<std::pair<uint32_t, size_t>> groups;
+        std::vector<PlannedTile> flat;
         for (const auto& r : reqs) {
             if (r.execution_class != cls || !is_tile_request(r)) continue;
-            for (uint32_t t = 0; t < r.row_count; t += kTileRowsPerTile) {
-                const uint32_t n = std::min(kTileRowsPerTile, r.row_count - t);
-                // rows of a request see prefix + index + 1 tokens
-                const uint32_t vis = r.max_visible != 0 ? r.max_visible - (r.row_count - t - n)
-                                                        : step.max_visible_tokens;
-                tiles.push_back({vis, {r.row_begin + t, n}});
+            for (uint32_t t = 0; t < r.row_count; t += kTileRowsPerTile * group) {
+                const size_t first = flat.size();
+                uint32_t vis = 0;
+                for (uint32_t j = 0; j < group; ++j) {
+                    const uint32_t tt = t + j * kTileRowsPerTile;
+                    if (tt >= r.row_count) {
+                        flat.push_back({r.row_begin + t, 0u});
+                        continue;
+                    }
+                    const uint32_t n = std::min(kTileRowsPerTile, r.row_count - tt);
+                    // rows of a request see prefix + index + 1 tokens
+                    vis = r.max_visible != 0 ? r.max_visible - (r.row_count - tt - n)
+                                             : step.max_visible_tokens;
+                    flat.push_back({r.row_begin + tt, n});
+                }
+                groups.push_back({vis, first});
             }
             plan.combine.push_back(r);
             lo = std::min(lo, r.row_begin);
             hi = std::max(hi, r.row_begin + r.row_count);
         }
-        // longest tiles first: workgroups are dispatched in tile order
-        std::stable_sort(tiles.begin(), tiles.end(),
+        // longest groups first: workgroups are dispatched in tile order
+        std::stable_sort(groups.begin(), groups.end(),
                          [](const auto& x, const auto& y) { return x.first > y.first; });
-        for (const auto& t : tiles) plan.tiles.push_back(t.second);
+        for (const auto& gr : groups)
+            for (uint32_t j = 0; j < group; ++j) plan.tiles.push_back(flat[gr.second + j]);
+        k.tiles_per_group = group;
         k.tile_count = static_cast<uint32_t>(plan.tiles.size()) - k.tile_first;
         k.req_count = static_cast<uint32_t>(plan.combine.size()) - k.req_first;
         if (k.tile_count == 0) continue;
         k.row_begin = lo;
         k.rows = hi - lo;
         const DecodeSplit s = choose_tile_split(
-            k.tile_count, k.rows, c.kv_heads, c.q_heads, c.head_dim,
+            k.tile_count, k.tiles_per_group, k.rows, c.kv_heads, c.q_heads, c.head_dim,
             step.kv_dtype == KVCacheDType::FP8_E4M3 ? 1u : 2u, c.page_tokens,
             step.max_visible_tokens, pbytes);
         k.splits = s.splits;
@@ -361,7 +382,8 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
             if (psk::paged_tiles_supported(*ca, kvd, step.k_pool, step.v_pool)) {
                 e = psk::launch_paged_tiles(*ca, kvd, step.k_pool, step.v_pool, ksf,
                                             vsf, tb.data(), tr.data(), k.tile_count,
-                                            step.partials, k.splits, k.pages_per_split, stream);
+                                            k.tiles_per_group, step.partials, k.splits,
+                                            k.pages_per_split, stream);
                 for (uint32_t q = 0; e == hipSuccess && k.splits > 1 && q < k.req_count; ++q) {
                     const StepRequest& r = plan.combine[k.req_first + q];
                     const PagedAttentionCommonArgs ra =
@@ -376,6 +398,7 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
             } else {
                 // shapes outside the tile kernel: every row of each tile on the decode kernel
                 for (uint32_t t = 0; e == hipSuccess && t < k.tile_count; ++t) {
+                    if (tr[t] == 0u) continue;   // group padding
                     const PagedAttentionCommonArgs ta = region_args(a, tb[t], tr[t]);
                     e = fp8 ? launch_attention_paged_fp8_e4m3(ta, k8, v8, ksf, vsf, stream)
                             : launch_attention_paged_bf16(ta, k16, v16, stream);

@@ -33,9 +33,14 @@ constexpr uint32_t kMaxTileSplits = 1024;
 // arguments; n_tiles == 0 means the implicit windows [16t, 16t+16).
 constexpr uint32_t kInlineTiles = 256;
 
+// Tiles per workgroup of a grouped launch (consecutive list entries of one
+// sequence; rows == 0 pads a group).
+constexpr int kTileGroup = 4;
+
 struct TileParams {
     psk_paged_attention_args a;
     uint32_t n_tiles;
+    uint32_t tiles_per_group;   // 1, or kTileGroup: explicit tiles grouped
     uint32_t tile_begin[kInlineTiles];
     uint8_t tile_rows[kInlineTiles];
     const uint8_t* k_pool;
@@ -85,8 +90,14 @@ constexpr int kTileStages = 4;
 // with two (the accumulators of 2 heads take 128 registers at D=256).
 constexpr int tile_waves_per_simd(int hpw) { return hpw == 1 ? 3 : 2; }
 
-template <int KVB, int D, int NW, int HPW, bool kAl16>
+// RT: row tiles per workgroup. RT == 1: the NW waves split the GQA group's
+// heads (HPW each) of one tile. RT > 1 (NW == RT): wave w owns tile w of a
+// group of RT consecutive tiles of one sequence and HPW heads of the group's
+// head part (blockIdx); the tiles share every staged K/V chunk.
+template <int KVB, int D, int NW, int HPW, int RT, bool kAl16>
 __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_kernel(const TileParams p) {
+    static_assert(RT == 1 || RT == NW, "grouped tiles: one wave per tile");
+    constexpr int WH = NW / RT;          // waves along the heads of one tile
     constexpr int H = 2;                 // 16-token halves per chunk
     constexpr int CT = 16 * H;           // tokens per chunk
     constexpr int NL = D * KVB / 64;     // 16 B DMA pieces per lane per half
@@ -118,23 +129,41 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     const uint32_t qpk = a.q_heads / a.kv_heads;
 
     const uint32_t split = blockIdx.x % p.splits;
-    const uint32_t rest = blockIdx.x / p.splits;
+    uint32_t rest = blockIdx.x / p.splits;
+    uint32_t hpart = 0;
+    if constexpr (RT > 1) {
+        const uint32_t hparts = (qpk + HPW - 1u) / HPW;
+        hpart = rest % hparts;
+        rest /= hparts;
+    }
     const uint32_t kv_head = rest % a.kv_heads;
-    const uint32_t tile = rest / a.kv_heads;
+    const uint32_t group = rest / a.kv_heads;
+    const uint32_t rt = RT > 1 ? w : 0u;
+    const uint32_t tile = group * RT + rt;
+    // the group's first tile names the sequence (workgroup-uniform)
+    uint32_t g0;
+    if (p.n_tiles != 0u) {
+        if (group * RT >= p.n_tiles) return;
+        g0 = p.tile_begin[group * RT];
+    } else {
+        g0 = group * RT * kTileRows;
+    }
+    if (g0 >= a.rows) return;
+    const uint32_t slot = a.row_sequence_slots[g0];
+    if (slot >= a.max_sequences) return;
+    // this wave's tile; a grouped tile past the list or of no rows computes nothing
     uint32_t r0, nrows;
     if (p.n_tiles != 0u) {
-        if (tile >= p.n_tiles) return;
-        r0 = p.tile_begin[tile];
-        nrows = p.tile_rows[tile];
+        const bool have = tile < p.n_tiles;
+        r0 = have ? p.tile_begin[tile] : g0;
+        nrows = have ? p.tile_rows[tile] : 0u;
     } else {
         r0 = tile * kTileRows;
         nrows = r0 < a.rows ? min((uint32_t)kTileRows, a.rows - r0) : 0u;
     }
-    if (nrows == 0u || r0 >= a.rows) return;
-    nrows = min(nrows, a.rows - r0);
+    if (r0 >= a.rows) nrows = 0u;
+    nrows = min(nrows, a.rows - min(r0, a.rows));
 
-    const uint32_t slot = a.row_sequence_slots[r0];
-    if (slot >= a.max_sequences) return;
     const uint64_t cap = (uint64_t)a.block_table_stride * a.page_tokens;
     // row n of the tile (column n of every MFMA): its own visibility
     const uint32_t row = r0 + n;
@@ -148,7 +177,17 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     uint32_t vis_max = vis;
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) vis_max = max(vis_max, (uint32_t)__shfl_xor((int)vis_max, o, 64));
-    if (vis_max == 0u) return;   // uniform: every wave saw the same 16 rows
+    const uint32_t wave_vis = vis_max;   // this wave's rows see tokens [0, wave_vis)
+    if constexpr (RT > 1) {
+        // the workgroup streams the longest visible range of its tiles
+        __shared__ uint32_t group_vis;
+        if (tid == 0) group_vis = 0u;
+        __syncthreads();
+        if (lane == 0) atomicMax(&group_vis, wave_vis);
+        __syncthreads();
+        vis_max = group_vis;
+    }
+    if (vis_max == 0u) return;   // uniform over the workgroup
     const uint32_t P = a.page_tokens;
     const uint32_t pc = (vis_max + P - 1u) / P;
     const uint32_t per = p.pages_per_split != 0u ? p.pages_per_split : (pc + p.splits - 1u) / p.splits;
@@ -162,7 +201,8 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     // Everything above is uniform over the workgroup, so all waves reach the
     // barriers below; a wave past the last query head of the group only
     // issues its share of the DMAs.
-    const bool computes = w * HPW < qpk;
+    const uint32_t hbase = RT > 1 ? hpart * HPW : w * HPW;   // first head (group index)
+    const bool computes = hbase < qpk && wave_vis > 0u;
 
     if (tid == 0) bad_lds = 0u;
 
@@ -173,7 +213,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     bf16x8 qf[HPW][NS];
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
-        const uint32_t gh = w * HPW + (uint32_t)i;
+        const uint32_t gh = hbase + (uint32_t)i;
         hv[i] = gh < qpk;
         const uint32_t head = kv_head * qpk + (hv[i] ? gh : 0u);
         const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
@@ -420,7 +460,8 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         auto step = [&](uint32_t c, uint8_t* __restrict__ next,
                         const uint8_t* __restrict__ cur) __attribute__((always_inline)) {
             issue(c + (kTileStages - 1u) * CT, next);
-            if (computes) consume(c, cur);
+            // chunks past this wave's rows add nothing to them
+            if (computes && c < wave_vis) consume(c, cur);
         };
 
         // kTileStages - 1 chunks in flight: the DMAs of chunk k go out
@@ -450,7 +491,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         if (part_row != nullptr && row_ok && g == 0) {
 #pragma unroll
             for (int i = 0; i < HPW; ++i)
-                if (hv[i]) part_row[w * HPW + i] = __builtin_nanf("");
+                if (hv[i]) part_row[hbase + i] = __builtin_nanf("");
         }
         return;
     }
@@ -460,7 +501,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
         if (!hv[i]) continue;
-        const uint32_t gh = w * HPW + (uint32_t)i;
+        const uint32_t gh = hbase + (uint32_t)i;
         const uint32_t head = kv_head * qpk + gh;
         const float l_tot = l_run[i] + __shfl_xor(l_run[i], 16, 64);
         const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
@@ -507,36 +548,44 @@ bool tile_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
     return true;
 }
 
-template <int KVB, int D, int NW, int HPW, bool kAl16>
+template <int KVB, int D, int NW, int HPW, int RT, bool kAl16>
 hipError_t launch_tile_t3(const TileParams& p, uint64_t grid, hipStream_t stream) {
     const size_t lds_bytes = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * tile_stage_bytes<KVB, D>();
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_tile_kernel<KVB, D, NW, HPW, kAl16>),
+            reinterpret_cast<const void*>(&paged_tile_kernel<KVB, D, NW, HPW, RT, kAl16>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((paged_tile_kernel<KVB, D, NW, HPW, kAl16>), dim3((uint32_t)grid), dim3(NW * 64),
-                       lds_bytes, stream, p);
+    hipLaunchKernelGGL((paged_tile_kernel<KVB, D, NW, HPW, RT, kAl16>), dim3((uint32_t)grid),
+                       dim3(NW * 64), lds_bytes, stream, p);
     return hipGetLastError();
 }
 
-template <int KVB, int D, int NW, int HPW>
+template <int KVB, int D, int NW, int HPW, int RT = 1>
 hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream) {
-    return (p.a.page_tokens & 15u) == 0u ? launch_tile_t3<KVB, D, NW, HPW, true>(p, grid, stream)
-                                         : launch_tile_t3<KVB, D, NW, HPW, false>(p, grid, stream);
+    return (p.a.page_tokens & 15u) == 0u ? launch_tile_t3<KVB, D, NW, HPW, RT, true>(p, grid, stream)
+                                         : launch_tile_t3<KVB, D, NW, HPW, RT, false>(p, grid, stream);
 }
 
 // Waves and heads per wave by group size: up to 4 heads one per wave (4
 // waves, so every SIMD issues part of the DMAs); 5-8 heads two per wave, so
 // each converted K/V fragment feeds two MFMAs and the LDS reads of a chunk
-// halve (measured on the 6-head group at D=256: 3 waves of two heads beat 6
-// waves of one by 12% in spite of a few spilled registers at 2 waves/SIMD).
+// halve. 5-6 heads in grouped launches (tiles_per_group == kTileGroup): four
+// waves, one per tile, each on two heads of the group's head part, so two
+// workgroups fill every SIMD with two waves (three waves per workgroup would
+// leave two SIMDs doubly loaded and every chunk barrier waiting on them).
 template <int KVB, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     const uint64_t tiles = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1) / kTileRows;
+    if (p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u) {
+        const uint64_t groups = (tiles + kTileGroup - 1) / kTileGroup;
+        const uint64_t grid = groups * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits;
+        if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        return launch_tile_t2<KVB, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
+    }
     const uint64_t grid = tiles * p.a.kv_heads * p.splits;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
     if (qpk <= 4u) return launch_tile_t2<KVB, D, 4, 1>(p, grid, stream);
@@ -584,6 +633,7 @@ TileParams make_tile(const psk_paged_attention_args& c, const void* k, const voi
     p.splits = splits;
     p.pages_per_split = pps;
     p.scale_log2 = c.scale * kLog2e;
+    p.tiles_per_group = 1u;
     return p;
 }
 
@@ -595,19 +645,25 @@ TileParams make_tile(const psk_paged_attention_args& c, const void* k, const voi
 hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
                               const void* v, const float* ks, const float* vs,
                               const uint32_t* tile_begin, const uint32_t* tile_rows,
-                              uint32_t n_tiles, float* partials, uint32_t splits,
-                              uint32_t pages_per_split, hipStream_t stream) {
+                              uint32_t n_tiles, uint32_t tiles_per_group, float* partials,
+                              uint32_t splits, uint32_t pages_per_split, hipStream_t stream) {
     const hipError_t e = tile_validate(&a, k, v);
     if (e != hipSuccess) return e;
     const int kvb = kv_dtype == PSK_KV_FP8_E4M3 ? 1 : 2;
     if (!tile_shape_ok(a, kvb, k, v)) return hipErrorNotSupported;
     if (splits > 1u && (partials == nullptr || pages_per_split == 0u)) return hipErrorInvalidValue;
+    if (tiles_per_group != 1u &&
+        (tiles_per_group != (uint32_t)kTileGroup || n_tiles % (uint32_t)kTileGroup != 0u))
+        return hipErrorInvalidValue;
     for (uint32_t b = 0; b < n_tiles; b += kInlineTiles) {
         TileParams p = make_tile(a, k, v, ks, vs, splits > 1u ? partials : nullptr, splits,
                                  pages_per_split);
+        p.tiles_per_group = tiles_per_group;
         p.n_tiles = n_tiles - b < kInlineTiles ? n_tiles - b : kInlineTiles;
         for (uint32_t i = 0; i < p.n_tiles; ++i) {
-            if (tile_rows[b + i] == 0u || tile_rows[b + i] > (uint32_t)kTileRows)
+            // rows == 0 only pads a group after its first tile
+            const bool pad_ok = tiles_per_group > 1u && i % tiles_per_group != 0u;
+            if ((tile_rows[b + i] == 0u && !pad_ok) || tile_rows[b + i] > (uint32_t)kTileRows)
                 return hipErrorInvalidValue;
             p.tile_begin[i] = tile_begin[b + i];
             p.tile_rows[i] = static_cast<uint8_t>(tile_rows[b + i]);
@@ -630,6 +686,19 @@ uint32_t tile_workgroups_per_cu(int kvb, uint32_t head_dim, uint32_t q_per_kv) {
     const uint32_t by_waves = 4u * (uint32_t)tile_waves_per_simd((int)hpw) / nw;
     const uint32_t n = by_lds < by_waves ? by_lds : by_waves;
     return n == 0u ? 1u : n;
+}
+
+// Tiles per workgroup the step planner should group a prefill launch into.
+uint32_t tile_group_size(uint32_t q_per_kv) {
+    return q_per_kv > 4u && q_per_kv <= 6u ? (uint32_t)kTileGroup : 1u;
+}
+
+// Workgroups of a tile launch of n_tiles (a multiple of tiles_per_group when grouped).
+uint64_t tile_launch_workgroups(uint64_t n_tiles, uint32_t tiles_per_group, uint32_t q_per_kv,
+                                uint32_t kv_heads) {
+    if (tiles_per_group > 1u)
+        return (n_tiles + tiles_per_group - 1u) / tiles_per_group * ((q_per_kv + 1u) / 2u) * kv_heads;
+    return n_tiles * kv_heads;
 }
 
 bool paged_tiles_supported(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,

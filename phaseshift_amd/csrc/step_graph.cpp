@@ -55,6 +55,7 @@ std::vector<uint8_t> plan_signature_bytes(const PagedAttentionStep& step, const 
         put(k, p.pages_per_split);
         put(k, p.tile_first);
         put(k, p.tile_count);
+        put(k, p.tiles_per_group);
         put(k, p.req_first);
         put(k, p.req_count);
     }

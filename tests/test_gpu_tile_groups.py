@@ -1,0 +1,84 @@
+"""Grouped prefill tiles (GQA groups of 5-6 heads): the step planner puts
+consecutive 16-row tiles of one prefill request into groups of four (one
+workgroup, one wave per tile, the group's K/V chunks staged once) and pads a
+short last group with empty tiles. Ragged requests (partial groups, a partial
+last tile, a chunk at position 0) and split and unsplit launches, every row
+against the fp32 oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import phaseshift_amd as P
+from phaseshift_amd import ops, state
+from tests.kvcase import bf16_normal, paged_layout, to_dev
+from tests.test_gpu_paged_attention import TOL, make_pools, oracle_out
+
+pytestmark = pytest.mark.gpu
+
+
+def grouped_step(dev, fp8, qh, kvh, D, split):
+    rng = np.random.default_rng(qh * 7 + fp8 + 2 * split)
+    # (prefix, rows, class): 328 rows = 20 full tiles + 8 (6 groups, the last
+    # padded), 136 rows from position 0 (3 groups), 128 rows (2 full groups),
+    # decode rows between them
+    reqs_spec = [(1500, 328, 2), (900, 1, 0), (0, 136, 2), (2100, 1, 0), (700, 128, 2),
+                 (333, 1, 0)]
+    lens = [p + n for p, n, _ in reqs_spec]
+    lay = paged_layout(rng, lens, 16, kvh, D, spare_pages=2)
+    kp, vp, ks, vs = make_pools(lay, fp8, 11 + qh, dev)
+    slots, pos, reqs, row = [], [], [], 0
+    for s, (p, n, cls) in enumerate(reqs_spec):
+        slots += [s] * n
+        pos += list(range(p, p + n))
+        reqs.append((row, n, cls, p + n))
+        row += n
+    slots, pos = np.array(slots, np.uint32), np.array(pos, np.uint32)
+    q = bf16_normal(rng, (row, qh * D))
+    g = ops.PoolGeometry(1, lay.num_pages, 16, kvh, D)
+    out = torch.full((row, qh * D), 7.0, dtype=torch.float32, device=dev)
+    a = ops.attention_args(g, 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                           to_dev(lay.block_tables), qh)
+    nbytes = (64 << 20) if split else 0
+    part = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=dev) if split else None
+    maxvis = max(lens)
+    kvd = P.KV_FP8 if fp8 else P.KV_BF16
+    plan = state.plan_step(a, kvd, reqs, maxvis, nbytes, partials_ptr=part, k_pool=kp,
+                           v_pool=vp, k_scale=ks, v_scale=vs, launch=True)
+    torch.cuda.synchronize()
+    want = oracle_out(lay, qh, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
+    return plan, out.cpu().numpy(), want
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("qh,kvh", [(24, 4), (20, 4)])   # 6 heads per group; 5 (a half-empty head part)
+@pytest.mark.parametrize("split", [False, True])
+def test_grouped_prefill_vs_oracle(dev, fp8, qh, kvh, split):
+    plan, got, want = grouped_step(dev, fp8, qh, kvh, 256, split)
+    kinds = [k.kind for k in plan.kernels[:plan.count]]
+    assert kinds.count(1) == 1                      # one tile launch for the three prefill requests
+    tile = [k for k in plan.kernels[:plan.count] if k.kind == 1][0]
+    assert (tile.splits > 1) == split
+    assert not np.any(got == 7.0)
+    err = np.max(np.abs(got - want), axis=1)
+    assert np.max(err) < TOL[fp8], (int(np.argmax(err)), float(np.max(err)))
+
+
+def test_grouped_prefill_d128(dev):
+    """head_dim 128 through the same grouped path."""
+    rng = np.random.default_rng(3)
+    lens = [400 + 200]
+    lay = paged_layout(rng, lens, 16, 2, 128, spare_pages=2)
+    kp, vp, ks, vs = make_pools(lay, True, 5, dev)
+    slots = np.zeros(200, np.uint32)
+    pos = np.arange(400, 600, dtype=np.uint32)
+    q = bf16_normal(rng, (200, 12 * 128))
+    g = ops.PoolGeometry(1, lay.num_pages, 16, 2, 128)
+    out = torch.full((200, 12 * 128), 7.0, dtype=torch.float32, device=dev)
+    a = ops.attention_args(g, 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                           to_dev(lay.block_tables), 12)
+    state.plan_step(a, P.KV_FP8, [(0, 200, 2, 600)], 600, 0, k_pool=kp, v_pool=vp, k_scale=ks,
+                    v_scale=vs, launch=True)
+    torch.cuda.synchronize()
+    want = oracle_out(lay, 12, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
+    assert np.max(np.abs(out.cpu().numpy() - want)) < TOL[True]
