@@ -115,7 +115,10 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     // remainder repeats earlier ones, which rewrite identical bytes), so the
     // vmcnt bookkeeping is one compile-time count per wave.
     constexpr int NI = 2 * H * NL + (KVB == 1 ? 2 * H : 0);
-    constexpr int DPW = (NI + NW - 1) / NW;
+    // NW == 2H: wave w owns one stream, K (w < H) or V, half w % H: its NL body
+    // pieces and (FP8) that half's scales, so the dealing is fixed per wave
+    constexpr bool kOwnStream = NW == 2 * H;
+    constexpr int DPW = kOwnStream ? NL + (KVB == 1 ? 1 : 0) : (NI + NW - 1) / NW;
     constexpr int kWinBytes = (int)kTilePageWindow * 4;
     static_assert(NL >= 1 && NS >= 1 && 2 * DPW < 64, "tile geometry");
 
@@ -270,7 +273,49 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
 
         // This wave's DMAs of the chunk at c into stage st (branch-free;
         // tokens past the range read the last token and are masked later).
+        auto issue_own = [&](uint32_t c, uint8_t* st) __attribute__((always_inline)) {
+            const uint32_t hf = wu % (uint32_t)H;   // scalar
+            const uint32_t kind = wu / (uint32_t)H;
+            const uint32_t tau = min(c + hf * 16u + n, t_last);
+            uint32_t page, off;
+            if constexpr (kAl16) {
+                const uint32_t hb = min(c + hf * 16u, t_last);
+                const uint32_t pi = hb / P;
+                page = __builtin_amdgcn_readfirstlane(win[pi - wp]);
+                off = tau - pi * P;
+            } else {
+                page = win[tau / P - wp];
+                off = tau % P;
+            }
+            const bool inv = page >= a.num_pages;
+            if (inv) bad_lds = 1u;
+            const uint32_t pg = inv ? 0u : page;
+            const uint8_t* pool = kind == 0u ? k_pool : v_pool;
+            uint8_t* dst = st + kind * KV_BYTES + hf * HALF_STRIDE;
+            if constexpr (kAl16) {
+                const uint8_t* src = pool + (layer_base + (uint64_t)pg * a.elems_per_page +
+                                             (uint64_t)kv_head * D) * KVB;
+                const uint32_t lo = off * a.elems_per_token * KVB + g * 16u;
+#pragma unroll
+                for (int i = 0; i < NL; ++i) load_lds<16>(src + (lo + i * 64u), dst + i * 1024);
+            } else {
+                const uint8_t* src = pool + (layer_base + (uint64_t)pg * a.elems_per_page +
+                                             (uint64_t)off * a.elems_per_token + (uint64_t)kv_head * D) * KVB +
+                                     g * 16u;
+#pragma unroll
+                for (int i = 0; i < NL; ++i) load_lds<16>(src + i * 64, dst + i * 1024);
+            }
+            if constexpr (KVB == 1) {
+                const uint64_t si = ((scale_layer + pg) * P + off) * a.kv_heads + kv_head;
+                load_lds<4>((kind == 0u ? k_scale : v_scale) + si,
+                            st + 2 * KV_BYTES + kind * SC_BYTES + hf * 256);
+            }
+        };
         auto issue = [&](uint32_t c, uint8_t* st) __attribute__((always_inline)) {
+            if constexpr (kOwnStream) {
+                issue_own(c, st);
+                return;
+            }
             // page ids of this lane's token in both halves first: no LDS read
             // follows a DMA of this step
             uint32_t pg[H], off[H];
@@ -570,12 +615,13 @@ hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream
 }
 
 // Waves and heads per wave by group size: up to 4 heads one per wave (4
-// waves, so every SIMD issues part of the DMAs); 5-8 heads two per wave, so
-// each converted K/V fragment feeds two MFMAs and the LDS reads of a chunk
-// halve. 5-6 heads in grouped launches (tiles_per_group == kTileGroup): four
-// waves, one per tile, each on two heads of the group's head part, so two
-// workgroups fill every SIMD with two waves (three waves per workgroup would
-// leave two SIMDs doubly loaded and every chunk barrier waiting on them).
+// waves, so every SIMD issues part of the DMAs); 5-6 heads one per wave (6
+// waves: two workgroups put 3 waves on every SIMD); 7-8 heads two per wave.
+// 5-6 heads in grouped launches (tiles_per_group == kTileGroup): four waves,
+// one per tile, each on two heads of the group's head part, so each converted
+// K/V fragment feeds two MFMAs and two workgroups put 2 waves on every SIMD.
+// Wave counts that load the SIMDs unevenly (3 waves per workgroup) lose: the
+// chunk barrier waits on the doubly loaded SIMDs.
 template <int KVB, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
@@ -589,7 +635,7 @@ hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint64_t grid = tiles * p.a.kv_heads * p.splits;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
     if (qpk <= 4u) return launch_tile_t2<KVB, D, 4, 1>(p, grid, stream);
-    if (qpk <= 6u) return launch_tile_t2<KVB, D, 3, 2>(p, grid, stream);
+    if (qpk <= 6u) return launch_tile_t2<KVB, D, 6, 1>(p, grid, stream);
     return launch_tile_t2<KVB, D, 4, 2>(p, grid, stream);
 }
 
