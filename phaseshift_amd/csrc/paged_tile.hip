@@ -18,6 +18,8 @@
 // kernel finishes it.
 #include "device_common.h"
 
+#include <type_traits>
+
 #include <phaseshift_kv/paged_attention.h>
 
 namespace psk {
@@ -115,9 +117,10 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     // remainder repeats earlier ones, which rewrite identical bytes), so the
     // vmcnt bookkeeping is one compile-time count per wave.
     constexpr int NI = 2 * H * NL + (KVB == 1 ? 2 * H : 0);
-    // NW == 2H: wave w owns one stream, K (w < H) or V, half w % H: its NL body
-    // pieces and (FP8) that half's scales, so the dealing is fixed per wave
-    constexpr bool kOwnStream = NW == 2 * H;
+    // NW >= 2H: wave w < 2H owns one stream, K (w < H) or V, half w % H: its
+    // NL body pieces and (FP8) that half's scales, so the dealing is fixed per
+    // wave; waves past 2H issue none (their vmcnt waits pass at once)
+    constexpr bool kOwnStream = NW >= 2 * H;
     constexpr int DPW = kOwnStream ? NL + (KVB == 1 ? 1 : 0) : (NI + NW - 1) / NW;
     constexpr int kWinBytes = (int)kTilePageWindow * 4;
     static_assert(NL >= 1 && NS >= 1 && 2 * DPW < 64, "tile geometry");
@@ -181,6 +184,11 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) vis_max = max(vis_max, (uint32_t)__shfl_xor((int)vis_max, o, 64));
     const uint32_t wave_vis = vis_max;   // this wave's rows see tokens [0, wave_vis)
+    // tokens [0, wave_vis_min) are visible to every row of the wave that is written
+    uint32_t wave_vis_min = row_ok ? vis : 0xFFFFFFFFu;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1)
+        wave_vis_min = min(wave_vis_min, (uint32_t)__shfl_xor((int)wave_vis_min, o, 64));
     if constexpr (RT > 1) {
         // the workgroup streams the longest visible range of its tiles
         __shared__ uint32_t group_vis;
@@ -274,6 +282,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         // This wave's DMAs of the chunk at c into stage st (branch-free;
         // tokens past the range read the last token and are masked later).
         auto issue_own = [&](uint32_t c, uint8_t* st) __attribute__((always_inline)) {
+            if (NW > 2 * H && wu >= 2u * H) return;
             const uint32_t hf = wu % (uint32_t)H;   // scalar
             const uint32_t kind = wu / (uint32_t)H;
             const uint32_t tau = min(c + hf * 16u + n, t_last);
@@ -365,7 +374,10 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         };
 
         // Scores, causal online softmax and PV of the chunk at c in stage st.
-        auto consume = [&](uint32_t c, const uint8_t* st) __attribute__((always_inline)) {
+        // kFull: every token of the chunk is visible to every written row and
+        // inside the split, so no causal mask is formed
+        auto consume = [&](uint32_t c, const uint8_t* st, auto full_tag) __attribute__((always_inline)) {
+            constexpr bool kFull = decltype(full_tag)::value;
             f32x4 sc[HPW][H];
 #pragma unroll
             for (int hf = 0; hf < H; ++hf) {
@@ -407,7 +419,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t tau = c + hf * 16 + 4 * g + r;
-                    tok_ok[hf][r] = tau < vis && tau < te;
+                    tok_ok[hf][r] = kFull || (tau < vis && tau < te);
                 }
             }
             u32x4 pf[HPW], pl[HPW];
@@ -506,7 +518,12 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                         const uint8_t* __restrict__ cur) __attribute__((always_inline)) {
             issue(c + (kTileStages - 1u) * CT, next);
             // chunks past this wave's rows add nothing to them
-            if (computes && c < wave_vis) consume(c, cur);
+            if (computes && c < wave_vis) {
+                if (c + CT <= wave_vis_min && c + CT <= te)
+                    consume(c, cur, std::true_type{});
+                else
+                    consume(c, cur, std::false_type{});
+            }
         };
 
         // kTileStages - 1 chunks in flight: the DMAs of chunk k go out
