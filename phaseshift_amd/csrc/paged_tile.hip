@@ -379,29 +379,75 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         auto consume = [&](uint32_t c, const uint8_t* st, auto full_tag) __attribute__((always_inline)) {
             constexpr bool kFull = decltype(full_tag)::value;
             f32x4 sc[HPW][H];
-#pragma unroll
-            for (int hf = 0; hf < H; ++hf) {
-                f32x4 acc[HPW];
-#pragma unroll
-                for (int i = 0; i < HPW; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-                const uint8_t* kb = st + hf * HALF_STRIDE + 16 * lane;
-#pragma unroll
-                for (int s = 0; s < NS; ++s) {
-                    // one K-step at a time keeps the converted fragments short-lived
-                    if (s % 2 == 0) __builtin_amdgcn_sched_barrier(0);
-                    bf16x8 kf;
-                    if constexpr (KVB == 2) {
-                        kf = *reinterpret_cast<const bf16x8*>(kb + 1024 * s);
+            if constexpr (NS % 2 == 0) {
+                // K in pairs of K-steps (16 B of FP8 or 2 x 16 B of BF16 per
+                // lane), each pair's LDS read issued one pair ahead so that its
+                // latency hides behind the previous pair's MFMAs
+                constexpr int NP = NS / 2;
+                struct KRaw {
+                    u32x4 a, b;
+                };
+                auto kread = [&](int u) __attribute__((always_inline)) {
+                    const uint8_t* kb = st + (u / NP) * HALF_STRIDE + 16 * lane;
+                    KRaw r;
+                    if constexpr (KVB == 1) {
+                        r.a = *reinterpret_cast<const u32x4*>(kb + 1024 * (u % NP));
+                        r.b = r.a;
                     } else {
-                        const u32x4 wv = *reinterpret_cast<const u32x4*>(kb + 1024 * (s >> 1));
-                        kf = (s & 1) ? fp8x8_to_bf16x8(wv[2], wv[3]) : fp8x8_to_bf16x8(wv[0], wv[1]);
+                        r.a = *reinterpret_cast<const u32x4*>(kb + 1024 * (2 * (u % NP)));
+                        r.b = *reinterpret_cast<const u32x4*>(kb + 1024 * (2 * (u % NP) + 1));
+                    }
+                    return r;
+                };
+                f32x4 acc[HPW];
+                KRaw cur = kread(0);
+#pragma unroll
+                for (int u = 0; u < H * NP; ++u) {
+                    KRaw nxt = cur;
+                    if (u + 1 < H * NP) nxt = kread(u + 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    const int sp = u % NP;
+                    if (sp == 0) {
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    }
+                    bf16x8 k0, k1;
+                    if constexpr (KVB == 1) {
+                        k0 = fp8x8_to_bf16x8(cur.a[0], cur.a[1]);
+                        k1 = fp8x8_to_bf16x8(cur.a[2], cur.a[3]);
+                    } else {
+                        k0 = __builtin_bit_cast(bf16x8, cur.a);
+                        k1 = __builtin_bit_cast(bf16x8, cur.b);
                     }
 #pragma unroll
                     for (int i = 0; i < HPW; ++i)
-                        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[i][s], acc[i], 0, 0, 0);
-                }
+                        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[i][2 * sp], acc[i], 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < HPW; ++i) sc[i][hf] = acc[i];
+                    for (int i = 0; i < HPW; ++i)
+                        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[i][2 * sp + 1], acc[i], 0, 0, 0);
+                    if (sp == NP - 1) {
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i) sc[i][u / NP] = acc[i];
+                    }
+                    cur = nxt;
+                }
+            } else {
+#pragma unroll
+                for (int hf = 0; hf < H; ++hf) {
+                    f32x4 acc[HPW];
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    const uint8_t* kb = st + hf * HALF_STRIDE + 16 * lane;
+#pragma unroll
+                    for (int s = 0; s < NS; ++s) {
+                        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kb + 1024 * s);
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i)
+                            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[i][s], acc[i], 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i) sc[i][hf] = acc[i];
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
             // lane (n, g): row n, tokens c + 16*hf + 4*g + r; causal per row
@@ -475,36 +521,57 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 }
             }
             // O^T += V^T P^T, one V fragment per output block for all heads.
-            // The scheduling barriers keep the compiler from hoisting every V
-            // read of the chunk at once.
+            // V is read in pairs of output blocks, each pair's transposing LDS
+            // reads issued one pair ahead of the previous pair's MFMAs.
             const uint8_t* vb = st + KV_BYTES + tr_off;
+            static_assert(NDB % 2 == 0, "output blocks in pairs");
+            struct VRaw {
+                u32x4 x[2];
+            };
+            auto vread = [&](int pr) __attribute__((always_inline)) {
+                VRaw r;
 #pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                if (db % 2 == 0) __builtin_amdgcn_sched_barrier(0);
-                if constexpr (KVB == 1) {
-                    const i32x2 x = tr8(vb + 256 * db);
-                    const f16x8 vf = fp8x8_to_f16x8((uint32_t)x[0], (uint32_t)x[1]);
-#pragma unroll
-                    for (int i = 0; i < HPW; ++i)
-                        o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            vf, __builtin_bit_cast(f16x8, pf[i]), o[i][db], 0, 0, 0);
-                } else {
-                    const i16x4 x0 = tr16(vb + 512 * db);
-                    const i16x4 x1 = tr16(vb + HALF_STRIDE + 512 * db);
-                    u32x4 u;
-                    u[0] = __builtin_bit_cast(u32x2, x0)[0];
-                    u[1] = __builtin_bit_cast(u32x2, x0)[1];
-                    u[2] = __builtin_bit_cast(u32x2, x1)[0];
-                    u[3] = __builtin_bit_cast(u32x2, x1)[1];
-                    const bf16x8 vf = __builtin_bit_cast(bf16x8, u);
-#pragma unroll
-                    for (int i = 0; i < HPW; ++i) {
-                        o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            vf, __builtin_bit_cast(bf16x8, pf[i]), o[i][db], 0, 0, 0);
-                        o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            vf, __builtin_bit_cast(bf16x8, pl[i]), o[i][db], 0, 0, 0);
+                for (int j = 0; j < 2; ++j) {
+                    const int db = 2 * pr + j;
+                    if constexpr (KVB == 1) {
+                        const i32x2 t = tr8(vb + 256 * db);
+                        r.x[j] = (u32x4){(uint32_t)t[0], (uint32_t)t[1], 0u, 0u};
+                    } else {
+                        const i16x4 x0 = tr16(vb + 512 * db);
+                        const i16x4 x1 = tr16(vb + HALF_STRIDE + 512 * db);
+                        r.x[j] = (u32x4){__builtin_bit_cast(u32x2, x0)[0], __builtin_bit_cast(u32x2, x0)[1],
+                                         __builtin_bit_cast(u32x2, x1)[0], __builtin_bit_cast(u32x2, x1)[1]};
                     }
                 }
+                return r;
+            };
+            VRaw vcur = vread(0);
+#pragma unroll
+            for (int pr = 0; pr < NDB / 2; ++pr) {
+                VRaw vnxt = vcur;
+                if (pr + 1 < NDB / 2) vnxt = vread(pr + 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int db = 2 * pr + j;
+                    if constexpr (KVB == 1) {
+                        const f16x8 vf = fp8x8_to_f16x8(vcur.x[j][0], vcur.x[j][1]);
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i)
+                            o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                vf, __builtin_bit_cast(f16x8, pf[i]), o[i][db], 0, 0, 0);
+                    } else {
+                        const bf16x8 vf = __builtin_bit_cast(bf16x8, vcur.x[j]);
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i) {
+                            o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                vf, __builtin_bit_cast(bf16x8, pf[i]), o[i][db], 0, 0, 0);
+                            o[i][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                vf, __builtin_bit_cast(bf16x8, pl[i]), o[i][db], 0, 0, 0);
+                        }
+                    }
+                }
+                vcur = vnxt;
             }
         };
 
