@@ -48,6 +48,7 @@ struct PagedAttentionStep {
     uint32_t max_visible_tokens = 0;
     float* partials = nullptr;                          // split-K workspace (device)
     uint64_t partial_bytes = 0;
+    bool concurrent_decode = true;                      // decode launches beside the tiles
 };
 
 struct DecodeSplit {
@@ -66,6 +67,8 @@ struct PlannedKernel {
     uint32_t tiles_per_group = 1; // Tile: consecutive tiles per workgroup (rows == 0 pads)
     uint32_t req_first = 0;       // Tile with splits > 1: combine ranges
     uint32_t req_count = 0;
+    uint32_t side = 0;            // 1: runs on the side stream, concurrently with the tiles
+    uint64_t partial_offset = 0;  // floats into the split-K workspace this launch uses
 };
 
 struct PlannedTile {

@@ -82,7 +82,8 @@ class StepRequest(C.Structure):
 
 
 class PlannedKernel(C.Structure):
-    _fields_ = [(n, C.c_uint32) for n in ("kind", "row_begin", "rows", "splits", "pages_per_split")]
+    _fields_ = [(n, C.c_uint32) for n in ("kind", "row_begin", "rows", "splits", "pages_per_split",
+                                          "side")]
 
 
 class StepPlan(C.Structure):

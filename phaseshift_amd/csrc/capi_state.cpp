@@ -222,6 +222,7 @@ int psk_build_step(const psk_paged_attention_args* common, uint32_t kv_dtype, co
             plan_out->kernels[i].rows = plan.kernels[i].rows;
             plan_out->kernels[i].splits = plan.kernels[i].splits;
             plan_out->kernels[i].pages_per_split = plan.kernels[i].pages_per_split;
+            plan_out->kernels[i].side = plan.kernels[i].side;
         }
     }
     return hipSuccess;

@@ -10,6 +10,8 @@
 #include <phaseshift_kv/dispatch.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <functional>
 #include <vector>
 
@@ -335,8 +337,76 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         Status st = push(k);
         if (!st.ok()) return st;
     }
+    // Decode launches of a step that also has tile launches run on a side
+    // stream, concurrently with the tiles: the HBM-bound decode workgroups
+    // take the CUs the compute-bound tile launch leaves idle in its tail.
+    // Each side gets its own part of the split-K workspace; when both parts
+    // do not fit, the launches stay in order on one stream.
+    uint64_t need_tile = 0, need_dec = 0;
+    bool any_tile = false, any_dec = false;
+    const uint32_t qpk = c.kv_heads ? c.q_heads / c.kv_heads : 0u;
+    for (uint32_t i = 0; i < plan.count; ++i) {
+        const PlannedKernel& k = plan.kernels[i];
+        const uint64_t need = k.splits > 1 ? (uint64_t)k.rows * c.kv_heads * k.splits * qpk *
+                                                 (2u + ::ps::kernel::kPagedAttentionHeadLimit) * 4u
+                                           : 0u;
+        if (k.kind == PlannedKernel::Kind::Tile) {
+            any_tile = true;
+            need_tile = std::max(need_tile, need);
+        } else {
+            any_dec = true;
+            need_dec = std::max(need_dec, need);
+        }
+    }
+    const uint64_t side_at = (need_tile + 255u) & ~uint64_t{255};
+    if (step.concurrent_decode && any_tile && any_dec &&
+        (need_dec == 0 || side_at + need_dec <= pbytes)) {
+        for (uint32_t i = 0; i < plan.count; ++i) {
+            PlannedKernel& k = plan.kernels[i];
+            if (k.kind != PlannedKernel::Kind::Decode) continue;
+            k.side = 1;
+            k.partial_offset = side_at / 4u;
+        }
+    }
     return Status::make_ok();
 }
+
+namespace {
+
+// Side stream and fork/join events per (device, caller stream), created on
+// first use and kept for the life of the process. Default priority, no
+// blocking with the null stream.
+struct SideStream {
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr;
+    hipEvent_t join = nullptr;
+};
+
+SideStream* side_stream_for(hipStream_t main) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, SideStream> table;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = table.find({dev, main});
+    if (it != table.end()) return &it->second;
+    SideStream s;
+    if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        if (s.join) (void)hipEventDestroy(s.join);
+        if (s.fork) (void)hipEventDestroy(s.fork);
+        if (s.stream) (void)hipStreamDestroy(s.stream);
+        return nullptr;   // the step then runs in order on `main`
+    }
+    return &table.emplace(std::make_pair(dev, main), s).first->second;
+}
+
+}  // namespace
 
 hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const PagedAttentionPlan& plan,
                                        hipStream_t stream) {
@@ -349,8 +419,8 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
     const auto* v8 = static_cast<const ::ps::qwen35::fp8e4m3_storage_t*>(step.v_pool);
     const auto* k16 = static_cast<const bf16_t*>(step.k_pool);
     const auto* v16 = static_cast<const bf16_t*>(step.v_pool);
-    for (uint32_t i = 0; i < plan.count; ++i) {
-        const PlannedKernel& k = plan.kernels[i];
+    auto run = [&](const PlannedKernel& k, hipStream_t stream) -> hipError_t {
+        float* const parts = step.partials ? step.partials + k.partial_offset : nullptr;
         const PagedAttentionCommonArgs a = region_args(step.common, k.row_begin, k.rows);
         hipError_t e = hipSuccess;
         if (psq) {
@@ -363,9 +433,9 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
             const uint32_t bph = a.head_dim / 32u;
             if (k.splits > 1) {
                 e = static_cast<hipError_t>(psk_attention_paged_psq_split_ex(
-                    ca, kvd, kc, vc, ks, vs, bph, step.partials, k.splits, k.pages_per_split, stream));
+                    ca, kvd, kc, vc, ks, vs, bph, parts, k.splits, k.pages_per_split, stream));
                 if (e == hipSuccess)
-                    e = launch_attention_paged_split_reduce_ex(a, step.partials, k.splits,
+                    e = launch_attention_paged_split_reduce_ex(a, parts, k.splits,
                                                                k.pages_per_split, stream);
             } else {
                 e = static_cast<hipError_t>(psk_attention_paged_psq(ca, kvd, kc, vc, ks, vs, bph, stream));
@@ -382,7 +452,7 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
             if (psk::paged_tiles_supported(*ca, kvd, step.k_pool, step.v_pool)) {
                 e = psk::launch_paged_tiles(*ca, kvd, step.k_pool, step.v_pool, ksf,
                                             vsf, tb.data(), tr.data(), k.tile_count,
-                                            k.tiles_per_group, step.partials, k.splits,
+                                            k.tiles_per_group, parts, k.splits,
                                             k.pages_per_split, stream);
                 for (uint32_t q = 0; e == hipSuccess && k.splits > 1 && q < k.req_count; ++q) {
                     const StepRequest& r = plan.combine[k.req_first + q];
@@ -392,7 +462,7 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
                     const uint64_t row_floats = (uint64_t)a.kv_heads * k.splits *
                                                 (a.q_heads / a.kv_heads) * (2u + kPagedAttentionHeadLimit);
                     e = launch_attention_paged_split_reduce_ex(
-                        ra, step.partials + (uint64_t)(r.row_begin - k.row_begin) * row_floats,
+                        ra, parts + (uint64_t)(r.row_begin - k.row_begin) * row_floats,
                         k.splits, k.pages_per_split, stream);
                 }
             } else {
@@ -405,21 +475,44 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
                 }
             }
         } else if (k.splits > 1) {
-            e = fp8 ? launch_attention_paged_fp8_e4m3_split(a, k8, v8, ksf, vsf, step.partials,
+            e = fp8 ? launch_attention_paged_fp8_e4m3_split(a, k8, v8, ksf, vsf, parts,
                                                             k.splits, k.pages_per_split, stream)
                     : static_cast<hipError_t>(psk_attention_paged_bf16_split_ex(
                           reinterpret_cast<const psk_paged_attention_args*>(&a), k16, v16,
-                          step.partials, k.splits, k.pages_per_split, stream));
+                          parts, k.splits, k.pages_per_split, stream));
             if (e == hipSuccess)
-                e = launch_attention_paged_split_reduce_ex(a, step.partials, k.splits,
+                e = launch_attention_paged_split_reduce_ex(a, parts, k.splits,
                                                            k.pages_per_split, stream);
         } else {
             e = fp8 ? launch_attention_paged_fp8_e4m3(a, k8, v8, ksf, vsf, stream)
                     : launch_attention_paged_bf16(a, k16, v16, stream);
         }
-        if (e != hipSuccess) return e;
+        return e;
+    };
+    bool fork = false;
+    for (uint32_t i = 0; i < plan.count; ++i) fork = fork || plan.kernels[i].side != 0;
+    SideStream* side = fork ? side_stream_for(stream) : nullptr;
+    if (side == nullptr) {
+        for (uint32_t i = 0; i < plan.count; ++i) {
+            const hipError_t e = run(plan.kernels[i], stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
     }
-    return hipSuccess;
+    // fork: the side stream starts after the work before this step on
+    // `stream`; `stream` continues only after the side launches (join)
+    hipError_t e = hipEventRecord(side->fork, stream);
+    if (e != hipSuccess) return e;
+    e = hipStreamWaitEvent(side->stream, side->fork, 0);
+    if (e != hipSuccess) return e;
+    for (uint32_t i = 0; e == hipSuccess && i < plan.count; ++i)
+        if (plan.kernels[i].side) e = run(plan.kernels[i], side->stream);
+    for (uint32_t i = 0; e == hipSuccess && i < plan.count; ++i)
+        if (!plan.kernels[i].side) e = run(plan.kernels[i], stream);
+    // join even after an error, so a capture never ends with the side stream forked
+    const hipError_t j1 = hipEventRecord(side->join, side->stream);
+    const hipError_t j2 = j1 == hipSuccess ? hipStreamWaitEvent(stream, side->join, 0) : j1;
+    return e != hipSuccess ? e : j2;
 }
 
 }  // namespace ps::qwen35::runtime

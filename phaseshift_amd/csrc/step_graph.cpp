@@ -56,6 +56,9 @@ std::vector<uint8_t> plan_signature_bytes(const PagedAttentionStep& step, const 
         put(k, p.tile_first);
         put(k, p.tile_count);
         put(k, p.tiles_per_group);
+        put(k, p.side);
+        put(k, static_cast<uint32_t>(p.partial_offset));
+        put(k, static_cast<uint32_t>(p.partial_offset >> 32));
         put(k, p.req_first);
         put(k, p.req_count);
     }

@@ -127,3 +127,32 @@ def test_psq_choose_decode_split_and_unknown_dtype():
         assert sp > 1 and sp * pp >= 2048
     with pytest.raises(P.HipError):
         ops.choose_decode_split(64, 24, 4, 256, 16, False, [32768] * 64, 1 << 40, kv_dtype=2)
+
+
+def test_decode_beside_tiles_on_a_side_stream():
+    """Decode launches of a step with tile launches go to the side stream when
+    both split-K workspaces fit side by side; otherwise the step stays in order."""
+    reqs = ([(i, 1, 0) for i in range(48)] + [(48 + 16 * i, 16, 1) for i in range(8)] +
+            [(176 + 512 * i, 512, 2) for i in range(8)])
+    plan = state.plan_step(args(4272), P.KV_FP8, reqs, 16384, 256 << 20)
+    ks = plan.kernels[:plan.count]
+    assert [k.side for k in ks] == [1, 0, 0]
+    # decode-only steps never fork
+    plan = state.plan_step(args(64), P.KV_FP8, [(i, 1, 0) for i in range(64)], 32768, 256 << 20)
+    assert [k.side for k in plan.kernels[:plan.count]] == [0]
+    # for any workspace: when the decode forks, the tile and decode partials
+    # sit side by side inside it; when they would not, the step stays in order
+    forked = ordered = 0
+    for cap in [1 << 20, 4 << 20, 8 << 20, 16 << 20, 24 << 20, 32 << 20, 64 << 20]:
+        plan = state.plan_step(args(4272), P.KV_FP8, reqs, 16384, cap)
+        ks = plan.kernels[:plan.count]
+        need = [k.rows * 4 * k.splits * 6 * 258 * 4 if k.splits > 1 else 0 for k in ks]
+        tile = max(n for k, n in zip(ks, need) if k.kind == 1)
+        dec = max(n for k, n in zip(ks, need) if k.kind == 0)
+        if ks[0].side:
+            forked += 1
+            assert dec == 0 or ((tile + 255) // 256) * 256 + dec <= cap
+        else:
+            ordered += 1
+            assert ((tile + 255) // 256) * 256 + dec > cap
+    assert forked and ordered
