@@ -28,6 +28,8 @@ inline constexpr uint32_t kMaxPlannedKernels = 16u;
 // K/V is then read once per block instead of once per draft row.
 inline constexpr uint32_t kVerifyTileMinRows = 8u;
 inline constexpr uint32_t kTileRowsPerTile = 16u;
+// Decode launches run beside the tile launches of a step from this many tile rows.
+inline constexpr uint64_t kForkMinTileRows = 1024u;
 
 struct StepRequest {
     uint32_t row_begin = 0;

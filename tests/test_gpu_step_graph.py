@@ -112,3 +112,47 @@ def test_lru_capacity(dev):
     assert how == 0                   # evicted: seen again from scratch
     torch.cuda.synchronize()
     assert torch.equal(outs[1], outs[2])
+
+
+def test_forked_step_replays_equal_eager(dev):
+    """A step with >= 1024 tile rows runs its decode launch on a side stream
+    (fork and join by events); the captured graph keeps the fork, and every
+    replay equals the eager step."""
+    rng = np.random.default_rng(17)
+    ctx = [int(x) for x in rng.integers(2200, 3000, 6)]
+    lens = ctx + [1024 + 700]
+    lay = paged_layout(rng, lens, PT, H, D, spare_pages=2)
+    g = ops.PoolGeometry(1, lay.num_pages, PT, H, D)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(17)
+    kp = torch.randint(0, 126, (g.pool_elems,), generator=gen, device=dev).to(torch.uint8)
+    vp = torch.randint(0, 126, (g.pool_elems,), generator=gen, device=dev).to(torch.uint8)
+    ks = torch.rand(g.scale_elems, generator=gen, device=dev) * 0.02 + 1e-3
+    vs = torch.rand(g.scale_elems, generator=gen, device=dev) * 0.02 + 1e-3
+    slots = np.array(list(range(6)) + [6] * 1024, np.uint32)
+    pos = np.array([c - 1 for c in ctx] + list(range(700, 1724)), np.uint32)
+    reqs = [(i, 1, 0, ctx[i]) for i in range(6)] + [(6, 1024, 2, 1724)]
+    rows = len(slots)
+    q = torch.randn((rows, QH * D), generator=gen, device=dev).to(torch.bfloat16)
+    nbytes = 64 << 20
+    part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    part_e = torch.empty_like(part)
+    out_g = torch.full((rows, QH * D), 7.0, device=dev)
+    out_e = torch.full((rows, QH * D), 7.0, device=dev)
+    s, p_, bt = to_dev(slots), to_dev(pos), to_dev(lay.block_tables)
+    a_g = ops.attention_args(g, 0, q, out_g, s, p_, bt, QH)
+    a_e = ops.attention_args(g, 0, q, out_e, s, p_, bt, QH)
+    cache = state.StepGraphCache(2)
+    hows = []
+    for it in range(4):
+        if it:
+            q.copy_(torch.randn(q.shape, generator=gen, device=dev).to(q.dtype))
+            _ = (torch.randn(1 << 20, device=dev) * 2).sum()
+        plan, how = cache.step(a_g, P.KV_FP8, reqs, 3000, nbytes, part, kp, vp, ks, vs)
+        hows.append(how)
+        state.plan_step(a_e, P.KV_FP8, reqs, 3000, nbytes, part_e, kp, vp, ks, vs, launch=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), (it, how)
+        assert not torch.any(out_g == 7.0)
+    assert hows == [0, 1, 2, 2]
+    assert [k.side for k in plan.kernels[:plan.count]] == [1, 0]

@@ -137,7 +137,10 @@ def test_decode_beside_tiles_on_a_side_stream():
     plan = state.plan_step(args(4272), P.KV_FP8, reqs, 16384, 256 << 20)
     ks = plan.kernels[:plan.count]
     assert [k.side for k in ks] == [1, 0, 0]
-    # decode-only steps never fork
+    # small tile steps (under 1024 tile rows) and decode-only steps never fork
+    small = [(i, 1, 0) for i in range(8)] + [(8, 16, 1), (24, 128, 2)]
+    plan = state.plan_step(args(152), P.KV_FP8, small, 16384, 256 << 20)
+    assert [k.side for k in plan.kernels[:plan.count]] == [0, 0, 0]
     plan = state.plan_step(args(64), P.KV_FP8, [(i, 1, 0) for i in range(64)], 32768, 256 << 20)
     assert [k.side for k in plan.kernels[:plan.count]] == [0]
     # for any workspace: when the decode forks, the tile and decode partials
