@@ -82,3 +82,38 @@ def test_grouped_prefill_d128(dev):
     torch.cuda.synchronize()
     want = oracle_out(lay, 12, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
     assert np.max(np.abs(out.cpu().numpy() - want)) < TOL[True]
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_grouped_and_verify_tiles_page24(dev, fp8):
+    """Page size 24 (not a multiple of 16): a 16-token half can straddle two
+    pages, so every lane looks up its own page in both the grouped (prefill)
+    and the six-wave (verify) tile kernels."""
+    rng = np.random.default_rng(24 + fp8)
+    spec = [(900, 200, 2), (1300, 16, 1), (40, 1, 0), (500, 136, 2)]
+    lens = [p + n for p, n, _ in spec]
+    P_ = 24
+    lay = paged_layout(rng, lens, P_, 4, 256, spare_pages=2)
+    kp, vp, ks, vs = make_pools(lay, fp8, 77 + fp8, dev)
+    slots, pos, reqs, row = [], [], [], 0
+    for s, (p, n, cls) in enumerate(spec):
+        slots += [s] * n
+        pos += list(range(p, p + n))
+        reqs.append((row, n, cls, p + n))
+        row += n
+    slots, pos = np.array(slots, np.uint32), np.array(pos, np.uint32)
+    q = bf16_normal(rng, (row, 24 * 256))
+    g = ops.PoolGeometry(1, lay.num_pages, P_, 4, 256)
+    out = torch.full((row, 24 * 256), 7.0, dtype=torch.float32, device=dev)
+    a = ops.attention_args(g, 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                           to_dev(lay.block_tables), 24)
+    part = torch.empty((64 << 20) // 4, dtype=torch.float32, device=dev)
+    plan = state.plan_step(a, P.KV_FP8 if fp8 else P.KV_BF16, reqs, max(lens), 64 << 20,
+                           partials_ptr=part, k_pool=kp, v_pool=vp, k_scale=ks, v_scale=vs,
+                           launch=True)
+    torch.cuda.synchronize()
+    assert [k.kind for k in plan.kernels[:plan.count]].count(1) == 2   # verify + prefill tiles
+    want = oracle_out(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
+    got = out.cpu().numpy()
+    assert not np.any(got == 7.0)
+    assert np.max(np.abs(got - want)) < TOL[fp8]
