@@ -122,8 +122,11 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
                              (uint64_t)row[u] * a.k_row_stride + head[u] * D + e;
         const uint16_t* vs = static_cast<const uint16_t*>(a.v_input) +
                              (uint64_t)row[u] * a.v_row_stride + head[u] * D + e;
-        kw[u] = *reinterpret_cast<const u32x4*>(ks);
-        vw[u] = *reinterpret_cast<const u32x4*>(vs);
+        // input rows are read once: non-temporal loads (and stores of the
+        // codes below) measured ~3.5% faster at 2^16 rows than the default
+        // policy (the PSQ kernel's 64 B-per-lane blocks measured slower with it)
+        kw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ks));
+        vw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vs));
     }
     uint32_t page[kUnroll], off[kUnroll];
     bool valid[kUnroll];
@@ -180,8 +183,8 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
             if (has_chunk) {
                 const u32x2 kc = encode8(kx, k_scale, 1.0f / k_scale, fast_div_ok(k_scale));
                 const u32x2 vc = encode8(vx, v_scale, 1.0f / v_scale, fast_div_ok(v_scale));
-                *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(p.k_pool) + dst) = kc;
-                *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(p.v_pool) + dst) = vc;
+                __builtin_nontemporal_store(kc, reinterpret_cast<u32x2*>(static_cast<uint8_t*>(p.k_pool) + dst));
+                __builtin_nontemporal_store(vc, reinterpret_cast<u32x2*>(static_cast<uint8_t*>(p.v_pool) + dst));
             }
         }
     }
