@@ -67,6 +67,27 @@ __host__ __device__ inline void page_bytes(const psk_page_copy_args& a, uint64_t
 
 // grid.x = page pairs * layers * 4 tensors (K, V, K-scale, V-scale); every
 // block copies one page body (or one page's scale rows) with 16 B accesses.
+// Copies `bytes` (a multiple of 16) with the workgroup's 256 threads: each
+// thread issues the loads of a 16 KB round (4 x 16 B per thread) before
+// its stores, so several loads are in flight per thread.
+__device__ __forceinline__ void copy16_block(uint8_t* d, const uint8_t* s, uint64_t bytes) {
+    constexpr int U = 4;
+    constexpr uint64_t kRound = 256u * 16u * U;
+    for (uint64_t o0 = (uint64_t)threadIdx.x * 16u; o0 < bytes; o0 += kRound) {
+        u32x4 v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const uint64_t o = o0 + (uint64_t)j * 256u * 16u;
+            if (o < bytes) v[j] = *reinterpret_cast<const u32x4*>(s + o);
+        }
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const uint64_t o = o0 + (uint64_t)j * 256u * 16u;
+            if (o < bytes) *reinterpret_cast<u32x4*>(d + o) = v[j];
+        }
+    }
+}
+
 __device__ __forceinline__ void copy_one(const psk_page_copy_args& a, uint32_t vec16,
                                          uint32_t dst_page, uint32_t src_page, uint32_t layer,
                                          uint32_t tensor) {
@@ -91,8 +112,7 @@ __device__ __forceinline__ void copy_one(const psk_page_copy_args& a, uint32_t v
         d = reinterpret_cast<uint8_t*>(tensor == 2u ? a.dst_k_scale : a.dst_v_scale) + dof;
     }
     if (vec16 && (bytes % 16u) == 0u) {
-        for (uint64_t o = (uint64_t)threadIdx.x * 16u; o < bytes; o += 256u * 16u)
-            *reinterpret_cast<u32x4*>(d + o) = *reinterpret_cast<const u32x4*>(s + o);
+        copy16_block(d, s, bytes);
     } else {
         for (uint64_t o = threadIdx.x; o < bytes; o += 256u) d[o] = s[o];
     }
@@ -159,8 +179,7 @@ __global__ __launch_bounds__(256) void copy_plan_kernel(const psk_page_copy_args
     uint8_t* dst = static_cast<uint8_t*>(sg.dst) + off;
     const bool al = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | n) & 15u) == 0u;
     if (al) {
-        for (uint64_t o = (uint64_t)threadIdx.x * 16u; o < n; o += 256u * 16u)
-            *reinterpret_cast<u32x4*>(dst + o) = *reinterpret_cast<const u32x4*>(src + o);
+        copy16_block(dst, src, n);
     } else {
         for (uint64_t o = threadIdx.x; o < n; o += 256u) dst[o] = src[o];
     }
