@@ -28,7 +28,7 @@ inline constexpr uint32_t kMaxPlannedKernels = 16u;
 // K/V is then read once per block instead of once per draft row.
 inline constexpr uint32_t kVerifyTileMinRows = 8u;
 inline constexpr uint32_t kTileRowsPerTile = 16u;
-// Decode launches run beside the tile launches of a step from this many tile rows.
+// A step's other launches run beside a tile launch of at least this many rows.
 inline constexpr uint64_t kForkMinTileRows = 1024u;
 
 struct StepRequest {
@@ -50,7 +50,7 @@ struct PagedAttentionStep {
     uint32_t max_visible_tokens = 0;
     float* partials = nullptr;                          // split-K workspace (device)
     uint64_t partial_bytes = 0;
-    bool concurrent_decode = true;                      // decode launches beside the tiles
+    bool concurrent_decode = true;                      // other launches beside the largest tile launch
 };
 
 struct DecodeSplit {
@@ -69,7 +69,7 @@ struct PlannedKernel {
     uint32_t tiles_per_group = 1; // Tile: consecutive tiles per workgroup (rows == 0 pads)
     uint32_t req_first = 0;       // Tile with splits > 1: combine ranges
     uint32_t req_count = 0;
-    uint32_t side = 0;            // 1: runs on the side stream, concurrently with the tiles
+    uint32_t side = 0;            // 1: runs on the side stream, beside the step's largest tile launch
     uint64_t partial_offset = 0;  // floats into the split-K workspace this launch uses
 };
 

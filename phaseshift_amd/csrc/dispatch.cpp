@@ -337,38 +337,36 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         Status st = push(k);
         if (!st.ok()) return st;
     }
-    // Decode launches of a step that also has tile launches run on a side
-    // stream, concurrently with the tiles: the HBM-bound decode workgroups
+    // In a step with a large tile launch (>= kForkMinTileRows rows), every
+    // other launch (decode, smaller tile launches) runs on a side stream,
+    // in order there and concurrently with the large one: their workgroups
     // take the CUs the compute-bound tile launch leaves idle in its tail.
-    // Each side gets its own part of the split-K workspace; when both parts
-    // do not fit, the launches stay in order on one stream.
-    uint64_t need_tile = 0, need_dec = 0, tile_rows = 0;
-    bool any_tile = false, any_dec = false;
+    // The large launch keeps the start of the split-K workspace, the side
+    // launches share the part after it (they run one after another); when
+    // both parts do not fit, the step stays in order on one stream.
     const uint32_t qpk = c.kv_heads ? c.q_heads / c.kv_heads : 0u;
-    for (uint32_t i = 0; i < plan.count; ++i) {
-        const PlannedKernel& k = plan.kernels[i];
-        const uint64_t need = k.splits > 1 ? (uint64_t)k.rows * c.kv_heads * k.splits * qpk *
-                                                 (2u + ::ps::kernel::kPagedAttentionHeadLimit) * 4u
-                                           : 0u;
-        if (k.kind == PlannedKernel::Kind::Tile) {
-            any_tile = true;
-            tile_rows += k.rows;
-            need_tile = std::max(need_tile, need);
-        } else {
-            any_dec = true;
-            need_dec = std::max(need_dec, need);
-        }
-    }
-    const uint64_t side_at = (need_tile + 255u) & ~uint64_t{255};
-    // small steps keep one stream: there the fork and join cost more than
-    // the overlap gains (measured ~20 us on a 168-row tile step under graph replay)
-    if (step.concurrent_decode && any_tile && any_dec && tile_rows >= kForkMinTileRows &&
-        (need_dec == 0 || side_at + need_dec <= pbytes)) {
-        for (uint32_t i = 0; i < plan.count; ++i) {
-            PlannedKernel& k = plan.kernels[i];
-            if (k.kind != PlannedKernel::Kind::Decode) continue;
-            k.side = 1;
-            k.partial_offset = side_at / 4u;
+    auto need_of = [&](const PlannedKernel& k) -> uint64_t {
+        return k.splits > 1 ? (uint64_t)k.rows * c.kv_heads * k.splits * qpk *
+                                  (2u + ::ps::kernel::kPagedAttentionHeadLimit) * 4u
+                            : 0u;
+    };
+    int main_k = -1;
+    for (uint32_t i = 0; i < plan.count; ++i)
+        if (plan.kernels[i].kind == PlannedKernel::Kind::Tile &&
+            (main_k < 0 || plan.kernels[i].rows > plan.kernels[main_k].rows))
+            main_k = (int)i;
+    if (step.concurrent_decode && main_k >= 0 && plan.count > 1 &&
+        plan.kernels[main_k].rows >= kForkMinTileRows) {
+        uint64_t need_side = 0;
+        for (uint32_t i = 0; i < plan.count; ++i)
+            if ((int)i != main_k) need_side = std::max(need_side, need_of(plan.kernels[i]));
+        const uint64_t side_at = (need_of(plan.kernels[main_k]) + 255u) & ~uint64_t{255};
+        if (need_side == 0 || side_at + need_side <= pbytes) {
+            for (uint32_t i = 0; i < plan.count; ++i) {
+                if ((int)i == main_k) continue;
+                plan.kernels[i].side = 1;
+                plan.kernels[i].partial_offset = side_at / 4u;
+            }
         }
     }
     return Status::make_ok();

@@ -92,6 +92,7 @@ def append_args(geom: PoolGeometry, layer: int, k_in, v_in, slots, positions, bl
     a.kv_heads, a.head_dim = geom.kv_heads, geom.head_dim
     a.elems_per_token, a.elems_per_page = geom.elems_per_token, geom.elems_per_page
     a.elems_per_layer = geom.elems_per_layer
+    a._tensors = (k_in, v_in, slots, positions, block_tables)   # see attention_args
     return a
 
 
@@ -129,6 +130,10 @@ def attention_args(geom: PoolGeometry, layer: int, q, out, slots, positions, blo
     a.elems_per_token, a.elems_per_page = geom.elems_per_token, geom.elems_per_page
     a.elems_per_layer = geom.elems_per_layer
     a.scale = 1.0 / math.sqrt(geom.head_dim) if scale is None else scale
+    # the struct holds raw device pointers: keep the tensors alive with it, so
+    # a temporary passed here is not freed and its memory handed to another
+    # allocation while launches still read it
+    a._tensors = (q, out, slots, positions, block_tables)
     return a
 
 

@@ -61,7 +61,12 @@ def test_grouped_prefill_vs_oracle(dev, fp8, qh, kvh, split):
     assert (tile.splits > 1) == split
     assert not np.any(got == 7.0)
     err = np.max(np.abs(got - want), axis=1)
-    assert np.max(err) < TOL[fp8], (int(np.argmax(err)), float(np.max(err)))
+    nan_rows = np.nonzero(np.isnan(got).any(axis=1))[0]
+    nan_heads = sorted(set(np.nonzero(np.isnan(got.reshape(got.shape[0], qh, -1)).any(axis=2))[1].tolist()))
+    assert np.max(err) < TOL[fp8], (int(np.argmax(err)), float(np.max(err)), len(nan_rows),
+                                    nan_rows[:8].tolist(), nan_heads,
+                                    [(k.kind, k.row_begin, k.rows, k.splits, k.pages_per_split, k.side)
+                                     for k in plan.kernels[:plan.count]])
 
 
 def test_grouped_prefill_d128(dev):

@@ -129,33 +129,65 @@ def test_psq_choose_decode_split_and_unknown_dtype():
         ops.choose_decode_split(64, 24, 4, 256, 16, False, [32768] * 64, 1 << 40, kv_dtype=2)
 
 
-def test_decode_beside_tiles_on_a_side_stream():
-    """Decode launches of a step with tile launches go to the side stream when
-    both split-K workspaces fit side by side; otherwise the step stays in order."""
+def test_other_launches_beside_the_largest_tile_launch():
+    """In a step with a tile launch of >= 1024 rows, every other launch (decode,
+    the verify tile launch) goes to the side stream when the split-K
+    workspace holds the large launch's partials and, after them, the largest
+    side launch's; otherwise the step stays in order."""
     reqs = ([(i, 1, 0) for i in range(48)] + [(48 + 16 * i, 16, 1) for i in range(8)] +
             [(176 + 512 * i, 512, 2) for i in range(8)])
     plan = state.plan_step(args(4272), P.KV_FP8, reqs, 16384, 256 << 20)
     ks = plan.kernels[:plan.count]
-    assert [k.side for k in ks] == [1, 0, 0]
-    # small tile steps (under 1024 tile rows) and decode-only steps never fork
+    assert [(k.kind, k.side) for k in ks] == [(0, 1), (1, 1), (1, 0)]
+    # small tile steps (largest tile launch under 1024 rows) and decode-only steps never fork
     small = [(i, 1, 0) for i in range(8)] + [(8, 16, 1), (24, 128, 2)]
     plan = state.plan_step(args(152), P.KV_FP8, small, 16384, 256 << 20)
     assert [k.side for k in plan.kernels[:plan.count]] == [0, 0, 0]
     plan = state.plan_step(args(64), P.KV_FP8, [(i, 1, 0) for i in range(64)], 32768, 256 << 20)
     assert [k.side for k in plan.kernels[:plan.count]] == [0]
-    # for any workspace: when the decode forks, the tile and decode partials
-    # sit side by side inside it; when they would not, the step stays in order
+    # for any workspace: side launches sit after the large launch's partials
+    # (one 1024-row prefill chunk beside 48 decode rows: the chunk splits too)
+    reqs = [(i, 1, 0) for i in range(48)] + [(48, 1024, 2)]
     forked = ordered = 0
-    for cap in [1 << 20, 4 << 20, 8 << 20, 16 << 20, 24 << 20, 32 << 20, 64 << 20]:
-        plan = state.plan_step(args(4272), P.KV_FP8, reqs, 16384, cap)
+    # (caps around 76 MB hold the chunk's 3-split partials but not the decode's beside them)
+    for cap in [1 << 20, 16 << 20, 64 << 20, 256 << 20] + [(70 + 2 * i) << 20 for i in range(8)]:
+        plan = state.plan_step(args(1072), P.KV_FP8, reqs, 16384, cap)
         ks = plan.kernels[:plan.count]
         need = [k.rows * 4 * k.splits * 6 * 258 * 4 if k.splits > 1 else 0 for k in ks]
-        tile = max(n for k, n in zip(ks, need) if k.kind == 1)
-        dec = max(n for k, n in zip(ks, need) if k.kind == 0)
+        main = max(range(len(ks)), key=lambda i: ks[i].rows if ks[i].kind == 1 else -1)
+        side = max(n for i, n in enumerate(need) if i != main)
+        at = ((need[main] + 255) // 256) * 256
         if ks[0].side:
             forked += 1
-            assert dec == 0 or ((tile + 255) // 256) * 256 + dec <= cap
+            assert all(k.side for i, k in enumerate(ks) if i != main) and not ks[main].side
+            assert side == 0 or at + side <= cap
         else:
             ordered += 1
-            assert ((tile + 255) // 256) * 256 + dec > cap
+            assert not any(k.side for k in ks)
+            assert at + side > cap
     assert forked and ordered
+
+
+def test_args_keep_their_tensors_alive():
+    """The argument structs hold raw device pointers; they keep the tensors
+    they point into alive (a temporary passed in must not be freed and its
+    memory reused while the struct is still launched)."""
+    import gc
+    import weakref
+    import torch
+    from phaseshift_amd import ops
+    g = ops.PoolGeometry(1, 8, 16, 4, 64)
+    q = torch.zeros((3, 8 * 64), dtype=torch.bfloat16)
+    ref = weakref.ref(q)
+    a = ops.attention_args(g, 0, q, torch.zeros((3, 8 * 64)), torch.zeros(3, dtype=torch.int32),
+                           torch.zeros(3, dtype=torch.int32), torch.zeros((2, 4), dtype=torch.int32), 8)
+    del q
+    gc.collect()
+    assert ref() is not None and a.q == ref().data_ptr()
+    k = torch.zeros((3, 4 * 64), dtype=torch.bfloat16)
+    ref_k = weakref.ref(k)
+    b = ops.append_args(g, 0, k, torch.zeros_like(k), torch.zeros(3, dtype=torch.int32),
+                        torch.zeros(3, dtype=torch.int32), torch.zeros((2, 4), dtype=torch.int32))
+    del k
+    gc.collect()
+    assert ref_k() is not None and b.k_input == ref_k().data_ptr()
