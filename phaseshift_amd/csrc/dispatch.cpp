@@ -506,10 +506,12 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
     if (e != hipSuccess) return e;
     e = hipStreamWaitEvent(side->stream, side->fork, 0);
     if (e != hipSuccess) return e;
-    for (uint32_t i = 0; e == hipSuccess && i < plan.count; ++i)
-        if (plan.kernels[i].side) e = run(plan.kernels[i], side->stream);
+    // the large launch is enqueued first, so its workgroups take the CUs
+    // first and the side launches fill its tail
     for (uint32_t i = 0; e == hipSuccess && i < plan.count; ++i)
         if (!plan.kernels[i].side) e = run(plan.kernels[i], stream);
+    for (uint32_t i = 0; e == hipSuccess && i < plan.count; ++i)
+        if (plan.kernels[i].side) e = run(plan.kernels[i], side->stream);
     // join even after an error, so a capture never ends with the side stream forked
     const hipError_t j1 = hipEventRecord(side->join, side->stream);
     const hipError_t j2 = j1 == hipSuccess ? hipStreamWaitEvent(stream, side->join, 0) : j1;
