@@ -138,13 +138,20 @@ typedef __attribute__((address_space(1))) void global_void_t;
 // immediate offset would be added to both addresses; it is 0 here). `dst`
 // must be wave-uniform. The hardware counts these loads in vmcnt and writes
 // LDS asynchronously: the data may be read only after s_waitcnt vmcnt.
-template <int BYTES>
+// CPOL is the cache policy: kCpolStream (the `nt` bit) for bytes read once
+// in whole 128 B lines. On MI355X a stream of such 16 B DMAs reaches ~6.8 TB/s
+// against ~6.1 TB/s with the default policy; DMAs that read half lines
+// (16 rows x 64 B per instruction) are slower with `nt` (~5.9 TB/s), since the
+// two halves of a line are no longer served by one L2 fill.
+constexpr int kCpolDefault = 0;
+constexpr int kCpolStream = 2;
+template <int BYTES, int CPOL = kCpolDefault>
 __device__ __forceinline__ void load_lds(const void* src, uint8_t* dst) {
     static_assert(BYTES == 4 || BYTES == 16, "DMA width");
     if constexpr (BYTES == 16)
-        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 16, 0, CPOL);
     else
-        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 4, 0, 0);
+        __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)dst, 4, 0, CPOL);
 }
 
 // Waits until at most N vector-memory operations of this wave are

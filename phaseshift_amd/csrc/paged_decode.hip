@@ -256,6 +256,12 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     constexpr int KV_BYTES = H * HALF_STRIDE;               // K (or V) of one chunk
     constexpr int SC_BYTES = KVB == 1 ? H * 256 : 0;       // k (or v) scales of one chunk
     constexpr int STAGE = stage_bytes<FMT, D>();
+    // FP8: a 16-token half of K (V) sits in LDS as NL 1 KB blocks, block j =
+    // tokens 8(j&1)..+7 x bytes [128(j>>1), +128), token row r (of 8) at
+    // +128r, its 16 B column c (of 8) at +16(c ^ r): each DMA instruction
+    // reads whole 128 B lines and the column reads stay conflict-free.
+    // Other formats: block i = bytes [64i, +64) of 16 tokens, lane-major.
+    constexpr bool kLineLayout = FMT == kFmtFp8 && CB % 128 == 0;
     // PSQ: dwords of block scales per token head (2 bf16 each); the scales of
     // a 16-token half sit dword-major in LDS: dword w of token t at 64w + 4t
     constexpr int SW = D / 64;
@@ -342,6 +348,18 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     } else {
         tr_off = 16u * (4u * g + (n >> 2)) + 256u * ((n >> 1) & 1u) + 8u * (n & 1u);
     }
+    // kLineLayout (FP8): the same (token, bytes) at their line-layout places.
+    //   K word i (bytes [64i + 16g, +16) of token n): 2048*(i>>1) + (i odd ? k_line ^ 64 : k_line)
+    //   V block db (bytes [16db, +16) of the tr-read token, +8*(n&1)):
+    //     v_line + 2048*(db>>3) + (16*(token & 7) ^ 16*(db & 7))
+    uint32_t k_line = 0, v_line = 0, v_row16 = 0;
+    if constexpr (kLineLayout) {
+        k_line = 1024u * (n >> 3) + 128u * (n & 7u) + 16u * (g ^ (n & 7u));
+        const uint32_t j = n >> 1;
+        const uint32_t t = 4u * g + (j & 3u);   // token within its half
+        v_row16 = 16u * (t & 7u);
+        v_line = (j < 4u ? 0u : (uint32_t)HALF_STRIDE) + 1024u * (t >> 3) + 128u * (t & 7u) + 8u * (n & 1u);
+    }
 
     float m_run = -INFINITY;   // running max (log2 units), head n
     float l_run = 0.0f;        // partial softmax sum of this lane's tokens
@@ -383,13 +401,37 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                     kPsq ? si * CB
                          : (layer_base + (uint64_t)page * a.elems_per_page +
                             (uint64_t)off * a.elems_per_token + (uint64_t)kvh * D) * KVB;
-                const uint8_t* ks = p.k_pool + cbase + g * 16;
-                const uint8_t* vs = p.v_pool + cbase + g * 16;
+                if constexpr (kLineLayout) {
+                    // instruction j: tokens 8(j&1) + (lane>>3) of the half, 16 B
+                    // column 8(j>>1) + ((lane&7) ^ (lane>>3)); every 8 lanes read
+                    // one token's whole 128 B line (non-temporal: read once)
 #pragma unroll
-                for (int i = 0; i < NL; ++i) load_lds<16>(ks + i * 64, st + hf * HALF_STRIDE + i * 1024);
+                    for (int tg = 0; tg < 2; ++tg) {
+                        const uint32_t tau8 = min(c + (uint32_t)hf * 16u + 8u * tg + (lane >> 3), t_last);
+                        uint32_t page8 = win[tau8 / P - wp];
+                        const bool inv8 = page8 >= a.num_pages;
+                        bad |= inv8;
+                        page8 = inv8 ? 0u : page8;
+                        const uint64_t b8 = layer_base + (uint64_t)page8 * a.elems_per_page +
+                                            (uint64_t)(tau8 % P) * a.elems_per_token + (uint64_t)kvh * D +
+                                            16u * (((lane & 7u) ^ (lane >> 3)));
 #pragma unroll
-                for (int i = 0; i < NL; ++i)
-                    load_lds<16>(vs + i * 64, st + KV_BYTES + hf * HALF_STRIDE + i * 1024);
+                        for (int cb = 0; cb < NL / 2; ++cb) {
+                            const int j = 2 * cb + tg;
+                            load_lds<16, kCpolStream>(p.k_pool + b8 + 128 * cb, st + hf * HALF_STRIDE + j * 1024);
+                            load_lds<16, kCpolStream>(p.v_pool + b8 + 128 * cb,
+                                                      st + KV_BYTES + hf * HALF_STRIDE + j * 1024);
+                        }
+                    }
+                } else {
+                    const uint8_t* ks = p.k_pool + cbase + g * 16;
+                    const uint8_t* vs = p.v_pool + cbase + g * 16;
+#pragma unroll
+                    for (int i = 0; i < NL; ++i) load_lds<16>(ks + i * 64, st + hf * HALF_STRIDE + i * 1024);
+#pragma unroll
+                    for (int i = 0; i < NL; ++i)
+                        load_lds<16>(vs + i * 64, st + KV_BYTES + hf * HALF_STRIDE + i * 1024);
+                }
                 if constexpr (FMT == kFmtFp8) {
                     load_lds<4>(static_cast<const float*>(p.k_scale) + si, st + 2 * KV_BYTES + hf * 256);
                     load_lds<4>(static_cast<const float*>(p.v_scale) + si,
@@ -453,6 +495,12 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                         bf16x8 kf;
                         if constexpr (KVB == 2) {
                             kf = *reinterpret_cast<const bf16x8*>(kb + 1024 * s);
+                        } else if constexpr (kLineLayout) {
+                            // bytes [64i + 16g, +16) of token n, i = s >> 1
+                            const int i = s >> 1;
+                            const u32x4 w = *reinterpret_cast<const u32x4*>(
+                                st + hf * HALF_STRIDE + 2048 * (i >> 1) + ((i & 1) ? (k_line ^ 64u) : k_line));
+                            kf = (s & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
                         } else {
                             const u32x4 w = *reinterpret_cast<const u32x4*>(kb + 1024 * (s >> 1));
                             kf = (s & 1) ? fp8x8_to_bf16x8(w[2], w[3]) : fp8x8_to_bf16x8(w[0], w[1]);
@@ -557,7 +605,11 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                 const bf16x8 pfl = __builtin_bit_cast(bf16x8, pl);
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
-                    const i32x2 w = lds_read_tr8(vb + 256 * db);
+                    i32x2 w;
+                    if constexpr (kLineLayout)
+                        w = lds_read_tr8(st + KV_BYTES + v_line + 2048 * (db >> 3) + (v_row16 ^ (16u * (db & 7))));
+                    else
+                        w = lds_read_tr8(vb + 256 * db);
                     const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
                     o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfh, o[db], 0, 0, 0);
                     o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pfl, o[db], 0, 0, 0);
