@@ -37,8 +37,8 @@ APPEND_BYTES_PER_ROW_FP8 = 2 * 4 * 256 * 2 + 8 + 4 + 2 * 4 * 256 + 2 * 4 * 4   #
 BYTES_PER_TOKEN_PSQ = {4: 2 * 4 * (128 + 16) + 4 / 16, 8: 2 * 4 * (256 + 16) + 4 / 16}
 APPEND_BYTES_PER_ROW_PSQ = {f: 2 * 4 * 256 * 2 + 8 + 4 + BYTES_PER_TOKEN_PSQ[f] - 4 / 16 for f in (4, 8)}
 # HBM bytes per main-line decode launch measured with rocprofv3 --pmc on this
-# kernel (FETCH_SIZE 2,139,725 KiB x 2.0 calibration + WRITE_SIZE 6,208 KiB).
-DECODE_TRAFFIC_BYTES = 2139725 * 1024 * 2 + 6208 * 1024
+# kernel (FETCH_SIZE 2,131,849 KiB x 2.0 calibration + WRITE_SIZE 6,206 KiB).
+DECODE_TRAFFIC_BYTES = 2131849 * 1024 * 2 + 6206 * 1024
 # Untimed warm-up runs at least `--warmup` steps and at least this long, so the
 # GPU clocks have ramped before a timed loop starts.
 WARM_MIN_S = 0.2
