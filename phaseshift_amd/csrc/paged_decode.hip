@@ -256,12 +256,15 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     constexpr int KV_BYTES = H * HALF_STRIDE;               // K (or V) of one chunk
     constexpr int SC_BYTES = KVB == 1 ? H * 256 : 0;       // k (or v) scales of one chunk
     constexpr int STAGE = stage_bytes<FMT, D>();
-    // FP8: a 16-token half of K (V) sits in LDS as NL 1 KB blocks, block j =
-    // tokens 8(j&1)..+7 x bytes [128(j>>1), +128), token row r (of 8) at
-    // +128r, its 16 B column c (of 8) at +16(c ^ r): each DMA instruction
-    // reads whole 128 B lines and the column reads stay conflict-free.
-    // Other formats: block i = bytes [64i, +64) of 16 tokens, lane-major.
-    constexpr bool kLineLayout = FMT == kFmtFp8 && CB % 128 == 0;
+    // Head slices of a multiple of 128 B (kLineLayout): a 16-token half of K
+    // (V) sits in LDS as NL 1 KB blocks, block j = tokens 8(j&1)..+7 x bytes
+    // [128(j>>1), +128), token row r (of 8) at +128r, its 16 B column c (of 8)
+    // at +16(c ^ r): each DMA instruction reads whole 128 B lines and the
+    // column reads stay conflict-free. Otherwise block i = bytes [64i, +64)
+    // of 16 tokens, lane-major.
+    // PSQ4 keeps the lane-major layout: at 128 B per token slice the line
+    // layout measured slower for it (4.53 against 4.7 TB/s at b64/32k).
+    constexpr bool kLineLayout = CB % 128 == 0 && FMT != kFmtPsq4;
     // PSQ: dwords of block scales per token head (2 bf16 each); the scales of
     // a 16-token half sit dword-major in LDS: dword w of token t at 64w + 4t
     constexpr int SW = D / 64;
@@ -352,13 +355,32 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     //   K word i (bytes [64i + 16g, +16) of token n): 2048*(i>>1) + (i odd ? k_line ^ 64 : k_line)
     //   V block db (bytes [16db, +16) of the tr-read token, +8*(n&1)):
     //     v_line + 2048*(db>>3) + (16*(token & 7) ^ 16*(db & 7))
-    uint32_t k_line = 0, v_line = 0, v_row16 = 0;
+    //   BF16 V block db (tr16 token t = 4g + (n>>2), bytes 32db + 16((n>>1)&1) + 8(n&1)):
+    //     v_line + 2048*(db>>2) + (32*(db&3) ^ v_row16)
+    //   PSQ8 K (bytes 32s + 8g of token n): 2048*(s>>2) + k_line + (32*(s&3) ^ k_x)
+    //   PSQ4 K (bytes 16s + 4g of token n): k_line + (16*s ^ k_x)
+    uint32_t k_line = 0, k_x = 0, v_line = 0, v_row16 = 0;
     if constexpr (kLineLayout) {
-        k_line = 1024u * (n >> 3) + 128u * (n & 7u) + 16u * (g ^ (n & 7u));
-        const uint32_t j = n >> 1;
-        const uint32_t t = 4u * g + (j & 3u);   // token within its half
-        v_row16 = 16u * (t & 7u);
-        v_line = (j < 4u ? 0u : (uint32_t)HALF_STRIDE) + 1024u * (t >> 3) + 128u * (t & 7u) + 8u * (n & 1u);
+        const uint32_t r = n & 7u;
+        if constexpr (FMT == kFmtPsq8) {
+            k_line = 1024u * (n >> 3) + 128u * r + 8u * (g & 1u);
+            k_x = (16u * (g >> 1)) ^ (16u * r);
+        } else if constexpr (FMT == kFmtPsq4) {
+            k_line = 1024u * (n >> 3) + 128u * r + 4u * g;
+            k_x = 16u * r;
+        } else {
+            k_line = 1024u * (n >> 3) + 128u * r + 16u * (g ^ r);
+        }
+        if constexpr (KVB == 1) {
+            const uint32_t j = n >> 1;
+            const uint32_t t = 4u * g + (j & 3u);   // token within its half
+            v_row16 = 16u * (t & 7u);
+            v_line = (j < 4u ? 0u : (uint32_t)HALF_STRIDE) + 1024u * (t >> 3) + 128u * (t & 7u) + 8u * (n & 1u);
+        } else {
+            const uint32_t t = 4u * g + (n >> 2);
+            v_row16 = (16u * ((n >> 1) & 1u)) ^ (16u * (t & 7u));
+            v_line = 1024u * (t >> 3) + 128u * (t & 7u) + 8u * (n & 1u);
+        }
     }
 
     float m_run = -INFINITY;   // running max (log2 units), head n
@@ -412,9 +434,13 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                         const bool inv8 = page8 >= a.num_pages;
                         bad |= inv8;
                         page8 = inv8 ? 0u : page8;
-                        const uint64_t b8 = layer_base + (uint64_t)page8 * a.elems_per_page +
-                                            (uint64_t)(tau8 % P) * a.elems_per_token + (uint64_t)kvh * D +
-                                            16u * (((lane & 7u) ^ (lane >> 3)));
+                        const uint32_t off8 = tau8 % P;
+                        const uint64_t si8 = ((scale_layer + page8) * P + off8) * a.kv_heads + kvh;
+                        const uint64_t b8 =
+                            (kPsq ? si8 * CB
+                                  : (layer_base + (uint64_t)page8 * a.elems_per_page +
+                                     (uint64_t)off8 * a.elems_per_token + (uint64_t)kvh * D) * KVB) +
+                            16u * ((lane & 7u) ^ (lane >> 3));
 #pragma unroll
                         for (int cb = 0; cb < NL / 2; ++cb) {
                             const int j = 2 * cb + tg;
@@ -463,14 +489,19 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                         bf16x8 kf;
                         if constexpr (FMT == kFmtPsq8) {
                             // bytes 32s + 8g .. +8 of token n
-                            const u32x2 w = *reinterpret_cast<const u32x2*>(
-                                kb + 1024 * (s >> 1) + 16 * (16 * (2 * (s & 1) + (int)(g >> 1)) + (int)n) +
-                                8 * (int)(g & 1u));
+                            const u32x2 w = kLineLayout
+                                ? *reinterpret_cast<const u32x2*>(kb + 2048 * (s >> 2) + k_line +
+                                                                  ((32u * (s & 3)) ^ k_x))
+                                : *reinterpret_cast<const u32x2*>(
+                                      kb + 1024 * (s >> 1) + 16 * (16 * (2 * (s & 1) + (int)(g >> 1)) + (int)n) +
+                                      8 * (int)(g & 1u));
                             kf = fp8x8_to_bf16x8(w[0], w[1]);
                         } else {
                             // bytes 16s + 4g .. +4 of token n: dims 4g.. (low
                             // nibbles) and 16 + 4g.. (high nibbles) of block s
-                            const uint32_t x = *reinterpret_cast<const uint32_t*>(kb + 256 * s + 16 * n + 4 * g);
+                            const uint32_t x = kLineLayout
+                                ? *reinterpret_cast<const uint32_t*>(kb + k_line + ((16u * s) ^ k_x))
+                                : *reinterpret_cast<const uint32_t*>(kb + 256 * s + 16 * n + 4 * g);
                             const uint32_t lo = psq4_e4m3x4(x, false), hi = psq4_e4m3x4(x, true);
                             u32x4 r;
                             r[0] = fp8x2_to_bf16x2(lo, false);
@@ -493,7 +524,10 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
 #pragma unroll
                     for (int s = 0; s < NS; ++s) {
                         bf16x8 kf;
-                        if constexpr (KVB == 2) {
+                        if constexpr (KVB == 2 && kLineLayout) {
+                            kf = *reinterpret_cast<const bf16x8*>(st + hf * HALF_STRIDE + 2048 * (s >> 1) +
+                                                                 ((s & 1) ? (k_line ^ 64u) : k_line));
+                        } else if constexpr (KVB == 2) {
                             kf = *reinterpret_cast<const bf16x8*>(kb + 1024 * s);
                         } else if constexpr (kLineLayout) {
                             // bytes [64i + 16g, +16) of token n, i = s >> 1
@@ -579,14 +613,19 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                     if constexpr (FMT == kFmtPsq8) {
 #pragma unroll
                         for (int h = 0; h < 2; ++h) {
-                            const i32x2 w = lds_read_tr8(vb + 256 * (2 * b + h));
+                            const int db = 2 * b + h;
+                            const i32x2 w = kLineLayout
+                                ? lds_read_tr8(st + KV_BYTES + v_line + 2048 * (db >> 3) + (v_row16 ^ (16u * (db & 7))))
+                                : lds_read_tr8(vb + 256 * db);
                             const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
                             o[2 * b + h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[2 * b + h], 0, 0, 0);
                         }
                     } else {
                         // byte i of block b for 8 tokens: dim i (low nibble)
                         // and dim 16 + i (high nibble)
-                        const i32x2 w = lds_read_tr8(vb + 256 * b);
+                        const i32x2 w = kLineLayout
+                            ? lds_read_tr8(st + KV_BYTES + v_line + 2048 * (b >> 3) + (v_row16 ^ (16u * (b & 7))))
+                            : lds_read_tr8(vb + 256 * b);
                         const bf16x8 vlo = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)w[0], false),
                                                            psq4_e4m3x4((uint32_t)w[1], false));
                         const bf16x8 vhi = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)w[0], true),
@@ -622,7 +661,9 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                 const i16x4 pfl = __builtin_bit_cast(i16x4, pl);
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
-                    const i16x4 vf = lds_read_tr16(vb + 512 * db);
+                    const i16x4 vf = kLineLayout
+                        ? lds_read_tr16(st + KV_BYTES + v_line + 2048 * (db >> 2) + ((32u * (db & 3)) ^ v_row16))
+                        : lds_read_tr16(vb + 512 * db);
                     o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pfh, o[db], 0, 0, 0);
                     o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pfl, o[db], 0, 0, 0);
                 }
