@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <queue>
 #include <functional>
 #include <vector>
 
@@ -71,21 +72,51 @@ uint32_t device_cus() {
     return cus;
 }
 
-// Makespan of the decode kernel's units (dense, longest first, unit u on XCD
-// u mod 8) under greedy dispatch onto `slots` workgroup slots per XCD, in
-// pages of work; every unit also pays `c0` pages of start-up.
-double split_makespan(const std::vector<double>& units, uint32_t slots, double c0) {
+// Makespan (seconds) of the decode kernel's units (dense, longest first, unit
+// u on XCD u mod 8, given in bytes) under greedy dispatch onto `slots`
+// workgroup slots per XCD. Fluid model fitted on MI355X (FP8 hd256, 18 split
+// sizes of two workloads, 2.5% rms): each XCD streams at most `xcd_bw` B/s,
+// shared evenly by its streaming workgroups; one workgroup streams at most
+// `wg_bw` (1.5x its fair share, so a tail runs faster than the bulk); every
+// unit first spends `c0` seconds of start-up (unit scan, block-table window,
+// first-chunk latency, epilogue) without streaming. The XCDs are independent.
+double split_makespan(const std::vector<double>& units, uint32_t slots, double xcd_bw,
+                      double wg_bw, double c0) {
     double worst = 0.0;
-    std::vector<double> free_at;
+    using Q = std::priority_queue<std::pair<double, double>, std::vector<std::pair<double, double>>,
+                                  std::greater<std::pair<double, double>>>;
     for (uint32_t x = 0; x < kXcds; ++x) {
-        free_at.assign(slots, 0.0);
-        std::make_heap(free_at.begin(), free_at.end(), std::greater<double>());
-        for (size_t i = x; i < units.size(); i += kXcds) {
-            std::pop_heap(free_at.begin(), free_at.end(), std::greater<double>());
-            free_at.back() += units[i] + c0;
-            std::push_heap(free_at.begin(), free_at.end(), std::greater<double>());
+        // start-ups: (end time, bytes); streams: virtual progress at which
+        // they end (every streaming unit receives the same rate)
+        Q delays;
+        std::priority_queue<double, std::vector<double>, std::greater<double>> streams;
+        double t = 0.0, vp = 0.0;
+        size_t next = x;
+        auto fill = [&] {
+            while (delays.size() + streams.size() < slots && next < units.size()) {
+                delays.push({t + c0, units[next]});
+                next += kXcds;
+            }
+        };
+        fill();
+        while (!delays.empty() || !streams.empty()) {
+            const double rate =
+                streams.empty() ? 0.0 : std::min(wg_bw, xcd_bw / (double)streams.size());
+            const double ts = streams.empty() ? 1e30 : t + (streams.top() - vp) / rate;
+            const double td = delays.empty() ? 1e30 : delays.top().first;
+            if (td <= ts) {
+                vp += (td - t) * rate;
+                t = td;
+                streams.push(vp + delays.top().second);
+                delays.pop();
+            } else {
+                vp = streams.top();
+                t = ts;
+                streams.pop();
+                fill();
+            }
         }
-        for (double t : free_at) worst = std::max(worst, t);
+        worst = std::max(worst, t);
     }
     return worst;
 }
@@ -110,15 +141,20 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
     const uint32_t per_cu = std::max<uint32_t>(1u, (uint32_t)((160u * 1024u) / lds));
     const uint32_t slots = std::max<uint32_t>(1u, device_cus() / kXcds) * per_cu;
     const uint64_t total_slots = (uint64_t)slots * kXcds;
-    // Start-up of a workgroup (unit scan, block-table window, first chunk
-    // latency, epilogue), fitted on MI355X: ~8 pages of FP8 hd256 x 4 heads.
-    // K bytes of a (token, head) slice plus its scales, per page of 4 heads
-    const double slice = kv_dtype == PSK_KV_BF16        ? 2.0 * head_dim
-                         : kv_dtype == PSK_KV_FP8_E4M3  ? head_dim + 8.0
-                         : kv_dtype == PSK_KV_PSQ4_W32  ? head_dim / 2.0 + head_dim / 16.0
-                                                        : head_dim + head_dim / 16.0;
+    // K and V bytes of one (token, head) with their scales, per page of the
+    // 4 kv heads one workgroup streams; the fitted fluid model
+    // (split_makespan) runs in bytes
+    const double slice = kv_dtype == PSK_KV_BF16        ? 4.0 * head_dim
+                         : kv_dtype == PSK_KV_FP8_E4M3  ? 2.0 * head_dim + 8.0
+                         : kv_dtype == PSK_KV_PSQ4_W32  ? head_dim + head_dim / 8.0
+                                                        : 2.0 * head_dim + head_dim / 8.0;
     const double page_bytes = 4.0 * page_tokens * slice;
-    const double c0 = 8.0 * 16 * 4 * (256 + 8) / page_bytes;
+    const double xcd_bw = 6.7e12 / kXcds;
+    // a workgroup alone on its CU streams up to 1.5x its fair share; where two
+    // share a CU (PSQ4, VALU-bound) the tail gains nothing (measured: 7 splits
+    // of 293 pages ran 4% slower than 8 of 256 at b64 x 32k)
+    const double wg_bw = (per_cu > 1 ? 1.0 : 1.5) * xcd_bw / (double)slots;
+    const double c0 = 10e-6;
     // Candidates (predicted makespan, splits, pages per split); splits == 1
     // competes when the rows alone fill every slot (it saves the combine pass,
     // ~2%).
@@ -137,11 +173,11 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
         const double share = indep ? 1.0 : 0.25;
         for (uint32_t r = 0; r < rows; ++r)
             for (uint32_t s = 0; s + 1 < (pages[r] + per - 1) / per; ++s)
-                for (uint32_t k = 0; k < copies; ++k) units.push_back(per * share);
+                for (uint32_t k = 0; k < copies; ++k) units.push_back(per * share * page_bytes);
         for (uint32_t r = 0; r < rows; ++r) {
             const uint32_t n = (pages[r] + per - 1) / per;
             if (n == 0) continue;
-            for (uint32_t k = 0; k < copies; ++k) units.push_back((pages[r] - (n - 1) * per) * share);
+            for (uint32_t k = 0; k < copies; ++k) units.push_back((pages[r] - (n - 1) * per) * share * page_bytes);
         }
     };
     if ((uint64_t)rows * groups >= total_slots) {
@@ -149,7 +185,7 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
         // more than the combine pass costs (~2%).
         build(max_pages, rows);
         std::sort(units.begin(), units.end(), std::greater<double>());
-        cands.push_back({split_makespan(units, slots, c0) / 1.02, 1u, 0u});
+        cands.push_back({split_makespan(units, slots, xcd_bw, wg_bw, c0) / 1.02, 1u, 0u});
     }
     for (uint32_t splits = 2; splits <= std::min<uint32_t>(kMaxSplits, max_pages); ++splits) {
         const uint32_t per = (max_pages + splits - 1) / splits;
@@ -160,9 +196,12 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
         if (need > partial_bytes) break;
         uint64_t n_units = 0;
         for (uint32_t r = 0; r < rows; ++r) n_units += (pages[r] + per - 1) / per;
-        if (n_units * groups > 8 * total_slots) break;   // finer splits only add start-ups
+        if (n_units * groups > 4 * total_slots) break;   // finer splits only add start-ups
         build(per, n_units);
-        cands.push_back({split_makespan(units, slots, c0), splits, per});
+        // the shared-item mode (below 128 workgroups) merges its 4 waves
+        // through LDS and measured up to 18% slower than the model
+        const double shared = n_units * groups >= 128 ? 1.0 : 1.1;
+        cands.push_back({split_makespan(units, slots, xcd_bw, wg_bw, c0) * shared, splits, per});
     }
     if (cands.empty()) return best;
     const Cand* pick = &cands[0];
