@@ -76,6 +76,72 @@ __device__ __forceinline__ bf16x8 q8(const uint16_t* q, bool ok) {
     return __builtin_bit_cast(bf16x8, r);
 }
 
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+
+// Packs 4 floats into 4 E4M3 bytes (hardware RNE; |x| <= 448 here).
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+}
+
+// FP8 QK^T on v_mfma_f32_16x16x128_f8f6f4: Q of one (row, head) as E4M3
+// hi + lo parts of q * 2^sh, sh = 8 - E with max|q| = m * 2^E (m in
+// [0.5, 1)), so max|q * 2^sh| is in [128, 256). hi = RNE(q * 2^sh) and lo =
+// RNE(q * 2^sh - hi) keep q to 2^-8 relative (the residual is exact in
+// fp32); scores are the MFMA sums times 2^-sh. Lane (n, g) holds dims
+// [64i + 16g, +16) of every 64-dim block i: bytes 0-15 of operand j are
+// block 2j, bytes 16-31 block 2j + 1, the K fragment's layout (the MFMA
+// pairs equal (lane group, byte) positions of its two operands).
+template <int D>
+__device__ __forceinline__ float q_split_e4m3(const uint16_t* qrow, bool ok, uint32_t g,
+                                              i32x8 (&hi)[D / 128], i32x8 (&lo)[D / 128]) {
+    constexpr int NB = D / 64;
+    float x[NB][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        u32x4 w0 = {0u, 0u, 0u, 0u}, w1 = {0u, 0u, 0u, 0u};
+        if (ok) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(qrow + 64 * i + 16 * g);
+            w0 = src[0];
+            w1 = src[1];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t wd = k < 4 ? w0[k] : w1[k - 4];
+            x[i][2 * k] = __builtin_bit_cast(float, wd << 16);
+            x[i][2 * k + 1] = __builtin_bit_cast(float, wd & 0xFFFF0000u);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i][k]));
+    }
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, 64));
+    const int sh = (amax > 0.0f && amax <= 3.0e38f) ? 8 - __builtin_amdgcn_frexp_expf(amax) : 0;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float y[4], r[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) y[t] = __builtin_ldexpf(x[i][4 * k + t], sh);
+            h[k] = f32x4_to_e4m3(y[0], y[1], y[2], y[3]);
+            r[0] = y[0] - __builtin_amdgcn_cvt_f32_fp8((int)h[k], 0);
+            r[1] = y[1] - __builtin_amdgcn_cvt_f32_fp8((int)h[k], 1);
+            r[2] = y[2] - __builtin_amdgcn_cvt_f32_fp8((int)h[k], 2);
+            r[3] = y[3] - __builtin_amdgcn_cvt_f32_fp8((int)h[k], 3);
+            l[k] = f32x4_to_e4m3(r[0], r[1], r[2], r[3]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            hi[i / 2][4 * (i & 1) + k] = (int)h[k];
+            lo[i / 2][4 * (i & 1) + k] = (int)l[k];
+        }
+    }
+    return __builtin_ldexpf(1.0f, -sh);
+}
+
 constexpr uint32_t kTilePageWindow = 1024;   // block-table entries staged in LDS per pass
 
 // LDS bytes of one pipeline stage: K and V of a 32-token chunk (lane-major DMA
@@ -105,6 +171,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     constexpr int NL = D * KVB / 64;     // 16 B DMA pieces per lane per half
     constexpr int NS = D / 32;           // K-steps of QK^T
     constexpr int NDB = D / 16;          // 16-dim output blocks
+    constexpr bool kF8Mfma = KVB == 1 && D % 128 == 0;
     // a 16-token half of K (V) in LDS, padded by 128 B so that the two halves
     // of a chunk fall on opposite halves of the 64 LDS banks (the transposing
     // V reads of one instruction touch both)
@@ -222,6 +289,10 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     // compute on zero Q and are never written
     bool hv[HPW];
     bf16x8 qf[HPW][NS];
+    // FP8 KV at D % 128 == 0: K codes go to the MFMA unconverted (Q as E4M3
+    // hi + lo, see q_split_e4m3); qinv = 2^-sh of each head's row
+    i32x8 qh[HPW][kF8Mfma ? D / 128 : 1], ql[HPW][kF8Mfma ? D / 128 : 1];
+    float qinv[HPW];
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
         const uint32_t gh = hbase + (uint32_t)i;
@@ -229,10 +300,15 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         const uint32_t head = kv_head * qpk + (hv[i] ? gh : 0u);
         const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
                                (uint64_t)(row_ok ? row : r0) * a.q_row_stride + (uint64_t)head * D;
+        qinv[i] = 1.0f;
+        if constexpr (kF8Mfma) {
+            qinv[i] = q_split_e4m3<D>(qrow, row_ok && hv[i], g, qh[i], ql[i]);
+        } else {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int d0 = KVB == 2 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
-            qf[i][s] = q8(qrow + d0, row_ok && hv[i]);
+            for (int s = 0; s < NS; ++s) {
+                const int d0 = KVB == 2 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
+                qf[i][s] = q8(qrow + d0, row_ok && hv[i]);
+            }
         }
     }
 
@@ -379,7 +455,44 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         auto consume = [&](uint32_t c, const uint8_t* st, auto full_tag) __attribute__((always_inline)) {
             constexpr bool kFull = decltype(full_tag)::value;
             f32x4 sc[HPW][H];
-            if constexpr (NS % 2 == 0) {
+            if constexpr (kF8Mfma) {
+                // 128 dims per MFMA: the lane's 16 B of blocks 2j and 2j + 1
+                // (one half), read one step ahead of the MFMAs they feed
+                constexpr int NJ = D / 128;
+                auto kread = [&](int u) __attribute__((always_inline)) {
+                    const uint8_t* kb = st + (u / NJ) * HALF_STRIDE + 16 * lane + 2048 * (u % NJ);
+                    const u32x4 x0 = *reinterpret_cast<const u32x4*>(kb);
+                    const u32x4 x1 = *reinterpret_cast<const u32x4*>(kb + 1024);
+                    return (i32x8){(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3],
+                                   (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+                };
+                f32x4 acc[HPW];
+                i32x8 cur = kread(0);
+#pragma unroll
+                for (int u = 0; u < H * NJ; ++u) {
+                    i32x8 nxt = cur;
+                    if (u + 1 < H * NJ) nxt = kread(u + 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    const int j = u % NJ;
+                    if (j == 0) {
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    }
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i)
+                        acc[i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(cur, qh[i][j], acc[i], 0, 0, 0, 0,
+                                                                                  0, 0);
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i)
+                        acc[i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(cur, ql[i][j], acc[i], 0, 0, 0, 0,
+                                                                                  0, 0);
+                    if (j == NJ - 1) {
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i) sc[i][u / NJ] = acc[i];
+                    }
+                    cur = nxt;
+                }
+            } else if constexpr (NS % 2 == 0) {
                 // K in pairs of K-steps (16 B of FP8 or 2 x 16 B of BF16 per
                 // lane), each pair's LDS read issued one pair ahead so that its
                 // latency hides behind the previous pair's MFMAs
@@ -477,7 +590,8 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 for (int hf = 0; hf < H; ++hf)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        s2[hf][r] = tok_ok[hf][r] ? sc[i][hf][r] * (p.scale_log2 * kscale[hf][r]) : -INFINITY;
+                        s2[hf][r] = tok_ok[hf][r] ? (sc[i][hf][r] * qinv[i]) * (p.scale_log2 * kscale[hf][r])
+                                                  : -INFINITY;
                         mx = __builtin_fmaxf(mx, s2[hf][r]);
                     }
                 mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
