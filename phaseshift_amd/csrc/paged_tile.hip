@@ -584,18 +584,20 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
             u32x4 pf[HPW], pl[HPW];
 #pragma unroll
             for (int i = 0; i < HPW; ++i) {
+                // scores in log2 units are s2 * qinv[i]: qinv > 0 scales the
+                // row maximum once and enters exp2 through one FMA per score
                 float s2[H][4];
                 float mx = -INFINITY;
 #pragma unroll
                 for (int hf = 0; hf < H; ++hf)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        s2[hf][r] = tok_ok[hf][r] ? (sc[i][hf][r] * qinv[i]) * (p.scale_log2 * kscale[hf][r])
-                                                  : -INFINITY;
+                        s2[hf][r] = tok_ok[hf][r] ? sc[i][hf][r] * (p.scale_log2 * kscale[hf][r]) : -INFINITY;
                         mx = __builtin_fmaxf(mx, s2[hf][r]);
                     }
                 mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
                 mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+                mx *= qinv[i];
                 // m_run is the row's softmax reference: it moves only when a
                 // score exceeds it by more than kLazyMaxSlack (then P <= 2^slack)
                 const bool moved = mx > m_run[i] + kLazyMaxSlack;
@@ -607,7 +609,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 for (int hf = 0; hf < H; ++hf)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
+                        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s2[hf][r], qinv[i], -m_use));
                         psum += e;
                         pv[hf][r] = e * vscale[hf][r];
                     }
