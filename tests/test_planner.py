@@ -191,3 +191,27 @@ def test_args_keep_their_tensors_alive():
     del k
     gc.collect()
     assert ref_k() is not None and b.k_input == ref_k().data_ptr()
+
+
+def test_split_chooser_against_measured_sweep():
+    """psk_choose_decode_split on the bench workloads picks a split whose measured
+    kernel time (one MI355X, tests/measured/decode_split_times_mi355x.json, written by
+    sweep_decode_splits.py beside it) is within 5% of the fastest measured split."""
+    import json
+    import os
+    import numpy as np
+    from phaseshift_amd import ops
+    path = os.path.join(os.path.dirname(__file__), "measured", "decode_split_times_mi355x.json")
+    times = json.load(open(path))
+    rng = np.random.default_rng(404)
+    cfg4 = np.exp(rng.uniform(np.log(4096), np.log(65536), 64)).astype(np.int64)
+    cfg3 = np.random.default_rng(303).integers(1024, 32769, 32)
+    cases = [("cfg4_fp8_loguniform_seed404", cfg4, True),
+             ("cfg3_bf16_uniform_seed303", cfg3, False),
+             ("main_fp8_b64_ctx32k", np.array([32768] * 64), True)]
+    for name, lens, fp8 in cases:
+        measured = {int(k): v for k, v in times[name].items()}
+        sp, pp = ops.choose_decode_split(len(lens), 24, 4, 256, 16, fp8, [int(x) for x in lens], 1 << 40)
+        assert pp in measured, (name, sp, pp)
+        best = min(measured.values())
+        assert measured[pp] <= 1.05 * best, (name, pp, measured[pp], best)
