@@ -222,10 +222,12 @@ int psk_attention_paged_prefill_fp8_e4m3(const psk_paged_attention_args* a,
 
 /* Additive: split-K over the same tiles; the combine is
  * psk_attention_paged_split_reduce_ex with the same splits / pages_per_split
- * (pages_per_split > 0 is required: the rows of a tile differ in length). */
+ * (pages_per_split > 0 is required: the rows of a tile differ in length).
+ * kv_dtype: PSK_KV_BF16, PSK_KV_FP8_E4M3 (f32 scale pools), PSK_KV_PSQ4_W32 or
+ * PSK_KV_PSQ8_W32 (bf16 block-scale pools, 4 B aligned; head_dim 128 or 256). */
 int psk_attention_paged_tile_split(const psk_paged_attention_args* a, uint32_t kv_dtype,
                                    const void* k_pool, const void* v_pool,
-                                   const float* k_scale_pool, const float* v_scale_pool,
+                                   const void* k_scale_pool, const void* v_scale_pool,
                                    float* partials, uint32_t splits, uint32_t pages_per_split,
                                    void* stream);
 

@@ -179,4 +179,39 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// KV formats of the attention kernels.
+constexpr int kFmtBf16 = 0;   // bf16 values
+constexpr int kFmtFp8 = 1;    // E4M3 codes, one f32 scale per (token, kv head)
+constexpr int kFmtPsq8 = 2;   // E4M3 codes, one bf16 scale per 32-value block
+constexpr int kFmtPsq4 = 3;   // cb10 nibbles, one bf16 scale per 32-value block
+
+template <int FMT>
+constexpr bool fmt_psq() { return FMT == kFmtPsq8 || FMT == kFmtPsq4; }
+// bytes of one (token, kv head) K (or V) slice
+template <int FMT, int D>
+constexpr int code_bytes() { return FMT == kFmtBf16 ? 2 * D : FMT == kFmtPsq4 ? D / 2 : D; }
+
+// Q fragment of a PSQ4 K-step: dims d0..d0+3 and d0+16..d0+19 (the low and
+// high nibbles of 4 code bytes), zeros past the group.
+__device__ __forceinline__ bf16x8 load_q4x2(const uint16_t* q, bool ok) {
+    u32x4 r = {0u, 0u, 0u, 0u};
+    if (ok) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            r[i] = (uint32_t)q[2 * i] | ((uint32_t)q[2 * i + 1] << 16);
+            r[2 + i] = (uint32_t)q[16 + 2 * i] | ((uint32_t)q[16 + 2 * i + 1] << 16);
+        }
+    }
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// The E4M3 codes of the cb10 values of 4 PSQ4 code bytes, low nibbles (hi =
+// false) or high nibbles: magnitude index -> E4M3 code of {0,1,2,3,4,6,8,10}
+// by byte permute, the nibble's sign bit -> bit 7.
+__device__ __forceinline__ uint32_t psq4_e4m3x4(uint32_t x, bool hi) {
+    const uint32_t idx = (hi ? (x >> 4) : x) & 0x07070707u;
+    const uint32_t mag = __builtin_amdgcn_perm(0x52504C48u, 0x44403800u, idx);
+    return mag | ((hi ? x : (x << 4)) & 0x80808080u);
+}
+
 }  // namespace psk

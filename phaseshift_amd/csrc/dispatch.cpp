@@ -18,17 +18,17 @@
 
 namespace psk {
 size_t decode_workgroup_lds_bytes(uint32_t kv_dtype, uint32_t head_dim);
-uint32_t tile_workgroups_per_cu(int kvb, uint32_t head_dim, uint32_t q_per_kv);
+uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q_per_kv);
 hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
-                              const void* v, const float* ks, const float* vs,
+                              const void* v, const void* ks, const void* vs,
                               const uint32_t* tile_begin, const uint32_t* tile_rows,
                               uint32_t n_tiles, uint32_t tiles_per_group, float* partials,
                               uint32_t splits, uint32_t pages_per_split, hipStream_t stream);
-uint32_t tile_group_size(uint32_t q_per_kv);
+uint32_t tile_group_size(uint32_t q_per_kv, uint32_t kv_dtype);
 uint64_t tile_launch_workgroups(uint64_t n_tiles, uint32_t tiles_per_group, uint32_t q_per_kv,
                                 uint32_t kv_heads);
 bool paged_tiles_supported(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
-                           const void* v);
+                           const void* v, const void* ks, const void* vs);
 }  // namespace psk
 
 namespace ps::qwen35::runtime {
@@ -219,13 +219,13 @@ namespace {
 // blocks over long contexts need splits to occupy the CUs).
 DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t tiles_per_group, uint32_t region_rows,
                               uint32_t kv_heads, uint32_t q_heads, uint32_t head_dim,
-                              uint32_t kv_bytes, uint32_t page_tokens,
+                              uint32_t kv_dtype, uint32_t page_tokens,
                               uint32_t max_visible_tokens, uint64_t partial_bytes) {
     DecodeSplit s;
     if (max_visible_tokens < kSplitMinVisible || n_tiles == 0 || kv_heads == 0) return s;
     const uint32_t q_per_kv = q_heads / kv_heads;
     const uint64_t slots = (uint64_t)device_cus() *
-                           psk::tile_workgroups_per_cu(kv_bytes == 1 ? 1 : 2, head_dim, q_per_kv);
+                           psk::tile_workgroups_per_cu(kv_dtype, head_dim, q_per_kv);
     const uint64_t wgs = psk::tile_launch_workgroups(n_tiles, tiles_per_group, q_per_kv, kv_heads);
     if (wgs >= slots) return s;
     const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
@@ -303,9 +303,12 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         next = r.row_begin + r.row_count;
     }
     if (next != c.rows) partition = false;
-    // PSQ pools have no tile kernel: every row of the step is a decode row
-    // (each attends to its own prefix, the reference's causal rule).
-    if (!partition || psq) return add_decode(0, c.rows);
+    // PSQ tiles cover head_dim 128 and 256 (q_per_kv <= 8 as every tile);
+    // other PSQ shapes run every row of the step as a decode row (each
+    // attends to its own prefix, the reference's causal rule).
+    const bool psq_tiles = (c.head_dim == 128 || c.head_dim == 256) && c.kv_heads != 0 &&
+                           c.q_heads / c.kv_heads <= 8u;
+    if (!partition || (psq && !psq_tiles)) return add_decode(0, c.rows);
 
     // decode launches: maximal runs of consecutive non-tile requests
     for (size_t i = 0; i < reqs.size();) {
@@ -329,7 +332,9 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         // prefill tiles go in groups of consecutive tiles of one request (the
         // kernel stages each K/V chunk once for the group); rows == 0 pads
         const uint32_t group =
-            cls == kExecPrefill ? psk::tile_group_size(c.kv_heads ? c.q_heads / c.kv_heads : 0u) : 1u;
+            cls == kExecPrefill ? psk::tile_group_size(c.kv_heads ? c.q_heads / c.kv_heads : 0u,
+                                                       static_cast<uint32_t>(step.kv_dtype))
+                                : 1u;
         // (visible bound, first tile of the group in `flat`)
         std::vector<std::pair<uint32_t, size_t>> groups;
         std::vector<PlannedTile> flat;
@@ -369,7 +374,7 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         k.rows = hi - lo;
         const DecodeSplit s = choose_tile_split(
             k.tile_count, k.tiles_per_group, k.rows, c.kv_heads, c.q_heads, c.head_dim,
-            step.kv_dtype == KVCacheDType::FP8_E4M3 ? 1u : 2u, c.page_tokens,
+            static_cast<uint32_t>(step.kv_dtype), c.page_tokens,
             step.max_visible_tokens, pbytes);
         k.splits = s.splits;
         k.pages_per_split = s.pages_per_split;
@@ -463,24 +468,7 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
         float* const parts = step.partials ? step.partials + k.partial_offset : nullptr;
         const PagedAttentionCommonArgs a = region_args(step.common, k.row_begin, k.rows);
         hipError_t e = hipSuccess;
-        if (psq) {
-            const auto* ca = reinterpret_cast<const psk_paged_attention_args*>(&a);
-            const auto* kc = static_cast<const uint8_t*>(step.k_pool);
-            const auto* vc = static_cast<const uint8_t*>(step.v_pool);
-            const auto* ks = static_cast<const uint16_t*>(step.k_scale_pool);
-            const auto* vs = static_cast<const uint16_t*>(step.v_scale_pool);
-            const uint32_t kvd = static_cast<uint32_t>(step.kv_dtype);
-            const uint32_t bph = a.head_dim / 32u;
-            if (k.splits > 1) {
-                e = static_cast<hipError_t>(psk_attention_paged_psq_split_ex(
-                    ca, kvd, kc, vc, ks, vs, bph, parts, k.splits, k.pages_per_split, stream));
-                if (e == hipSuccess)
-                    e = launch_attention_paged_split_reduce_ex(a, parts, k.splits,
-                                                               k.pages_per_split, stream);
-            } else {
-                e = static_cast<hipError_t>(psk_attention_paged_psq(ca, kvd, kc, vc, ks, vs, bph, stream));
-            }
-        } else if (k.kind == PlannedKernel::Kind::Tile) {
+        if (k.kind == PlannedKernel::Kind::Tile) {
             // tile rows are relative to the launch region
             std::vector<uint32_t> tb(k.tile_count), tr(k.tile_count);
             for (uint32_t t = 0; t < k.tile_count; ++t) {
@@ -488,10 +476,11 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
                 tr[t] = plan.tiles[k.tile_first + t].rows;
             }
             const psk_paged_attention_args* ca = reinterpret_cast<const psk_paged_attention_args*>(&a);
-            const uint32_t kvd = fp8 ? PSK_KV_FP8_E4M3 : PSK_KV_BF16;
-            if (psk::paged_tiles_supported(*ca, kvd, step.k_pool, step.v_pool)) {
-                e = psk::launch_paged_tiles(*ca, kvd, step.k_pool, step.v_pool, ksf,
-                                            vsf, tb.data(), tr.data(), k.tile_count,
+            const uint32_t kvd = static_cast<uint32_t>(step.kv_dtype);
+            if (psk::paged_tiles_supported(*ca, kvd, step.k_pool, step.v_pool, step.k_scale_pool,
+                                           step.v_scale_pool)) {
+                e = psk::launch_paged_tiles(*ca, kvd, step.k_pool, step.v_pool, step.k_scale_pool,
+                                            step.v_scale_pool, tb.data(), tr.data(), k.tile_count,
                                             k.tiles_per_group, parts, k.splits,
                                             k.pages_per_split, stream);
                 for (uint32_t q = 0; e == hipSuccess && k.splits > 1 && q < k.req_count; ++q) {
@@ -510,9 +499,33 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
                 for (uint32_t t = 0; e == hipSuccess && t < k.tile_count; ++t) {
                     if (tr[t] == 0u) continue;   // group padding
                     const PagedAttentionCommonArgs ta = region_args(a, tb[t], tr[t]);
-                    e = fp8 ? launch_attention_paged_fp8_e4m3(ta, k8, v8, ksf, vsf, stream)
-                            : launch_attention_paged_bf16(ta, k16, v16, stream);
+                    if (psq)
+                        e = static_cast<hipError_t>(psk_attention_paged_psq(
+                            reinterpret_cast<const psk_paged_attention_args*>(&ta), kvd,
+                            static_cast<const uint8_t*>(step.k_pool), static_cast<const uint8_t*>(step.v_pool),
+                            static_cast<const uint16_t*>(step.k_scale_pool),
+                            static_cast<const uint16_t*>(step.v_scale_pool), a.head_dim / 32u, stream));
+                    else
+                        e = fp8 ? launch_attention_paged_fp8_e4m3(ta, k8, v8, ksf, vsf, stream)
+                                : launch_attention_paged_bf16(ta, k16, v16, stream);
                 }
+            }
+        } else if (psq) {
+            const auto* ca = reinterpret_cast<const psk_paged_attention_args*>(&a);
+            const auto* kc = static_cast<const uint8_t*>(step.k_pool);
+            const auto* vc = static_cast<const uint8_t*>(step.v_pool);
+            const auto* ks = static_cast<const uint16_t*>(step.k_scale_pool);
+            const auto* vs = static_cast<const uint16_t*>(step.v_scale_pool);
+            const uint32_t kvd = static_cast<uint32_t>(step.kv_dtype);
+            const uint32_t bph = a.head_dim / 32u;
+            if (k.splits > 1) {
+                e = static_cast<hipError_t>(psk_attention_paged_psq_split_ex(
+                    ca, kvd, kc, vc, ks, vs, bph, parts, k.splits, k.pages_per_split, stream));
+                if (e == hipSuccess)
+                    e = launch_attention_paged_split_reduce_ex(a, parts, k.splits,
+                                                               k.pages_per_split, stream);
+            } else {
+                e = static_cast<hipError_t>(psk_attention_paged_psq(ca, kvd, kc, vc, ks, vs, bph, stream));
             }
         } else if (k.splits > 1) {
             e = fp8 ? launch_attention_paged_fp8_e4m3_split(a, k8, v8, ksf, vsf, parts,

@@ -38,18 +38,6 @@
 namespace psk {
 namespace {
 
-// KV formats of the decode kernel.
-constexpr int kFmtBf16 = 0;   // bf16 values
-constexpr int kFmtFp8 = 1;    // E4M3 codes, one f32 scale per (token, kv head)
-constexpr int kFmtPsq8 = 2;   // E4M3 codes, one bf16 scale per 32-value block
-constexpr int kFmtPsq4 = 3;   // cb10 nibbles, one bf16 scale per 32-value block
-
-template <int FMT>
-constexpr bool fmt_psq() { return FMT == kFmtPsq8 || FMT == kFmtPsq4; }
-// bytes of one (token, kv head) K (or V) slice
-template <int FMT, int D>
-constexpr int code_bytes() { return FMT == kFmtBf16 ? 2 * D : FMT == kFmtPsq4 ? D / 2 : D; }
-
 struct DecodeParams {
     psk_paged_attention_args a;
     const uint8_t* k_pool;
@@ -84,29 +72,6 @@ __device__ __forceinline__ bf16x8 load_q8(const uint16_t* q, bool ok) {
 
 template <int FMT>
 constexpr int chunk_halves() { return FMT == kFmtBf16 ? 1 : 2; }   // 16-token halves per chunk
-
-// Q fragment of a PSQ4 K-step: dims d0..d0+3 and d0+16..d0+19 (the low and
-// high nibbles of 4 code bytes), zeros past the group.
-__device__ __forceinline__ bf16x8 load_q4x2(const uint16_t* q, bool ok) {
-    u32x4 r = {0u, 0u, 0u, 0u};
-    if (ok) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            r[i] = (uint32_t)q[2 * i] | ((uint32_t)q[2 * i + 1] << 16);
-            r[2 + i] = (uint32_t)q[16 + 2 * i] | ((uint32_t)q[16 + 2 * i + 1] << 16);
-        }
-    }
-    return __builtin_bit_cast(bf16x8, r);
-}
-
-// The E4M3 codes of the cb10 values of 4 PSQ4 code bytes, low nibbles (hi =
-// false) or high nibbles: magnitude index -> E4M3 code of {0,1,2,3,4,6,8,10}
-// by byte permute, the nibble's sign bit -> bit 7.
-__device__ __forceinline__ uint32_t psq4_e4m3x4(uint32_t x, bool hi) {
-    const uint32_t idx = (hi ? (x >> 4) : x) & 0x07070707u;
-    const uint32_t mag = __builtin_amdgcn_perm(0x52504C48u, 0x44403800u, idx);
-    return mag | ((hi ? x : (x << 4)) & 0x80808080u);
-}
 
 typedef __attribute__((ext_vector_type(2))) int i32x2;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
@@ -1194,15 +1159,33 @@ extern "C" int psk_attention_paged_psq8(const psk_paged_attention_args* a, const
 }
 // Prefill rows run as independent decode rows (each sees its own pos + 1
 // tokens, the reference's causal rule).
+namespace psk {
+bool launch_prefill_psq_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* kc,
+                              const void* vc, const void* ks, const void* vs, hipStream_t stream,
+                              hipError_t& err);
+}  // namespace psk
+
+// PSQ prefill (paged_prefill.hip:461-490,852-880): 16-row tiles of the
+// launch (the tile contract of the BF16 / FP8 prefill launchers) on the tile
+// kernel; shapes outside it run row by row on the PSQ decode kernel.
+static int prefill_psq(const psk_paged_attention_args* a, uint32_t kv_dtype, const uint8_t* kc,
+                       const uint8_t* vc, const uint16_t* ks, const uint16_t* vs, uint32_t bph,
+                       void* stream) {
+    hipError_t e = psk::validate_psq(a, kc, vc, ks, vs, bph);
+    if (e != hipSuccess) return e;
+    if (psk::launch_prefill_psq_tiles(*a, kv_dtype, kc, vc, ks, vs, static_cast<hipStream_t>(stream), e))
+        return e;
+    return psk_attention_paged_psq(a, kv_dtype, kc, vc, ks, vs, bph, stream);
+}
 extern "C" int psk_attention_paged_prefill_psq4(const psk_paged_attention_args* a, const uint8_t* kc,
                                                 const uint8_t* vc, const uint16_t* ks,
                                                 const uint16_t* vs, uint32_t bph, void* stream) {
-    return psk_attention_paged_psq(a, PSK_KV_PSQ4_W32, kc, vc, ks, vs, bph, stream);
+    return prefill_psq(a, PSK_KV_PSQ4_W32, kc, vc, ks, vs, bph, stream);
 }
 extern "C" int psk_attention_paged_prefill_psq8(const psk_paged_attention_args* a, const uint8_t* kc,
                                                 const uint8_t* vc, const uint16_t* ks,
                                                 const uint16_t* vs, uint32_t bph, void* stream) {
-    return psk_attention_paged_psq(a, PSK_KV_PSQ8_W32, kc, vc, ks, vs, bph, stream);
+    return prefill_psq(a, PSK_KV_PSQ8_W32, kc, vc, ks, vs, bph, stream);
 }
 extern "C" int psk_attention_paged_psq4_split(const psk_paged_attention_args* a, const uint8_t* kc,
                                               const uint8_t* vc, const uint16_t* ks,

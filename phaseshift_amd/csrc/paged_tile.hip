@@ -145,10 +145,11 @@ __device__ __forceinline__ float q_split_e4m3(const uint16_t* qrow, bool ok, uin
 constexpr uint32_t kTilePageWindow = 1024;   // block-table entries staged in LDS per pass
 
 // LDS bytes of one pipeline stage: K and V of a 32-token chunk (lane-major DMA
-// layout) and, FP8, the k/v scales of its tokens.
-template <int KVB, int D>
+// layout) and, FP8 and PSQ, the k/v scales of its tokens (256 B per 16-token
+// half: FP8 one f32 per token, PSQ dword w of token t at 64w + 4t).
+template <int FMT, int D>
 constexpr int tile_stage_bytes() {
-    return 2 * 2 * (16 * D * KVB + 128) + (KVB == 1 ? 2 * 2 * 256 : 0);
+    return 2 * 2 * (16 * code_bytes<FMT, D>() + 128) + (FMT != kFmtBf16 ? 2 * 2 * 256 : 0);
 }
 constexpr int kTileStages = 4;
 
@@ -162,23 +163,30 @@ constexpr int tile_waves_per_simd(int hpw) { return hpw == 1 ? 3 : 2; }
 // heads (HPW each) of one tile. RT > 1 (NW == RT): wave w owns tile w of a
 // group of RT consecutive tiles of one sequence and HPW heads of the group's
 // head part (blockIdx); the tiles share every staged K/V chunk.
-template <int KVB, int D, int NW, int HPW, int RT, bool kAl16>
+template <int FMT, int D, int NW, int HPW, int RT, bool kAl16>
 __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_kernel(const TileParams p) {
     static_assert(RT == 1 || RT == NW, "grouped tiles: one wave per tile");
+    constexpr int KVB = FMT == kFmtBf16 ? 2 : 1;   // bytes per value (PSQ4: codes of 2 values per byte)
+    constexpr bool kPsq = fmt_psq<FMT>();
+    constexpr int CB = code_bytes<FMT, D>();       // K (V) bytes of one token's head slice
     constexpr int WH = NW / RT;          // waves along the heads of one tile
     constexpr int H = 2;                 // 16-token halves per chunk
     constexpr int CT = 16 * H;           // tokens per chunk
-    constexpr int NL = D * KVB / 64;     // 16 B DMA pieces per lane per half
+    constexpr int NL = CB / 64;          // 16 B DMA pieces per lane per half
     constexpr int NS = D / 32;           // K-steps of QK^T
     constexpr int NDB = D / 16;          // 16-dim output blocks
-    constexpr bool kF8Mfma = KVB == 1 && D % 128 == 0;
+    constexpr bool kF8Mfma = FMT == kFmtFp8 && D % 128 == 0;
     // a 16-token half of K (V) in LDS, padded by 128 B so that the two halves
     // of a chunk fall on opposite halves of the 64 LDS banks (the transposing
     // V reads of one instruction touch both)
-    constexpr int HALF_STRIDE = 16 * D * KVB + 128;
+    constexpr int HALF_STRIDE = 16 * CB + 128;
     constexpr int KV_BYTES = H * HALF_STRIDE;
     constexpr int SC_BYTES = KVB == 1 ? H * 256 : 0;
-    constexpr int STAGE = tile_stage_bytes<KVB, D>();
+    constexpr int STAGE = tile_stage_bytes<FMT, D>();
+    // PSQ: dwords of block scales per (token, head); byte offsets of one
+    // (token, head) slice's codes and scales are its slice index times CB and
+    // times 2 * D / 32
+    constexpr int SW = D / 64;
     // DMA instructions of one chunk (K, V, then FP8 k/v scales), dealt
     // round-robin over the NW waves; every wave issues DPW of them (the
     // remainder repeats earlier ones, which rewrite identical bytes), so the
@@ -306,8 +314,17 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         } else {
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                const int d0 = KVB == 2 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
-                qf[i][s] = q8(qrow + d0, row_ok && hv[i]);
+                if constexpr (FMT == kFmtPsq4) {
+                    // K-step s = block s: dims 4g.. and 16 + 4g.. (nibbles)
+                    qf[i][s] = load_q4x2(qrow + s * 32 + (int)g * 4, row_ok && hv[i]);
+                } else {
+                    // BF16, PSQ8 (K-step s = block s): dims 32s + 8g..; FP8:
+                    // the 16 B of 64-dim block s/2 split in two K-steps
+                    const int d0 = (FMT == kFmtBf16 || FMT == kFmtPsq8)
+                                       ? s * 32 + (int)g * 8
+                                       : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
+                    qf[i][s] = q8(qrow + d0, row_ok && hv[i]);
+                }
             }
         }
     }
@@ -355,6 +372,30 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         if (ts >= te) continue;
         const uint32_t t_last = te - 1u;
 
+        // Byte offset of the (page pg, token 0, kv_head) slice in a code
+        // pool, and the bytes between consecutive tokens' slices. PSQ slices
+        // are indexed like their scales: ((layer * pages + pg) * P + off) *
+        // kv_heads + kv_head, CB bytes each.
+        auto slice_base = [&](uint32_t pg) __attribute__((always_inline)) -> uint64_t {
+            if constexpr (kPsq)
+                return ((scale_layer + pg) * P * a.kv_heads + kv_head) * (uint64_t)CB;
+            else
+                return (layer_base + (uint64_t)pg * a.elems_per_page + (uint64_t)kv_head * D) * KVB;
+        };
+        const uint32_t tok_bytes = kPsq ? a.kv_heads * (uint32_t)CB : a.elems_per_token * (uint32_t)KVB;
+        // Source of this lane's scale DMA for the token at (pg, off): FP8 its
+        // f32 scale; PSQ dword g of its block scales (lanes past the last
+        // dword repeat it)
+        auto scale_src = [&](uint32_t kind, uint32_t pg, uint32_t off) __attribute__((always_inline)) {
+            const uint64_t si = ((scale_layer + pg) * P + off) * a.kv_heads + kv_head;
+            const float* base = kind == 0u ? k_scale : v_scale;
+            if constexpr (kPsq)
+                return static_cast<const void*>(reinterpret_cast<const uint8_t*>(base) + si * (2u * D / 32u) +
+                                                4u * min(g, (uint32_t)SW - 1u));
+            else
+                return static_cast<const void*>(base + si);
+        };
+
         // This wave's DMAs of the chunk at c into stage st (branch-free;
         // tokens past the range read the last token and are masked later).
         auto issue_own = [&](uint32_t c, uint8_t* st) __attribute__((always_inline)) {
@@ -378,23 +419,16 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
             const uint8_t* pool = kind == 0u ? k_pool : v_pool;
             uint8_t* dst = st + kind * KV_BYTES + hf * HALF_STRIDE;
             if constexpr (kAl16) {
-                const uint8_t* src = pool + (layer_base + (uint64_t)pg * a.elems_per_page +
-                                             (uint64_t)kv_head * D) * KVB;
-                const uint32_t lo = off * a.elems_per_token * KVB + g * 16u;
+                const uint8_t* src = pool + slice_base(pg);
+                const uint32_t lo = off * tok_bytes + g * 16u;
 #pragma unroll
                 for (int i = 0; i < NL; ++i) load_lds<16>(src + (lo + i * 64u), dst + i * 1024);
             } else {
-                const uint8_t* src = pool + (layer_base + (uint64_t)pg * a.elems_per_page +
-                                             (uint64_t)off * a.elems_per_token + (uint64_t)kv_head * D) * KVB +
-                                     g * 16u;
+                const uint8_t* src = pool + slice_base(pg) + (uint64_t)off * tok_bytes + g * 16u;
 #pragma unroll
                 for (int i = 0; i < NL; ++i) load_lds<16>(src + i * 64, dst + i * 1024);
             }
-            if constexpr (KVB == 1) {
-                const uint64_t si = ((scale_layer + pg) * P + off) * a.kv_heads + kv_head;
-                load_lds<4>((kind == 0u ? k_scale : v_scale) + si,
-                            st + 2 * KV_BYTES + kind * SC_BYTES + hf * 256);
-            }
+            if constexpr (KVB == 1) load_lds<4>(scale_src(kind, pg, off), st + 2 * KV_BYTES + kind * SC_BYTES + hf * 256);
         };
         auto issue = [&](uint32_t c, uint8_t* st) __attribute__((always_inline)) {
             if constexpr (kOwnStream) {
@@ -430,21 +464,16 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                     const uint8_t* src;
                     if constexpr (kAl16) {
                         // uniform page base + 32-bit lane offset
-                        const uint64_t base = (layer_base + (uint64_t)pg[hf] * a.elems_per_page +
-                                               (uint64_t)kv_head * D) * KVB;
-                        src = (kind == 0u ? k_pool : v_pool) + base +
-                              (off[hf] * a.elems_per_token * KVB + g * 16u + i * 64u);
+                        src = (kind == 0u ? k_pool : v_pool) + slice_base(pg[hf]) +
+                              (off[hf] * tok_bytes + g * 16u + i * 64u);
                     } else {
-                        const uint64_t elem = layer_base + (uint64_t)pg[hf] * a.elems_per_page +
-                                              (uint64_t)off[hf] * a.elems_per_token + (uint64_t)kv_head * D;
-                        src = (kind == 0u ? k_pool : v_pool) + elem * KVB + g * 16 + i * 64;
+                        src = (kind == 0u ? k_pool : v_pool) + slice_base(pg[hf]) +
+                              (uint64_t)off[hf] * tok_bytes + g * 16 + i * 64;
                     }
                     load_lds<16>(src, st + kind * KV_BYTES + hf * HALF_STRIDE + i * 1024);
                 } else {
                     const uint32_t kind = (j - 2u * H * NL) & 1u, hf = (j - 2u * H * NL) >> 1;
-                    const uint64_t si = ((scale_layer + pg[hf]) * P + off[hf]) * a.kv_heads + kv_head;
-                    load_lds<4>((kind == 0u ? k_scale : v_scale) + si,
-                                st + 2 * KV_BYTES + kind * SC_BYTES + hf * 256);
+                    load_lds<4>(scale_src(kind, pg[hf], off[hf]), st + 2 * KV_BYTES + kind * SC_BYTES + hf * 256);
                 }
             }
         };
@@ -455,7 +484,57 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         auto consume = [&](uint32_t c, const uint8_t* st, auto full_tag) __attribute__((always_inline)) {
             constexpr bool kFull = decltype(full_tag)::value;
             f32x4 sc[HPW][H];
-            if constexpr (kF8Mfma) {
+            if constexpr (kPsq) {
+                // K-step s = block s: the block's partial scores times its K
+                // scale of each token 4g + r (bf16 -> f32 by shift); every
+                // converted K fragment feeds the MFMAs of all HPW heads
+#pragma unroll
+                for (int hf = 0; hf < H; ++hf) {
+                    const uint8_t* kb = st + hf * HALF_STRIDE;
+                    const uint8_t* kscl = st + 2 * KV_BYTES + hf * 256 + 16 * g;
+                    f32x4 acc[HPW];
+#pragma unroll
+                    for (int s = 0; s < NS; ++s) {
+                        // one K-step at a time: unbounded hoisting of the
+                        // LDS reads across steps spills registers
+                        __builtin_amdgcn_sched_barrier(0);
+                        bf16x8 kf;
+                        if constexpr (FMT == kFmtPsq8) {
+                            // bytes 32s + 8g .. +8 of token n
+                            const u32x2 w = *reinterpret_cast<const u32x2*>(
+                                kb + 1024 * (s >> 1) + 16 * (16 * (2 * (s & 1) + (int)(g >> 1)) + (int)n) +
+                                8 * (int)(g & 1u));
+                            kf = fp8x8_to_bf16x8(w[0], w[1]);
+                        } else {
+                            // bytes 16s + 4g .. +4 of token n: dims 4g.. (low
+                            // nibbles) and 16 + 4g.. (high nibbles) of block s
+                            const uint32_t x = *reinterpret_cast<const uint32_t*>(kb + 256 * s + 16 * n + 4 * g);
+                            const uint32_t lo = psq4_e4m3x4(x, false), hi = psq4_e4m3x4(x, true);
+                            u32x4 r;
+                            r[0] = fp8x2_to_bf16x2(lo, false);
+                            r[1] = fp8x2_to_bf16x2(lo, true);
+                            r[2] = fp8x2_to_bf16x2(hi, false);
+                            r[3] = fp8x2_to_bf16x2(hi, true);
+                            kf = __builtin_bit_cast(bf16x8, r);
+                        }
+                        const u32x4 kw = *reinterpret_cast<const u32x4*>(kscl + 64 * (s >> 1));
+                        float ksc[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            ksc[r] = __uint_as_float((s & 1) ? (kw[r] & 0xFFFF0000u) : (kw[r] << 16));
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i) {
+                            const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                kf, qf[i][s], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                acc[i][r] = s == 0 ? part[r] * ksc[r] : __builtin_fmaf(part[r], ksc[r], acc[i][r]);
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i) sc[i][hf] = acc[i];
+                }
+            } else if constexpr (kF8Mfma) {
                 // 128 dims per MFMA: the lane's 16 B of blocks 2j and 2j + 1
                 // (one half), read one step ahead of the MFMAs they feed
                 constexpr int NJ = D / 128;
@@ -570,7 +649,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
             for (int hf = 0; hf < H; ++hf) {
                 kscale[hf] = (f32x4){1.f, 1.f, 1.f, 1.f};
                 vscale[hf] = (f32x4){1.f, 1.f, 1.f, 1.f};
-                if constexpr (KVB == 1) {
+                if constexpr (FMT == kFmtFp8) {
                     kscale[hf] = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + hf * 256 + 16 * g);
                     vscale[hf] = *reinterpret_cast<const f32x4*>(st + 2 * KV_BYTES + SC_BYTES +
                                                                  hf * 256 + 16 * g);
@@ -582,6 +661,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 }
             }
             u32x4 pf[HPW], pl[HPW];
+            float pw[kPsq ? HPW : 1][H][4];   // PSQ: P before the per-block V scales
 #pragma unroll
             for (int i = 0; i < HPW; ++i) {
                 // scores in log2 units are s2 * qinv[i]: qinv > 0 scales the
@@ -619,7 +699,12 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
 #pragma unroll
                     for (int db = 0; db < NDB; ++db) o[i][db] *= alpha;
                 }
-                if constexpr (KVB == 1) {
+                if constexpr (kPsq) {
+#pragma unroll
+                    for (int hf = 0; hf < H; ++hf)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) pw[i][hf][r] = pv[hf][r];
+                } else if constexpr (KVB == 1) {
                     // FP8: P (v_scale folded in) as one f16 operand (11 mantissa
                     // bits); V as f16 (E4M3 values are exact in f16)
                     pf[i][0] = pack_f16x2(pv[0][0], pv[0][1]);
@@ -640,6 +725,60 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
             // V is read in pairs of output blocks, each pair's transposing LDS
             // reads issued one pair ahead of the previous pair's MFMAs.
             const uint8_t* vb = st + KV_BYTES + tr_off;
+            if constexpr (kPsq) {
+                // Per block b: P times the block's V scale of each of the
+                // lane's tokens (4g + r of both halves), one bf16 P operand per
+                // head; the block's V^T fragments are converted once for all
+                // heads (PSQ8: output blocks 2b, 2b + 1; PSQ4: byte i of the
+                // block holds dims i and 16 + i).
+                const uint8_t* vscl = st + 2 * KV_BYTES + SC_BYTES + 16 * g;
+#pragma unroll
+                for (int b = 0; b < NS; ++b) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    const u32x4 w0 = *reinterpret_cast<const u32x4*>(vscl + 64 * (b >> 1));
+                    const u32x4 w1 = *reinterpret_cast<const u32x4*>(vscl + 256 + 64 * (b >> 1));
+                    float vs0[4], vs1[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        vs0[r] = __uint_as_float((b & 1) ? (w0[r] & 0xFFFF0000u) : (w0[r] << 16));
+                        vs1[r] = __uint_as_float((b & 1) ? (w1[r] & 0xFFFF0000u) : (w1[r] << 16));
+                    }
+                    bf16x8 pb[HPW];
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i) {
+                        u32x4 ph;
+                        ph[0] = pack_bf16x2(pw[i][0][0] * vs0[0], pw[i][0][1] * vs0[1]);
+                        ph[1] = pack_bf16x2(pw[i][0][2] * vs0[2], pw[i][0][3] * vs0[3]);
+                        ph[2] = pack_bf16x2(pw[i][1][0] * vs1[0], pw[i][1][1] * vs1[1]);
+                        ph[3] = pack_bf16x2(pw[i][1][2] * vs1[2], pw[i][1][3] * vs1[3]);
+                        pb[i] = __builtin_bit_cast(bf16x8, ph);
+                    }
+                    if constexpr (FMT == kFmtPsq8) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const i32x2 w = tr8(vb + 256 * (2 * b + h));
+                            const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
+#pragma unroll
+                            for (int i = 0; i < HPW; ++i)
+                                o[i][2 * b + h] =
+                                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[i], o[i][2 * b + h], 0, 0, 0);
+                        }
+                    } else {
+                        const i32x2 w = tr8(vb + 256 * b);
+                        const bf16x8 vlo = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)w[0], false),
+                                                           psq4_e4m3x4((uint32_t)w[1], false));
+                        const bf16x8 vhi = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)w[0], true),
+                                                           psq4_e4m3x4((uint32_t)w[1], true));
+#pragma unroll
+                        for (int i = 0; i < HPW; ++i) {
+                            o[i][2 * b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vlo, pb[i], o[i][2 * b], 0, 0, 0);
+                            o[i][2 * b + 1] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_bf16(vhi, pb[i], o[i][2 * b + 1], 0, 0, 0);
+                        }
+                    }
+                }
+                return;
+            }
             static_assert(NDB % 2 == 0, "output blocks in pairs");
             struct VRaw {
                 u32x4 x[2];
@@ -779,13 +918,22 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     }
 }
 
-bool tile_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, const void* vp) {
+// kv_dtype: PSK_KV_*. PSQ: head_dim 128 or 256 (every (token, head) code
+// slice then starts on 16 B), scale pools 4 B aligned (checked by the
+// launchers that take them).
+bool tile_shape_ok(const psk_paged_attention_args& c, uint32_t kv_dtype, const void* kp, const void* vp) {
     const uint32_t qpk = c.q_heads / c.kv_heads;
     if (qpk == 0u || qpk > (uint32_t)kMaxTileHeads) return false;
     const uint32_t D = c.head_dim;
-    if (!(D == 64 || D == 128 || D == 256 || (D == 32 && kvb == 2))) return false;
-    const uint32_t al = 16u / (uint32_t)kvb;
-    if (c.elems_per_token % al || c.elems_per_page % al || c.elems_per_layer % al) return false;
+    const bool psq = kv_dtype == PSK_KV_PSQ4_W32 || kv_dtype == PSK_KV_PSQ8_W32;
+    if (psq) {
+        if (!(D == 128 || D == 256)) return false;
+    } else {
+        const uint32_t kvb = kv_dtype == PSK_KV_FP8_E4M3 ? 1u : 2u;
+        if (!(D == 64 || D == 128 || D == 256 || (D == 32 && kvb == 2))) return false;
+        const uint32_t al = 16u / kvb;
+        if (c.elems_per_token % al || c.elems_per_page % al || c.elems_per_layer % al) return false;
+    }
     if (reinterpret_cast<uintptr_t>(kp) % 16u || reinterpret_cast<uintptr_t>(vp) % 16u) return false;
     // vector output stores: 16 B (f32) / 8 B (bf16) at head*D + 4*k
     const uint32_t oal = c.output_dtype == PSK_OUT_F32 ? 4u : 4u;
@@ -793,25 +941,25 @@ bool tile_shape_ok(const psk_paged_attention_args& c, int kvb, const void* kp, c
     return true;
 }
 
-template <int KVB, int D, int NW, int HPW, int RT, bool kAl16>
+template <int FMT, int D, int NW, int HPW, int RT, bool kAl16>
 hipError_t launch_tile_t3(const TileParams& p, uint64_t grid, hipStream_t stream) {
-    const size_t lds_bytes = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * tile_stage_bytes<KVB, D>();
+    const size_t lds_bytes = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * tile_stage_bytes<FMT, D>();
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_tile_kernel<KVB, D, NW, HPW, RT, kAl16>),
+            reinterpret_cast<const void*>(&paged_tile_kernel<FMT, D, NW, HPW, RT, kAl16>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((paged_tile_kernel<KVB, D, NW, HPW, RT, kAl16>), dim3((uint32_t)grid),
+    hipLaunchKernelGGL((paged_tile_kernel<FMT, D, NW, HPW, RT, kAl16>), dim3((uint32_t)grid),
                        dim3(NW * 64), lds_bytes, stream, p);
     return hipGetLastError();
 }
 
-template <int KVB, int D, int NW, int HPW, int RT = 1>
+template <int FMT, int D, int NW, int HPW, int RT = 1>
 hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream) {
-    return (p.a.page_tokens & 15u) == 0u ? launch_tile_t3<KVB, D, NW, HPW, RT, true>(p, grid, stream)
-                                         : launch_tile_t3<KVB, D, NW, HPW, RT, false>(p, grid, stream);
+    return (p.a.page_tokens & 15u) == 0u ? launch_tile_t3<FMT, D, NW, HPW, RT, true>(p, grid, stream)
+                                         : launch_tile_t3<FMT, D, NW, HPW, RT, false>(p, grid, stream);
 }
 
 // Waves and heads per wave by group size: up to 4 heads one per wave (4
@@ -822,34 +970,67 @@ hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream
 // K/V fragment feeds two MFMAs and two workgroups put 2 waves on every SIMD.
 // Wave counts that load the SIMDs unevenly (3 waves per workgroup) lose: the
 // chunk barrier waits on the doubly loaded SIMDs.
-template <int KVB, int D>
+template <int FMT, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     const uint64_t tiles = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1) / kTileRows;
-    if (p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u) {
-        const uint64_t groups = (tiles + kTileGroup - 1) / kTileGroup;
-        const uint64_t grid = groups * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits;
-        if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-        return launch_tile_t2<KVB, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
+    if constexpr (!fmt_psq<FMT>()) {
+        if (p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u) {
+            const uint64_t groups = (tiles + kTileGroup - 1) / kTileGroup;
+            const uint64_t grid = groups * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits;
+            if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+            return launch_tile_t2<FMT, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
+        }
     }
+    // PSQ: one head per wave only (its per-block scaling does not fit two
+    // heads' accumulators and Q fragments in 256 registers); a grouped tile
+    // list runs tile by tile (padding tiles have no rows and exit)
     const uint64_t grid = tiles * p.a.kv_heads * p.splits;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    if (qpk <= 4u) return launch_tile_t2<KVB, D, 4, 1>(p, grid, stream);
-    if (qpk <= 6u) return launch_tile_t2<KVB, D, 6, 1>(p, grid, stream);
-    return launch_tile_t2<KVB, D, 4, 2>(p, grid, stream);
+    if (qpk <= 4u) return launch_tile_t2<FMT, D, 4, 1>(p, grid, stream);
+    if (qpk <= 6u) return launch_tile_t2<FMT, D, 6, 1>(p, grid, stream);
+    if constexpr (fmt_psq<FMT>())
+        return launch_tile_t2<FMT, D, 8, 1>(p, grid, stream);
+    else
+        return launch_tile_t2<FMT, D, 4, 2>(p, grid, stream);
 }
 
-template <int KVB>
+template <int FMT>
 hipError_t launch_tile(const TileParams& p, hipStream_t stream) {
     switch (p.a.head_dim) {
-        case 256: return launch_tile_t<KVB, 256>(p, stream);
-        case 128: return launch_tile_t<KVB, 128>(p, stream);
-        case 64: return launch_tile_t<KVB, 64>(p, stream);
+        case 256: return launch_tile_t<FMT, 256>(p, stream);
+        case 128: return launch_tile_t<FMT, 128>(p, stream);
+        case 64:
+            if constexpr (!fmt_psq<FMT>()) return launch_tile_t<FMT, 64>(p, stream);
+            return hipErrorNotSupported;
         case 32:
-            if constexpr (KVB == 2) return launch_tile_t<2, 32>(p, stream);
+            if constexpr (FMT == kFmtBf16) return launch_tile_t<kFmtBf16, 32>(p, stream);
             return hipErrorNotSupported;
         default: return hipErrorNotSupported;
     }
+}
+
+// kv_dtype: PSK_KV_*; checked by the callers
+hipError_t launch_tile_fmt(const TileParams& p, uint32_t kv_dtype, hipStream_t stream) {
+    switch (kv_dtype) {
+        case PSK_KV_BF16: return launch_tile<kFmtBf16>(p, stream);
+        case PSK_KV_FP8_E4M3: return launch_tile<kFmtFp8>(p, stream);
+        case PSK_KV_PSQ8_W32: return launch_tile<kFmtPsq8>(p, stream);
+        case PSK_KV_PSQ4_W32: return launch_tile<kFmtPsq4>(p, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool known_kv(uint32_t kv_dtype) {
+    return kv_dtype == PSK_KV_BF16 || kv_dtype == PSK_KV_FP8_E4M3 || kv_dtype == PSK_KV_PSQ4_W32 ||
+           kv_dtype == PSK_KV_PSQ8_W32;
+}
+
+// PSQ scale pools: bf16 block scales, read by 4 B DMAs
+bool psq_scales_ok(uint32_t kv_dtype, const void* ks, const void* vs) {
+    if (kv_dtype != PSK_KV_PSQ4_W32 && kv_dtype != PSK_KV_PSQ8_W32) return true;
+    return ks != nullptr && vs != nullptr && reinterpret_cast<uintptr_t>(ks) % 4u == 0u &&
+           reinterpret_cast<uintptr_t>(vs) % 4u == 0u;
 }
 
 hipError_t tile_validate(const psk_paged_attention_args* a, const void* k, const void* v) {
@@ -888,22 +1069,23 @@ TileParams make_tile(const psk_paged_attention_args& c, const void* k, const voi
 // Tile launch over explicit tiles (row_begin, rows) of one launch, any
 // number of them (chunks of kInlineTiles per launch). Used by the step
 // planner; every tile's rows must belong to one sequence.
+// ks / vs: FP8 f32 scale pools, PSQ bf16 block-scale pools, BF16 unused.
 hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
-                              const void* v, const float* ks, const float* vs,
+                              const void* v, const void* ks, const void* vs,
                               const uint32_t* tile_begin, const uint32_t* tile_rows,
                               uint32_t n_tiles, uint32_t tiles_per_group, float* partials,
                               uint32_t splits, uint32_t pages_per_split, hipStream_t stream) {
     const hipError_t e = tile_validate(&a, k, v);
     if (e != hipSuccess) return e;
-    const int kvb = kv_dtype == PSK_KV_FP8_E4M3 ? 1 : 2;
-    if (!tile_shape_ok(a, kvb, k, v)) return hipErrorNotSupported;
+    if (!known_kv(kv_dtype)) return hipErrorInvalidValue;
+    if (!tile_shape_ok(a, kv_dtype, k, v) || !psq_scales_ok(kv_dtype, ks, vs)) return hipErrorNotSupported;
     if (splits > 1u && (partials == nullptr || pages_per_split == 0u)) return hipErrorInvalidValue;
     if (tiles_per_group != 1u &&
         (tiles_per_group != (uint32_t)kTileGroup || n_tiles % (uint32_t)kTileGroup != 0u))
         return hipErrorInvalidValue;
     for (uint32_t b = 0; b < n_tiles; b += kInlineTiles) {
-        TileParams p = make_tile(a, k, v, ks, vs, splits > 1u ? partials : nullptr, splits,
-                                 pages_per_split);
+        TileParams p = make_tile(a, k, v, static_cast<const float*>(ks), static_cast<const float*>(vs),
+                                 splits > 1u ? partials : nullptr, splits, pages_per_split);
         p.tiles_per_group = tiles_per_group;
         p.n_tiles = n_tiles - b < kInlineTiles ? n_tiles - b : kInlineTiles;
         for (uint32_t i = 0; i < p.n_tiles; ++i) {
@@ -914,7 +1096,7 @@ hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dty
             p.tile_begin[i] = tile_begin[b + i];
             p.tile_rows[i] = static_cast<uint8_t>(tile_rows[b + i]);
         }
-        const hipError_t le = kvb == 1 ? launch_tile<1>(p, stream) : launch_tile<2>(p, stream);
+        const hipError_t le = launch_tile_fmt(p, kv_dtype, stream);
         if (le != hipSuccess) return le;
     }
     return hipSuccess;
@@ -922,20 +1104,25 @@ hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dty
 
 // Tile workgroups that fit one CU: LDS (block-table window + pipeline
 // stages) and waves (3 per SIMD with one head per wave, 2 with two).
-uint32_t tile_workgroups_per_cu(int kvb, uint32_t head_dim, uint32_t q_per_kv) {
+// kv_dtype: PSK_KV_*.
+uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q_per_kv) {
     const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
-    const size_t stage = 2 * 2 * (16 * D * kvb + 128) + (kvb == 1 ? 2 * 2 * 256 : 0);
+    const size_t cb = kv_dtype == PSK_KV_BF16 ? 2 * D : kv_dtype == PSK_KV_PSQ4_W32 ? D / 2 : D;
+    const size_t stage = 2 * 2 * (16 * cb + 128) + (kv_dtype != PSK_KV_BF16 ? 2 * 2 * 256 : 0);
     const size_t lds = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * stage + 64;
     const uint32_t by_lds = (uint32_t)((160u * 1024u) / lds);
-    const uint32_t hpw = q_per_kv <= 4u ? 1u : 2u;
-    const uint32_t nw = q_per_kv <= 4u ? 4u : (q_per_kv + hpw - 1u) / hpw;
+    const bool psq = kv_dtype == PSK_KV_PSQ4_W32 || kv_dtype == PSK_KV_PSQ8_W32;
+    const uint32_t hpw = q_per_kv <= 4u || psq ? 1u : 2u;
+    const uint32_t nw = q_per_kv <= 4u ? 4u : psq ? (q_per_kv <= 6u ? 6u : 8u) : (q_per_kv + hpw - 1u) / hpw;
     const uint32_t by_waves = 4u * (uint32_t)tile_waves_per_simd((int)hpw) / nw;
     const uint32_t n = by_lds < by_waves ? by_lds : by_waves;
     return n == 0u ? 1u : n;
 }
 
-// Tiles per workgroup the step planner should group a prefill launch into.
-uint32_t tile_group_size(uint32_t q_per_kv) {
+// Tiles per workgroup the step planner should group a prefill launch into
+// (PSQ tiles are not grouped). kv_dtype: PSK_KV_*.
+uint32_t tile_group_size(uint32_t q_per_kv, uint32_t kv_dtype) {
+    if (kv_dtype == PSK_KV_PSQ4_W32 || kv_dtype == PSK_KV_PSQ8_W32) return 1u;
     return q_per_kv > 4u && q_per_kv <= 6u ? (uint32_t)kTileGroup : 1u;
 }
 
@@ -948,8 +1135,21 @@ uint64_t tile_launch_workgroups(uint64_t n_tiles, uint32_t tiles_per_group, uint
 }
 
 bool paged_tiles_supported(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
-                           const void* v) {
-    return tile_shape_ok(a, kv_dtype == PSK_KV_FP8_E4M3 ? 1 : 2, k, v);
+                           const void* v, const void* ks, const void* vs) {
+    return known_kv(kv_dtype) && tile_shape_ok(a, kv_dtype, k, v) && psq_scales_ok(kv_dtype, ks, vs);
+}
+
+// PSQ prefill tiles (the reference's launch_attention_paged_prefill_psq{4,8}):
+// implicit tiles of 16 rows; false when the shape is outside the tile kernel
+// (the caller then runs the rows on the decode kernel).
+bool launch_prefill_psq_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* kc,
+                              const void* vc, const void* ks, const void* vs, hipStream_t stream,
+                              hipError_t& err) {
+    if (!paged_tiles_supported(a, kv_dtype, kc, vc, ks, vs)) return false;
+    err = launch_tile_fmt(make_tile(a, kc, vc, static_cast<const float*>(ks), static_cast<const float*>(vs),
+                                    nullptr, 1u, 0u),
+                          kv_dtype, stream);
+    return true;
 }
 
 }  // namespace psk
@@ -962,10 +1162,10 @@ extern "C" int psk_attention_paged_prefill_bf16(const psk_paged_attention_args* 
                                                 const void* v_pool, void* stream) {
     const hipError_t e = psk::tile_validate(a, k_pool, v_pool);
     if (e != hipSuccess) return e;
-    if (!psk::tile_shape_ok(*a, 2, k_pool, v_pool))
+    if (!psk::tile_shape_ok(*a, PSK_KV_BF16, k_pool, v_pool))
         return psk_attention_paged_bf16(a, k_pool, v_pool, stream);
-    return psk::launch_tile<2>(psk::make_tile(*a, k_pool, v_pool, nullptr, nullptr, nullptr, 1u, 0u),
-                               static_cast<hipStream_t>(stream));
+    return psk::launch_tile<psk::kFmtBf16>(
+        psk::make_tile(*a, k_pool, v_pool, nullptr, nullptr, nullptr, 1u, 0u), static_cast<hipStream_t>(stream));
 }
 
 extern "C" int psk_attention_paged_prefill_fp8_e4m3(const psk_paged_attention_args* a,
@@ -975,28 +1175,29 @@ extern "C" int psk_attention_paged_prefill_fp8_e4m3(const psk_paged_attention_ar
     const hipError_t e = psk::tile_validate(a, k_pool, v_pool);
     if (e != hipSuccess) return e;
     if (k_scale_pool == nullptr || v_scale_pool == nullptr) return hipErrorInvalidValue;
-    if (!psk::tile_shape_ok(*a, 1, k_pool, v_pool))
+    if (!psk::tile_shape_ok(*a, PSK_KV_FP8_E4M3, k_pool, v_pool))
         return psk_attention_paged_fp8_e4m3(a, k_pool, v_pool, k_scale_pool, v_scale_pool, stream);
-    return psk::launch_tile<1>(
+    return psk::launch_tile<psk::kFmtFp8>(
         psk::make_tile(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, nullptr, 1u, 0u),
         static_cast<hipStream_t>(stream));
 }
 
 extern "C" int psk_attention_paged_tile_split(const psk_paged_attention_args* a, uint32_t kv_dtype,
                                               const void* k_pool, const void* v_pool,
-                                              const float* k_scale_pool, const float* v_scale_pool,
+                                              const void* k_scale_pool, const void* v_scale_pool,
                                               float* partials, uint32_t splits,
                                               uint32_t pages_per_split, void* stream) {
     const hipError_t e = psk::tile_validate(a, k_pool, v_pool);
     if (e != hipSuccess) return e;
     if (partials == nullptr || splits == 0u || splits > psk::kMaxTileSplits || pages_per_split == 0u)
         return hipErrorInvalidValue;
-    const int kvb = kv_dtype == PSK_KV_FP8_E4M3 ? 1 : 2;
-    if (kv_dtype != PSK_KV_FP8_E4M3 && kv_dtype != PSK_KV_BF16) return hipErrorInvalidValue;
-    if (kvb == 1 && (k_scale_pool == nullptr || v_scale_pool == nullptr)) return hipErrorInvalidValue;
-    if (!psk::tile_shape_ok(*a, kvb, k_pool, v_pool)) return hipErrorNotSupported;
-    const psk::TileParams p = psk::make_tile(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, partials,
-                                             splits, pages_per_split);
-    return kvb == 1 ? psk::launch_tile<1>(p, static_cast<hipStream_t>(stream))
-                    : psk::launch_tile<2>(p, static_cast<hipStream_t>(stream));
+    if (!psk::known_kv(kv_dtype)) return hipErrorInvalidValue;
+    if (kv_dtype != PSK_KV_BF16 && (k_scale_pool == nullptr || v_scale_pool == nullptr))
+        return hipErrorInvalidValue;
+    if (!psk::tile_shape_ok(*a, kv_dtype, k_pool, v_pool) || !psk::psq_scales_ok(kv_dtype, k_scale_pool, v_scale_pool))
+        return hipErrorNotSupported;
+    const psk::TileParams p =
+        psk::make_tile(*a, k_pool, v_pool, static_cast<const float*>(k_scale_pool),
+                       static_cast<const float*>(v_scale_pool), partials, splits, pages_per_split);
+    return psk::launch_tile_fmt(p, kv_dtype, static_cast<hipStream_t>(stream));
 }

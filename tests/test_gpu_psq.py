@@ -382,7 +382,113 @@ def test_planner_step_over_psq_pools(dev, fmt):
     plan = state.plan_step(a, KV_PSQ4 if fmt == 4 else KV_PSQ8, reqs, 3000, nbytes, part,
                            *pools, launch=True)
     torch.cuda.synchronize()
-    assert plan.count == 1 and plan.kernels[0].rows == 19
+    # decode rows 0-2 on the decode kernel, the verify block on the tile kernel
+    assert plan.count == 2 and plan.kernels[0].rows == 3 and plan.kernels[1].rows == 16
+    want = oracle_attn(lay, fmt, 24, q, slots, pos, lay.block_tables, pools)
+    assert np.max(np.abs(out.cpu().numpy() - want)) < TOL
+
+
+# ------------------------------------------------------------------ PSQ tiles
+def prefill_rows_case(dev, fmt, qh, kvh, D, P, prefix, rows, seed):
+    rng = np.random.default_rng(seed)
+    lay = paged_layout(rng, [prefix + rows], P, kvh, D, spare_pages=1)
+    pools = dev_pools(lay, fmt, dev, seed=seed)
+    slots = np.zeros(rows, np.uint32)
+    pos = np.arange(prefix, prefix + rows, dtype=np.uint32)
+    q = bf16_normal(rng, (rows, qh * D))
+    return lay, pools, slots, pos, q
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("qh,kvh,D,P", [
+    (24, 4, 256, 16),    # 6 one-head waves (the qwen35 group)
+    (32, 4, 256, 16),    # 8 one-head waves
+    (8, 2, 128, 16),     # 4 waves, head_dim 128
+    (24, 4, 256, 24),    # page 24: 16-token halves straddle pages
+])
+def test_prefill_tiles_match_oracle_and_decode(dev, fmt, qh, kvh, D, P):
+    """launch_attention_paged_prefill_psq{4,8} on the PSQ tile kernel: 50
+    causal rows (3 full tiles and a ragged one) after a 300-token prefix,
+    against the fp32 oracle and against the PSQ decode kernel on the same
+    rows (same exact K/V conversion, bf16 P: they differ by summation order)."""
+    lay, pools, slots, pos, q = prefill_rows_case(dev, fmt, qh, kvh, D, P, 300, 50,
+                                                  seed=qh + D + P + fmt)
+    bt = lay.block_tables
+    want = oracle_attn(lay, fmt, qh, q, slots, pos, bt, pools)
+    got = run_attn(dev, lay, fmt, qh, q, slots, pos, bt, pools, kind="prefill")
+    assert np.max(np.abs(got - want)) < TOL
+    dec = run_attn(dev, lay, fmt, qh, q, slots, pos, bt, pools)
+    assert np.max(np.abs(got - dec)) < 1e-2
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_tile_split_over_psq_pools(dev, fmt):
+    """psk_attention_paged_tile_split with PSQ pools and the shared combine:
+    explicit tiles of two sequences, split-K over the context."""
+    import ctypes as C
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8, lib, check
+    rng = np.random.default_rng(70 + fmt)
+    lens = [2000, 1200]
+    lay = paged_layout(rng, lens, 16, 4, 256, spare_pages=1)
+    pools = dev_pools(lay, fmt, dev, seed=70 + fmt)
+    # rows: 20 of sequence 0 (tiles of 16 + 4), 9 of sequence 1
+    slots = np.array([0] * 20 + [1] * 9, np.uint32)
+    pos = np.array(list(range(1980, 2000)) + list(range(1191, 1200)), np.uint32)
+    rows = len(slots)
+    q = bf16_normal(rng, (rows, 24 * 256))
+    bt = lay.block_tables
+    want = oracle_attn(lay, fmt, 24, q, slots, pos, bt, pools)
+    L = lib()
+    st = torch.cuda.current_stream().cuda_stream
+    for splits, pps in ((4, 32), (16, 8)):
+        out = torch.full((rows, 24 * 256), 7.0, dtype=torch.float32, device=dev)
+        part = torch.empty(ops.split_partials_bytes(rows, 24, 4, splits) // 4, device=dev)
+        a = ops.attention_args(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                               to_dev(bt), 24)
+        # implicit tiles [16t, 16t+16) would mix the sequences at rows 16-19:
+        # run the two sequences as two launches of their own rows
+        for r0, n in ((0, 20), (20, 9)):
+            sub = ops.attention_args(geom_of(lay), 0, to_dev(q[r0:r0 + n]), out[r0:r0 + n],
+                                     to_dev(slots[r0:r0 + n]), to_dev(pos[r0:r0 + n]),
+                                     to_dev(bt), 24)
+            check("tile_split", L.psk_attention_paged_tile_split(
+                C.byref(sub), KV_PSQ4 if fmt == 4 else KV_PSQ8, *(t.data_ptr() for t in pools),
+                part.data_ptr(), splits, pps, st))
+            check("reduce", L.psk_attention_paged_split_reduce_ex(C.byref(sub), part.data_ptr(),
+                                                                  splits, pps, st))
+        torch.cuda.synchronize()
+        assert np.max(np.abs(out.cpu().numpy() - want)) < TOL, (splits, pps)
+    # scale pools must be 4 B aligned for the block-scale DMAs
+    assert L.psk_attention_paged_tile_split(
+        C.byref(a), KV_PSQ4 if fmt == 4 else KV_PSQ8, pools[0].data_ptr(), pools[1].data_ptr(),
+        pools[2].data_ptr() + 2, pools[3].data_ptr(), part.data_ptr(), 4, 32, st) != 0
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_mixed_step_with_prefill_over_psq_pools(dev, fmt):
+    """A config-5-shaped step over PSQ pools through the planner: decode rows,
+    a 16-row verify block and a 160-row prefill chunk (tile launches), against
+    the oracle."""
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8, state
+    rng = np.random.default_rng(80 + fmt)
+    lens = [2500, 900, 600 + 16, 1000 + 160]
+    lay = paged_layout(rng, lens, 16, 4, 256, spare_pages=1)
+    pools = dev_pools(lay, fmt, dev, seed=80 + fmt)
+    slots = np.array([0, 1] + [2] * 16 + [3] * 160, np.uint32)
+    pos = np.array([2499, 899] + list(range(600, 616)) + list(range(1000, 1160)), np.uint32)
+    rows = len(slots)
+    q = bf16_normal(rng, (rows, 24 * 256))
+    out = torch.full((rows, 24 * 256), 7.0, dtype=torch.float32, device=dev)
+    a = ops.attention_args(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                           to_dev(lay.block_tables), 24)
+    nbytes = 256 << 20
+    part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    reqs = [(0, 1, 0, 2500), (1, 1, 0, 900), (2, 16, 1, 616), (18, 160, 2, 1160)]
+    plan = state.plan_step(a, KV_PSQ4 if fmt == 4 else KV_PSQ8, reqs, 2500, nbytes, part,
+                           *pools, launch=True)
+    torch.cuda.synchronize()
+    kinds = sorted((k.kind, k.rows) for k in plan.kernels[:plan.count])
+    assert kinds == [(0, 2), (1, 16), (1, 160)], kinds
     want = oracle_attn(lay, fmt, 24, q, slots, pos, lay.block_tables, pools)
     assert np.max(np.abs(out.cpu().numpy() - want)) < TOL
 

@@ -105,15 +105,18 @@ def test_choose_decode_split_export():
     assert sp == 1   # below the reference's 2048-token split threshold
 
 
-def test_psq_steps_run_every_row_on_decode():
-    """PSQ pools have no tile kernel: the config-5 request mix becomes one
-    decode launch over all rows, split by the chooser."""
+def test_psq_steps_use_tiles_where_the_tile_kernel_covers_them():
+    """PSQ pools at head_dim 256: the config-5 request mix plans like FP8 (decode
+    rows, one verify tile launch, one prefill tile launch); at head_dim 64 (outside the PSQ tile kernel) every row is a
+    decode row."""
     reqs = ([(i, 1, 0) for i in range(48)] + [(48 + 16 * i, 16, 1) for i in range(8)] +
             [(176 + 512 * i, 512, 2) for i in range(8)])
     for dt in (P.KV_PSQ4, P.KV_PSQ8):
         plan = state.plan_step(args(4272), dt, reqs, 16384, 256 << 20)
         ks = kernels(plan)
-        assert len(ks) == 1 and ks[0][:3] == (0, 0, 4272)
+        assert [k[:3] for k in ks] == [(0, 0, 48), (1, 48, 128), (1, 176, 4096)]
+        plan = state.plan_step(args(4272, hd=64), dt, reqs, 16384, 256 << 20)
+        assert [k[:3] for k in kernels(plan)] == [(0, 0, 4272)]
         plan = state.plan_step(args(64), dt, [(i, 1, 0) for i in range(64)], 32768, 1 << 30)
         assert kernels(plan)[0][3] > 1
 
