@@ -317,6 +317,52 @@ def run_psq(torch, ops, steps, warmup, dev):
                 frac_of_peak=round(nb_ / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
         del kin, vin, akc, avc, aks, avs
         torch.cuda.empty_cache()
+
+        # prefill: config 5's 8 chunks of 512 causal rows (contexts U[2k, 16k]
+        # before the chunk) on the PSQ tile kernel, and the same rows on the
+        # PSQ decode kernel (the row-by-row path the tiles replace)
+        rng = np.random.default_rng(5005)
+        pre = rng.integers(2048, 16385, 8)
+        lens = pre + 512
+        need = (lens + P - 1) // P
+        gp = ops.PoolGeometry(1, int(need.sum()), P, H, D)
+        stride = int(need.max())
+        perm = rng.permutation(int(need.sum())).astype(np.int32)
+        btp = np.full((8, stride), -1, np.int32)
+        o_ = 0
+        for r, n in enumerate(need):
+            btp[r, :n] = perm[o_:o_ + n]
+            o_ += n
+        nb, cb = gp.psq_blocks, gp.psq_code_bytes(fmt)
+        kc = torch.randint(0, 126, (cb,), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
+        vc = torch.randint(0, 126, (cb,), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
+        ks = (torch.rand(nb, generator=gen, device=dev) * 0.01 + 1e-3).to(torch.bfloat16)
+        vs = (torch.rand(nb, generator=gen, device=dev) * 0.01 + 1e-3).to(torch.bfloat16)
+        prow = 8 * 512
+        q = torch.randn((prow, QH * D), generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty((prow, QH * D), dtype=torch.bfloat16, device=dev)
+        pslots = torch.from_numpy(np.repeat(np.arange(8), 512).astype(np.int32)).to(dev)
+        ppos = torch.from_numpy(np.concatenate([np.arange(p0, p0 + 512) for p0 in pre]).astype(np.int32)).to(dev)
+        btd = torch.from_numpy(btp).to(dev)
+        flops = float(sum(int(p0) * 512 + 512 * 513 // 2 for p0 in pre)) * QH * D * 4
+        pt = {}
+        for kind, reps in (("prefill", steps), ("decode", 2)):
+            def launch():
+                ops.paged_attention_psq(gp, 0, q, out, pslots, ppos, btd, kc, vc, ks, vs, QH, fmt,
+                                        kind=kind)
+
+            warm(torch, launch, 1 if kind == "decode" else warmup)
+            t = Timer(torch)
+            with t:
+                for _ in range(reps):
+                    launch()
+            pt[kind] = t.ms() / reps
+        res[f"psq{fmt}_prefill_cfg5_chunks"] = dict(
+            rows=prow, tile_ms=round(pt["prefill"], 4), decode_path_ms=round(pt["decode"], 4),
+            tile_tflops=round(flops / (pt["prefill"] * 1e-3) / 1e12, 1),
+            speedup=round(pt["decode"] / pt["prefill"], 2))
+        del kc, vc, ks, vs, q, out
+        torch.cuda.empty_cache()
     return res
 
 
