@@ -3,6 +3,7 @@
 // full width.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <cstdint>
 
 namespace psk {
@@ -212,6 +213,19 @@ __device__ __forceinline__ uint32_t psq4_e4m3x4(uint32_t x, bool hi) {
     const uint32_t idx = (hi ? (x >> 4) : x) & 0x07070707u;
     const uint32_t mag = __builtin_amdgcn_perm(0x52504C48u, 0x44403800u, idx);
     return mag | ((hi ? x : (x << 4)) & 0x80808080u);
+}
+
+// Raises kernel fn's dynamic LDS limit to the CU's 160 KB (less 1 KB of
+// static LDS) on the current device, once per device: `done` holds one bit per
+// device index that is already set up (devices past 63 are set up on every call).
+inline hipError_t allow_full_lds(const void* fn, std::atomic<uint64_t>& done) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hipErrorInvalidDevice;
+    const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t{1} << dev) : 0u;
+    if (bit != 0u && (done.load(std::memory_order_acquire) & bit) != 0u) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+    if (e == hipSuccess && bit != 0u) done.fetch_or(bit, std::memory_order_release);
+    return e;
 }
 
 }  // namespace psk

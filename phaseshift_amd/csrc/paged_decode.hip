@@ -889,9 +889,9 @@ hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t st
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
-        static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_decode_kernel<FMT, D, kIndep, NW>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+        static std::atomic<uint64_t> lds_ready{0};
+        const hipError_t attr =
+            allow_full_lds(reinterpret_cast<const void*>(&paged_decode_kernel<FMT, D, kIndep, NW>), lds_ready);
         if (attr != hipSuccess) return attr;
     }
     hipLaunchKernelGGL((paged_decode_kernel<FMT, D, kIndep, NW>), dim3((uint32_t)grid),

@@ -946,9 +946,9 @@ hipError_t launch_tile_t3(const TileParams& p, uint64_t grid, hipStream_t stream
     const size_t lds_bytes = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * tile_stage_bytes<FMT, D>();
     if (lds_bytes > 64u * 1024u) {
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
-        static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&paged_tile_kernel<FMT, D, NW, HPW, RT, kAl16>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+        static std::atomic<uint64_t> lds_ready{0};
+        const hipError_t attr =
+            allow_full_lds(reinterpret_cast<const void*>(&paged_tile_kernel<FMT, D, NW, HPW, RT, kAl16>), lds_ready);
         if (attr != hipSuccess) return attr;
     }
     hipLaunchKernelGGL((paged_tile_kernel<FMT, D, NW, HPW, RT, kAl16>), dim3((uint32_t)grid),
