@@ -1,7 +1,9 @@
-"""The PSQ4 append kernel's branch-free cb10 magnitude index equals the
-reference's comparison chain (psq_device.h:22-31) for every non-negative
-float bit pattern, NaNs and +inf included. Exhaustive, on the CPU (IEEE
-fmin/fmax/ceil/fma are the device's v_min/v_max/v_ceil/v_fma)."""
+"""The PSQ4 append kernel's branch-free cb10 code (a 3-bit lookup of
+min(ceil(|x| * 2/s), 19)) equals the reference's comparison chain
+(psq_device.h:22-31): exhaustively for every non-negative float bit pattern
+(NaNs and +inf included) and for 2^26 random (x, bf16 scale) pairs, on the CPU
+(IEEE fminf/ceilf and one rounding per multiply are the device's v_min,
+v_ceil and v_mul)."""
 import os
 import subprocess
 
