@@ -315,13 +315,6 @@ __device__ __forceinline__ uint32_t cb10_code(float x, float inv2) {
     return m | (x < 0.0f ? 8u : 0u);   // -0.0 and NaN: no sign, as the reference
 }
 
-// cb10 value of a code: magnitudes 0 1 2 3 4 6 8 10.
-__device__ __forceinline__ float cb10_value(uint32_t c) {
-    const uint32_t m = c & 7u;
-    const float mag = (float)(m < 5u ? m : 2u * m - 4u);
-    return (c & 8u) ? -mag : mag;
-}
-
 // Codes of the 32 values for scale s (all 0 unless s > 0): PSQ4 cb10 codes of
 // x * (1/s), PSQ8 SATFINITE E4M3 codes of x * (1/s) packed 4 per dword.
 template <bool kPsq4>
@@ -408,16 +401,21 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
         // reference's butterfly order; s1 = bf16(num / den), then re-encode
         float nm[32], dn[32];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            float q;
-            if constexpr (kPsq4) {
-                q = cb10_value(c[i]);
-            } else {
-                const f32x2 q2 = __builtin_amdgcn_cvt_pk_f32_fp8(c[i >> 2] >> (16 * ((i >> 1) & 1)), false);
-                q = (i & 1) ? q2[1] : q2[0];
+        for (int i = 0; i < 32; i += 4) {
+            // PSQ4: 4 codes -> their E4M3 bytes (cb10 magnitudes 0 1 2 3 4
+            // 6 8 10 are exact in E4M3, code 8 is -0) -> f32 by the hardware
+            // conversion, as PSQ8's codes
+            const uint32_t w = kPsq4 ? psq4_e4m3x4(c[i] | (c[i + 1] << 8) | (c[i + 2] << 16) | (c[i + 3] << 24),
+                                                   false)
+                                     : c[i >> 2];
+            const f32x2 q01 = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+            const f32x2 q23 = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+            const float q[4] = {q01[0], q01[1], q23[0], q23[1]};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                nm[i + j] = x[i + j] * q[j];
+                dn[i + j] = q[j] * q[j];
             }
-            nm[i] = x[i] * q;
-            dn[i] = q * q;
         }
         const float num = butterfly_sum32(nm);
         const float den = butterfly_sum32(dn);
