@@ -672,9 +672,9 @@ def cpu_baseline(lens_row, seconds_cap=30.0):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the KV path needs no collective; "
-              "sharding is by KV head / batch row, see DESIGN.md); run with --gpus 1",
-              file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the KV path needs no collective: "
+              "it shards by KV head or batch row, each GPU running these kernels on its own "
+              "pool); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
     from phaseshift_amd import ops
