@@ -136,6 +136,26 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
         for (uint32_t r = 0; r < rows; ++r)
             pages[r] = std::min(max_pages, (row_visible[r] + page_tokens - 1) / page_tokens);
     const uint32_t q_per_kv = q_heads / kv_heads;
+    // The last few choices of this thread, keyed by every input: decode steps
+    // repeat them until a row crosses a page (every page_tokens steps for a
+    // long row), and a long context with few rows is the costly simulation.
+    struct Memo {
+        std::vector<uint64_t> key;
+        DecodeSplit val;
+    };
+    thread_local Memo memo[4];
+    thread_local uint32_t memo_next = 0;
+    std::vector<uint64_t> key = {rows, kv_heads, q_heads, head_dim, kv_dtype, page_tokens, max_pages,
+                                 partial_bytes, device_cus()};
+    key.insert(key.end(), pages.begin(), pages.end());
+    for (const Memo& m : memo)
+        if (m.key == key) return m.val;
+    auto remember = [&](const DecodeSplit& v) {
+        memo[memo_next].key = key;
+        memo[memo_next].val = v;
+        memo_next = (memo_next + 1u) % 4u;
+        return v;
+    };
     const uint32_t groups = (kv_heads + 3u) / 4u;   // independent-wave workgroups per unit
     const size_t lds = psk::decode_workgroup_lds_bytes(kv_dtype, head_dim);
     const uint32_t per_cu = std::max<uint32_t>(1u, (uint32_t)((160u * 1024u) / lds));
@@ -203,13 +223,13 @@ DecodeSplit choose_decode_split(uint32_t rows, uint32_t kv_heads, uint32_t q_hea
         const double shared = n_units * groups >= 128 ? 1.0 : 1.1;
         cands.push_back({split_makespan(units, slots, xcd_bw, wg_bw, c0) * shared, splits, per});
     }
-    if (cands.empty()) return best;
+    if (cands.empty()) return remember(best);
     const Cand* pick = &cands[0];
     for (const Cand& c : cands)
         if (c.t < pick->t) pick = &c;
     best.splits = pick->splits;
     best.pages_per_split = pick->per;
-    return best;
+    return remember(best);
 }
 
 namespace {
