@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,psq,prefix,graph")
+    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,psq,prefix,graph,loop,dropin")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times), the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -507,6 +507,136 @@ def run_step_graph(torch, ops, steps, warmup, dev):
     return res
 
 
+def run_dropin_unpatched(torch, ops, steps, warmup, dev):
+    """What an unmodified PhaseShift dispatcher gets when it links this library:
+    it calls the reference-signature launchers (ps::kernel::launch_*, by their
+    mangled names) the way paged_attention_dispatch.hip:437-477,790-894 does —
+    FP8 KV unsplit (its plan admits no FP8 split) at the north-star batch 64 x
+    32k, and BF16 at its fixed 16 splits + the bf16 reduce at BASELINE config 3.
+    Kernel times from HIP events on the launch stream."""
+    import ctypes as C
+    import phaseshift_amd
+    cdll = C.CDLL(phaseshift_amd.LIB_PATH)
+    P, U = C.c_void_p, C.c_uint32
+    fp8_fn = cdll["_ZN2ps6kernel31launch_attention_paged_fp8_e4m3ERKNS0_24PagedAttentionCommonArgs"
+                  "EPKhS5_PKfS7_P12ihipStream_t"]
+    fp8_fn.argtypes, fp8_fn.restype = [P] * 6, C.c_int
+    sp_fn = cdll["_ZN2ps6kernel33launch_attention_paged_bf16_splitERKNS0_24PagedAttentionCommonArgs"
+                 "EPKNS_6bf16_tES6_PfjP12ihipStream_t"]
+    sp_fn.argtypes, sp_fn.restype = [P, P, P, P, U, P], C.c_int
+    rd_fn = cdll["_ZN2ps6kernel40launch_attention_paged_bf16_split_reduceERKNS0_24PagedAttentionCommonArgs"
+                 "EPKfjP12ihipStream_t"]
+    rd_fn.argtypes, rd_fn.restype = [P, P, U, P], C.c_int
+    s = torch.cuda.current_stream().cuda_stream
+    res = {}
+
+    def timed(fn):
+        warm(torch, fn, warmup)
+        t = Timer(torch)
+        with t:
+            for _ in range(steps):
+                fn()
+        return t.ms() / steps
+
+    st = decode_setup(torch, ops, [32768] * 64, True, 11, dev)
+    a = ops.attention_args(st["g"], 0, st["q"], st["out"], st["slots"], st["pos"], st["bt"], st["QH"])
+    ptrs = (st["kp"].data_ptr(), st["vp"].data_ptr(), st["ks"].data_ptr(), st["vs"].data_ptr())
+
+    def fp8_unsplit():
+        assert fp8_fn(C.addressof(a), *ptrs, s) == 0
+
+    ms = timed(fp8_unsplit)
+    nb = 64 * 32768 * BYTES_PER_TOKEN_FP8 + 64 * 24 * 256 * 2
+    res["fp8_unsplit_b64_ctx32k"] = dict(kernel_ms=round(ms, 4), GBps=round(nb / (ms * 1e-3) / 1e9, 1),
+                                         frac_of_peak=round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+    del st, a
+    torch.cuda.empty_cache()
+    rng = np.random.default_rng(303)
+    lens = rng.integers(1024, 32769, 32)
+    st = decode_setup(torch, ops, lens, False, 303, dev)
+    a = ops.attention_args(st["g"], 0, st["q"], st["out"], st["slots"], st["pos"], st["bt"], st["QH"])
+    part = torch.empty(ops.split_partials_bytes(32, 24, 4, 16) // 4, dtype=torch.float32, device=dev)
+    kp, vp = st["kp"].data_ptr(), st["vp"].data_ptr()
+
+    def split16():
+        assert sp_fn(C.addressof(a), kp, vp, part.data_ptr(), 16, s) == 0
+
+    def reduce16():
+        assert rd_fn(C.addressof(a), part.data_ptr(), 16, s) == 0
+
+    step_ms = timed(lambda: (split16(), reduce16()))
+    k_ms = timed(split16)
+    nb = float(lens.sum()) * BYTES_PER_TOKEN_BF16 + 32 * 24 * 256 * 2
+    res["bf16_split16_cfg3"] = dict(ms_per_step=round(step_ms, 4), split_kernel_ms=round(k_ms, 4),
+                                    GBps=round(nb / (step_ms * 1e-3) / 1e9, 1),
+                                    frac_of_peak=round(nb / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+    del st, a, part
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_decode_loop(torch, ops, dev, n_steps=64):
+    """Continuous decode at BASELINE config 4 (64 rows, FP8, ctx log-U[4k,64k]):
+    n_steps consecutive steps through psk_paged_attention_step (plan + split
+    launch + combine), every row's position advancing by one token per step and
+    each request carrying its row's visible length, as a serving loop sees
+    them. Host time is the C-ABI call alone (request arrays are built before
+    the loop); GPU time is HIP events around the whole loop. The device
+    positions advance by a small fill between steps, outside both figures'
+    planning but inside the GPU time."""
+    import ctypes as C
+    from phaseshift_amd import KV_FP8, StepPlan, StepRequest, check, lib
+    from phaseshift_amd.ops import _stream
+    rng = np.random.default_rng(404)
+    lens = np.exp(rng.uniform(np.log(4096), np.log(65536), 64)).astype(np.int64)
+    st = decode_setup(torch, ops, lens + n_steps + 1, True, 404, dev)
+    rows = len(lens)
+    pos = torch.tensor(lens - 1, dtype=torch.int32, device=dev)
+    a = ops.attention_args(st["g"], 0, st["q"], st["out"], st["slots"], pos, st["bt"], st["QH"])
+    pbytes = 64 << 20
+    part = torch.empty(pbytes // 4, dtype=torch.float32, device=dev)
+    L = lib()
+    s = _stream(None)
+    ptrs = (st["kp"].data_ptr(), st["vp"].data_ptr(), st["ks"].data_ptr(), st["vs"].data_ptr())
+    one = torch.ones(rows, dtype=torch.int32, device=dev)
+    req_sets = []
+    for i in range(n_steps + 1):
+        rq = (StepRequest * rows)()
+        for r in range(rows):
+            rq[r].row_begin, rq[r].row_count, rq[r].execution_class = r, 1, 0
+            rq[r].max_visible = int(lens[r]) + i
+        req_sets.append((rq, int(lens.max()) + i))
+    plan = StepPlan()
+
+    def step(i):
+        rq, mv = req_sets[i]
+        h0 = time.perf_counter_ns()
+        check("psk_paged_attention_step", L.psk_paged_attention_step(
+            C.byref(a), KV_FP8, *ptrs, rq, rows, mv, part.data_ptr(), pbytes, C.byref(plan), s))
+        h = time.perf_counter_ns() - h0
+        pos.add_(one)
+        return h
+
+    # the first plan of the batch (cold: the chooser simulates)
+    cold_us = step(0) / 1e3
+    torch.cuda.synchronize()
+    t = Timer(torch)
+    host = []
+    with t:
+        for i in range(1, n_steps + 1):
+            host.append(step(i))
+    gpu_ms = t.ms() / n_steps
+    host_us = np.asarray(host, np.float64) / 1e3
+    splits = [int(plan.kernels[0].splits), int(plan.kernels[0].pages_per_split)]
+    del st
+    torch.cuda.empty_cache()
+    return dict(steps=n_steps, host_us_per_step_mean=round(float(host_us.mean()), 2),
+                host_us_per_step_p50=round(float(np.median(host_us)), 2),
+                host_us_per_step_max=round(float(host_us.max()), 2),
+                first_plan_host_us=round(cold_us, 1), gpu_ms_per_step=round(gpu_ms, 4),
+                last_plan_splits_pages=splits)
+
+
 def run_mixed_step(torch, ops, steps, warmup, dev):
     """BASELINE config 5, one continuous-batching step on the device: row
     metadata from the request descriptors, KV append (fused FP8 quantization) of
@@ -669,6 +799,56 @@ def cpu_baseline(lens_row, seconds_cap=30.0):
                        f"{en:.1f} s; {d1} rows on 1 thread in {e1:.1f} s")
 
 
+def cpu_baseline_append(rows=1 << 16, budget_s=5.0):
+    """Scalar C oracle of the FP8 KV append (or_kv_append_fp8, the restatement
+    of kv_append.hip:127-272) on the 2^16-row workload of the GPU append line
+    (4 kv heads, hd 256, page 16, rows scattered over 4096 sequences), single
+    threaded and on a thread pool over row chunks (rows of distinct (slot,
+    position) write disjoint pool entries), each for about budget_s seconds."""
+    import concurrent.futures as cf
+    import oracle
+    H, D, P = 4, 256, 16
+    rng = np.random.default_rng(7)
+    seqs = max(1, rows // P)
+    num_pages = seqs + 16
+    bt = rng.permutation(num_pages)[:seqs].astype(np.uint32).reshape(seqs, 1)
+    perm = rng.permutation(rows)
+    slots = np.repeat(np.arange(seqs), P)[:rows].astype(np.uint32)[perm]
+    pos = np.tile(np.arange(P), seqs)[:rows].astype(np.uint32)[perm]
+    k = oracle.f32_to_bf16(rng.standard_normal((rows, H * D), dtype=np.float32))
+    v = oracle.f32_to_bf16(rng.standard_normal((rows, H * D), dtype=np.float32))
+    n = num_pages * P * H * D
+    kp, vp = np.zeros(n, np.uint8), np.zeros(n, np.uint8)
+    ks, vs = np.zeros(n // D, np.float32), np.zeros(n // D, np.float32)
+    geom = dict(layer=0, page_tokens=P, num_pages=num_pages, num_attention_layers=1, kv_heads=H,
+                head_dim=D, block_table_stride=1, max_sequences=seqs)
+
+    def chunk(a, b):
+        oracle.kv_append(geom, k[a:b], v[a:b], slots[a:b], pos[a:b], bt, kp, vp, ks, vs)
+
+    def timed(threads):
+        done, t0 = 0, time.perf_counter()
+        bounds = np.linspace(0, rows, threads * 4 + 1).astype(int)
+        while time.perf_counter() - t0 < budget_s:
+            if threads == 1:
+                chunk(0, rows)
+            else:
+                with cf.ThreadPoolExecutor(threads) as ex:
+                    list(ex.map(lambda i: chunk(bounds[i], bounds[i + 1]), range(len(bounds) - 1)))
+            done += rows
+        el = time.perf_counter() - t0
+        return done, el, done / el
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    d1, e1, t1 = timed(1)
+    dn, en, tn = timed(threads) if threads > 1 else (d1, e1, t1)
+    return dict(tokens_per_s=round(tn, 1), GBps=round(tn * APPEND_BYTES_PER_ROW_FP8 / 1e9, 4),
+                cores=threads, single_thread_tokens_per_s=round(t1, 1), kind="port",
+                sample=f"FP8 append of {rows} rows (4 kv heads, hd 256), scalar C oracle (gcc -O2): "
+                       f"{dn} rows on {threads} threads in {en:.1f} s; {d1} rows on 1 thread in "
+                       f"{e1:.1f} s")
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -688,7 +868,7 @@ def main():
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 5}))
         return
     only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5", "psq",
-                                                     "prefix", "graph"}
+                                                     "prefix", "graph", "loop", "dropin"}
     extra = {}
 
     # ---- main: north-star point, FP8 batch 64 @ 32k
@@ -742,12 +922,22 @@ def main():
     if "graph" in only:
         extra["step_graph_fp8"] = run_step_graph(torch, ops, args.steps, args.warmup, dev)
 
+    if "dropin" in only:
+        extra["dropin_unpatched_dispatcher"] = run_dropin_unpatched(torch, ops, args.steps,
+                                                                    args.warmup, dev)
+
+    if "loop" in only:
+        extra["cfg4_decode_loop_planned"] = run_decode_loop(torch, ops, dev)
+
     if "cfg5" in only:
         extra["cfg5_mixed_step"] = run_mixed_step(torch, ops, max(5, args.steps // 2),
                                                   args.warmup, dev)
         torch.cuda.empty_cache()
 
-    cpu = None if args.no_cpu else cpu_baseline(32768)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(32768)
+        cpu["kv_append_fp8"] = cpu_baseline_append()
     line = {
         "metric": "paged decode-attn HBM GB/s (% of 8 TB/s peak) + KV-append tokens/s, 1 GPU",
         "value": round(value, 2),

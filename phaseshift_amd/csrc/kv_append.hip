@@ -302,15 +302,17 @@ __device__ __forceinline__ float psq_bf16_round(float v) {
 // cb10_encode (psq_device.h:22-35): magnitude index of a = |x| * inv against
 // the midpoints 0.5 1.5 2.5 3.5 5 7 9 (7 above 9 and for NaN), sign in bit 3.
 // Computed without comparisons from k = ceil(2a), see below. Equal to the
-// reference's chain for every float a >= 0 and for 2^26 random (x, bf16
+// reference's chain for every float a >= 0, for every positive bf16 scale
+// (subnormals included) over a spread of x, and for 2^26 random (x, bf16
 // scale) pairs, checked on the CPU (tests/native/cb10_branchless.c).
-__device__ __forceinline__ uint32_t cb10_code(float x, float inv2) {
+__device__ __forceinline__ uint32_t cb10_code(float x, float inv) {
     // The code boundaries a > 0.5, 1.5, 2.5, 3.5, 5, 7, 9 of a = |x| * inv are
-    // thresholds on k = ceil(2a) = ceil(|x| * inv2), inv2 = 2 * inv (scaling by 2
-    // commutes with the rounding; below the normal range ceil gives 1 either
-    // way): code(k) for k = 0..19 in 3-bit fields; NaN and Inf give k = 19 (7).
+    // thresholds on k = ceil(2a): code(k) for k = 0..19 in 3-bit fields; NaN and
+    // Inf give k = 19 (7). The doubling follows the product, so it is exact
+    // whenever a is finite and overflows only where a > 9 already gives 7 (a
+    // precomputed 2 * inv would overflow for subnormal scales with a finite).
     constexpr uint64_t kLut = 0x0fb6d6db246d2240ull;
-    const float k = __builtin_fminf(__builtin_ceilf(__builtin_fabsf(x) * inv2), 19.0f);
+    const float k = __builtin_fminf(__builtin_ceilf((__builtin_fabsf(x) * inv) * 2.0f), 19.0f);
     const uint32_t m = (uint32_t)(kLut >> (3u * (uint32_t)k)) & 7u;
     return m | (x < 0.0f ? 8u : 0u);   // -0.0 and NaN: no sign, as the reference
 }
@@ -323,9 +325,8 @@ __device__ __forceinline__ void psq_codes(const float (&x)[32], float s, uint32_
     const float inv = 1.0f / s;
     const uint32_t keep = s > 0.0f ? 0xFFFFFFFFu : 0u;   // all codes 0 unless s > 0
     if constexpr (kPsq4) {
-        const float inv2 = 2.0f * inv;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) c[i] = cb10_code(x[i], inv2) & keep;
+        for (int i = 0; i < 32; ++i) c[i] = cb10_code(x[i], inv) & keep;
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i += 4) {

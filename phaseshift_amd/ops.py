@@ -75,9 +75,26 @@ def _check_u32(*ts):
             raise TypeError("row metadata and block tables must be 32-bit integer tensors")
 
 
+def _check_append_input(geom: PoolGeometry, k_in, v_in):
+    """The launchers read each input row as kv_heads*head_dim packed bf16 values
+    (kv_append.hip:21-49): any other dtype, a non-unit inner stride or a short
+    row would be read as garbage codes, so reject them here."""
+    width = geom.kv_heads * geom.head_dim
+    for name, t in (("k_in", k_in), ("v_in", v_in)):
+        if t.dtype not in (torch.bfloat16, torch.int16, torch.uint16):
+            raise TypeError(f"{name} must hold bf16 values (bfloat16 or its int16 bits), got {t.dtype}")
+        if t.dim() != 2 or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be a 2-D [rows, >= kv_heads*head_dim] tensor with unit inner stride")
+        if t.shape[1] < width or t.stride(0) < width:
+            raise ValueError(f"{name} rows must hold kv_heads*head_dim = {width} values")
+    if k_in.shape[0] != v_in.shape[0]:
+        raise ValueError("k_in and v_in must have the same number of rows")
+
+
 def append_args(geom: PoolGeometry, layer: int, k_in, v_in, slots, positions, block_tables,
                 max_sequences: int | None = None) -> KvAppendArgs:
     _check_u32(slots, positions, block_tables)
+    _check_append_input(geom, k_in, v_in)
     a = KvAppendArgs()
     a.k_input, a.v_input = _ptr(k_in), _ptr(v_in)
     a.k_row_stride, a.v_row_stride = k_in.stride(0), v_in.stride(0)

@@ -143,3 +143,25 @@ def oracle_attention_psq_parallel(geom, q, slots, positions, block_tables, kc, v
     with ThreadPoolExecutor(len(bounds) - 1) as ex:
         list(ex.map(job, range(len(bounds) - 1)))
     return out
+
+
+def assert_attention_close(got, want, tol_abs, rel=1e-2, what=""):
+    """Attention parity: the north-star max-abs bound over every value, and a
+    per-row bound relative to that row's largest oracle output, so rows whose
+    outputs are small (long, flat softmaxes) are still held to the oracle.
+    Set PSK_ERR_LOG to a path to append the observed errors there."""
+    import os
+    got = np.asarray(got, np.float64).reshape(len(want), -1)
+    want = np.asarray(want, np.float64).reshape(len(want), -1)
+    err = np.abs(got - want)
+    row_err = err.max(axis=1)
+    row_max = np.abs(want).max(axis=1)
+    worst_rel = float(np.max(row_err / np.maximum(row_max, 1e-30)))
+    log = os.environ.get("PSK_ERR_LOG")
+    if log:
+        with open(log, "a") as f:
+            f.write(f"{what} abs={err.max():.3e} rel={worst_rel:.3e} rowmax_min={row_max.min():.3e}\n")
+    assert np.all(np.isfinite(got)), what
+    assert err.max() < tol_abs, (what, float(err.max()))
+    bad = np.nonzero(row_err > rel * row_max + 1e-6)[0]
+    assert bad.size == 0, (what, "row", int(bad[0]), float(row_err[bad[0]]), float(row_max[bad[0]]))

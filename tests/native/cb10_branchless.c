@@ -1,11 +1,15 @@
 /* Check: the branch-free cb10 code of the PSQ4 append kernel
- * (phaseshift_amd/csrc/kv_append.hip, cb10_code: k = min(ceil(|x| * 2inv), 19)
+ * (phaseshift_amd/csrc/kv_append.hip, cb10_code: k = min(ceil((|x| * inv) * 2), 19)
  * and a 3-bit lookup of k) equals the reference's comparison chain
  * (psq_device.h:22-31, restated as or_cb10_encode in oracle/ps_oracle.c):
  *   1. exhaustively for every float bit pattern x >= 0 at inv = 1 (including
  *      +inf and every NaN), i.e. for every |x| * inv;
  *   2. for 2^26 random (x, bf16 scale) pairs over 2^-80 .. 2^20 magnitudes,
- *      with inv = 1 / s as the kernel computes it, signs included.
+ *      with inv = 1 / s as the kernel computes it, signs included;
+ *   3. for every positive bf16 scale 0x0001..0x7F7F, subnormals included
+ *      (where 2 / s overflows while 1 / s is finite), against 2048 x values
+ *      each: 0, the code boundaries times s and their float neighbours, and
+ *      random x of magnitude 2^-39 .. 2^13 times s.
  * Uses the same IEEE operations as the device code: fminf (NaN -> other
  * operand), ceilf, one rounding per multiply. */
 #include <math.h>
@@ -16,9 +20,8 @@
 uint8_t or_cb10_encode(float x, float inv_scale);
 
 static uint32_t lut_code(float x, float inv) {
-    const float inv2 = 2.0f * inv;
     const uint64_t lut = 0x0fb6d6db246d2240ull;   /* code(k), k = 0..19, 3 bits each */
-    const float k = fminf(ceilf(fabsf(x) * inv2), 19.0f);
+    const float k = fminf(ceilf((fabsf(x) * inv) * 2.0f), 19.0f);
     const uint32_t m = (uint32_t)(lut >> (3u * (uint32_t)k)) & 7u;
     return m | (x < 0.0f ? 8u : 0u);
 }
@@ -59,6 +62,41 @@ int main(void) {
         if (lut_code(x, inv) != want) {
             if (bad < 16) printf("mismatch x=%a s=%a: %u vs %u\n", x, s, lut_code(x, inv), want);
             ++bad;
+        }
+    }
+    static const float kBounds[7] = {0.5f, 1.5f, 2.5f, 3.5f, 5.0f, 7.0f, 9.0f};
+#pragma omp parallel for reduction(+ : bad) schedule(dynamic, 64)
+    for (int32_t sbits = 1; sbits <= 0x7F7F; ++sbits) {
+        const uint32_t sb = (uint32_t)sbits << 16;
+        float s;
+        memcpy(&s, &sb, 4);
+        const float inv = 1.0f / s;
+        uint64_t st = 0x243F6A8885A308D3ull ^ ((uint64_t)sbits * 0x9E3779B97F4A7C15ull);
+        for (int j = 0; j < 2048; ++j) {
+            float x;
+            if (j == 0) {
+                x = 0.0f;
+            } else if (j <= 42) {
+                const float b = kBounds[(j - 1) % 7] * s;     /* boundary times s */
+                const int nb = (j - 1) / 7;                    /* 0..5: neighbours */
+                x = nb == 0 ? b : nb == 1 ? nextafterf(b, 0.0f) : nb == 2 ? nextafterf(b, INFINITY)
+                  : nb == 3 ? -b : nb == 4 ? nextafterf(nextafterf(b, 0.0f), 0.0f)
+                  : nextafterf(nextafterf(b, INFINITY), INFINITY);
+            } else {
+                st ^= st << 13;
+                st ^= st >> 7;
+                st ^= st << 17;
+                const int e = (int)(st >> 58) - 12;             /* -12 .. 51 */
+                const float m = 1.0f + (float)((st >> 20) & 0xFFFFF) / 1048576.0f;
+                x = ldexpf(m, e > 12 ? e - 52 : e) * s;   /* 2^-39 .. 2^13 */
+                if (st & 1u) x = -x;
+            }
+            const uint32_t want = or_cb10_encode(x, inv);
+            const uint32_t got = lut_code(x, inv);
+            if (got != want) {
+                if (bad < 24) printf("mismatch x=%a s=%a: %u vs %u\n", x, s, got, want);
+                ++bad;
+            }
         }
     }
     printf("mismatches %llu\n", (unsigned long long)bad);

@@ -1,8 +1,9 @@
 """The PSQ4 append kernel's branch-free cb10 code (a 3-bit lookup of
-min(ceil(|x| * 2/s), 19)) equals the reference's comparison chain
-(psq_device.h:22-31): exhaustively for every non-negative float bit pattern
-(NaNs and +inf included) and for 2^26 random (x, bf16 scale) pairs, on the CPU
-(IEEE fminf/ceilf and one rounding per multiply are the device's v_min,
+min(ceil((|x| * inv) * 2), 19), inv = 1/s) equals the reference's comparison
+chain (psq_device.h:22-31): exhaustively for every non-negative float bit
+pattern (NaNs and +inf included), for every positive bf16 scale (subnormals
+included) over a spread of x, and for 2^26 random (x, bf16 scale) pairs, on the
+CPU (IEEE fminf/ceilf and one rounding per multiply are the device's v_min,
 v_ceil and v_mul)."""
 import os
 import subprocess

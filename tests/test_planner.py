@@ -1,6 +1,8 @@
 """Step planner (host logic, no GPU): region rules of the reference
 (paged_attention_dispatch.hip:705-788) plus the tile routing of verify blocks
 and the split sizing. Runs the C-ABI in plan-only mode."""
+import numpy as np
+import pytest
 import phaseshift_amd as P
 from phaseshift_amd import state
 
@@ -218,3 +220,69 @@ def test_split_chooser_against_measured_sweep():
         assert pp in measured, (name, sp, pp)
         best = min(measured.values())
         assert measured[pp] <= 1.05 * best, (name, pp, measured[pp], best)
+
+
+def test_append_rejects_inputs_it_would_misread():
+    """kv_append / kv_append_psq read each input row as kv_heads*head_dim packed
+    bf16 values: float32, transposed or short inputs are rejected up front."""
+    import torch
+    from phaseshift_amd import ops
+    g = ops.PoolGeometry(1, 8, 16, 4, 64)
+    i32 = lambda *s: torch.zeros(s, dtype=torch.int32)
+    good = torch.zeros((3, 4 * 64), dtype=torch.bfloat16)
+    ops.append_args(g, 0, good, good, i32(3), i32(3), i32(2, 4))
+    for bad, exc in ((torch.zeros((3, 256)), TypeError),
+                     (torch.zeros((256, 3), dtype=torch.bfloat16).t(), ValueError),
+                     (torch.zeros((3, 255), dtype=torch.bfloat16), ValueError),
+                     (torch.zeros((4, 256), dtype=torch.bfloat16), ValueError)):
+        with pytest.raises(exc):
+            ops.append_args(g, 0, good, bad, i32(3), i32(3), i32(2, 4))
+
+
+def _fresh_split(*args, **kw):
+    """psk_choose_decode_split in a new thread: its plan memo is thread-local,
+    so this is a computation from scratch."""
+    import threading
+    from phaseshift_amd import ops
+    out = []
+    t = threading.Thread(target=lambda: out.append(ops.choose_decode_split(*args, **kw)))
+    t.start()
+    t.join()
+    return out[0]
+
+
+def test_split_memo_reuse_rules():
+    """The chooser's per-thread plan memo: identical inputs give the fresh
+    answer in any A, B, A order; a plan is reused across small page drifts
+    only while it stays valid (no row needs more splits, the unit count is
+    unchanged, the total drift is at most 1/64 of the pages); any other input
+    change (partials workspace, a long jump, the batch shape) recomputes."""
+    from phaseshift_amd import ops
+    rng = np.random.default_rng(404)
+    A = [int(x) for x in np.exp(rng.uniform(np.log(4096), np.log(65536), 64))]
+    B = [32768] * 64
+    args = lambda v, pb=64 << 20: (64, 24, 4, 256, 16, True, v, pb)
+    fa, fb = _fresh_split(*args(A)), _fresh_split(*args(B))
+    assert fa != fb
+    for v, want in ((A, fa), (B, fb), (A, fa), (B, fb)):
+        assert ops.choose_decode_split(*args(v)) == want
+    # one row grows by one page (16 tokens): the memo answers with A's plan
+    A1 = list(A)
+    A1[3] += 16
+    assert ops.choose_decode_split(*args(A1)) == fa
+    sp, pp = fa
+    # a row pushed past sp * pp pages would need more splits: recomputed
+    A2 = list(A)
+    A2[0] = sp * pp * 16 + 1
+    assert ops.choose_decode_split(*args(A2)) == _fresh_split(*args(A2))
+    # drift above 1/64 of the pages: recomputed
+    A3 = [x + 400 for x in A]
+    assert ops.choose_decode_split(*args(A3)) == _fresh_split(*args(A3))
+    # a different partials workspace: recomputed
+    assert ops.choose_decode_split(*args(A, 8 << 20)) == _fresh_split(*args(A, 8 << 20))
+    # a unit-count change (a row crossing a multiple of the split size)
+    A4 = list(A)
+    r = int(np.argmax([(-(-x // 16)) % pp for x in A]))   # row nearest its next boundary
+    A4[r] = (-(-A[r] // 16) // pp + 1) * pp * 16 + 1
+    if (-(-A4[r] // 16) + pp - 1) // pp <= sp:
+        assert ops.choose_decode_split(*args(A4)) == _fresh_split(*args(A4))
