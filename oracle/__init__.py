@@ -78,6 +78,7 @@ def ref_lib():
         _ref.ref_f32_to_bf16_range.argtypes = [C.c_uint32, C.c_uint32, _u16p]
         _ref.ref_psq4_encode_block.argtypes = [_f32p, C.c_uint32, _f32p, _u8p]
         _ref.ref_psq4_pack_codes.argtypes = [_u8p, _u8p]
+        _ref.ref_psq8_encode_block.argtypes = [_f32p, C.c_uint32, _f32p, _u8p]
         _ref.ref_psq_bf16_round_array.argtypes = [_f32p, _f32p, C.c_uint64]
         _ref.ref_cb10_encode_array.argtypes = [_f32p, _f32p, _u8p, C.c_uint64]
         _ref.ref_cb10_code_to_f32.restype = C.c_float

@@ -8,11 +8,14 @@
 //   psq_bf16_round, cb10_encode / cb10_code_to_f32
 //       reference include/phaseshift/quantization/psq/psq4_kv.h:9-79,
 //       psq_device.h:13-35 (header-only host code)
-// psq8_kv.h is not built: it includes hip/hip_fp8.h, which a host compiler
-// cannot take.
+//   ps::quantization::psq::psq8_{maxabs,lsq1}_encode_block
+//       reference include/phaseshift/quantization/psq/psq8_kv.h:30-90 (host
+//       branch: the reference's own e4m3 codec). psq8_kv.h includes
+//       hip/hip_fp8.h, so this file is compiled by hipcc's host pass only.
 #include <phaseshift/core/memory/types.h>
 #include <phaseshift/quantization/fpx/e4m3.h>
 #include <phaseshift/quantization/psq/psq4_kv.h>
+#include <phaseshift/quantization/psq/psq8_kv.h>
 
 #include <cstdint>
 #include <cstring>
@@ -59,6 +62,13 @@ void ref_psq_bf16_round_array(const float* in, float* out, uint64_t n) {
 
 void ref_cb10_encode_array(const float* x, const float* inv, uint8_t* out, uint64_t n) {
     for (uint64_t i = 0; i < n; ++i) out[i] = ps::quantization::psq::cb10_encode(x[i], inv[i]);
+}
+
+void ref_psq8_encode_block(const float* x, uint32_t lsq1, float* scale, uint8_t* codes) {
+    if (lsq1)
+        ps::quantization::psq::psq8_lsq1_encode_block(x, 32u, *scale, codes);
+    else
+        ps::quantization::psq::psq8_maxabs_encode_block(x, 32u, *scale, codes);
 }
 
 float ref_cb10_code_to_f32(uint8_t c) { return ps::quantization::psq::cb10_code_to_f32(c); }

@@ -278,8 +278,10 @@ def test_psq_launchers_match_capi_and_oracle(dev, ref_api, fmt):
     g = geom_of(lay)
     slots = np.concatenate([np.full(n, i, np.uint32) for i, n in enumerate(lens)])
     pos = np.concatenate([np.arange(n, dtype=np.uint32) for n in lens])
-    k_in = bf16_normal(rng, (len(pos), 1024), 0.02)
-    v_in = bf16_normal(rng, (len(pos), 1024), 0.02)
+    # no outliers here: outputs stay O(1), where the north-star max-abs bound
+    # bites (append with outliers is held bit-exact in test_gpu_psq.py)
+    k_in = bf16_normal(rng, (len(pos), 1024))
+    v_in = bf16_normal(rng, (len(pos), 1024))
     dk_in, dv_in, dsl, dpos, dbt = (to_dev(k_in), to_dev(v_in), to_dev(slots), to_dev(pos),
                                     to_dev(lay.block_tables))
     nb, cb = g.psq_blocks, g.psq_code_bytes(fmt)

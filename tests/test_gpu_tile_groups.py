@@ -11,8 +11,8 @@ import torch
 
 import phaseshift_amd as P
 from phaseshift_amd import ops, state
-from tests.kvcase import bf16_normal, paged_layout, to_dev
-from tests.test_gpu_paged_attention import TOL, make_pools, oracle_out
+from tests.kvcase import assert_attention_close, bf16_normal, paged_layout, to_dev
+from tests.test_gpu_paged_attention import REL, TOL, make_pools, oracle_out
 
 pytestmark = pytest.mark.gpu
 
@@ -67,6 +67,7 @@ def test_grouped_prefill_vs_oracle(dev, fp8, qh, kvh, split):
                                     nan_rows[:8].tolist(), nan_heads,
                                     [(k.kind, k.row_begin, k.rows, k.splits, k.pages_per_split, k.side)
                                      for k in plan.kernels[:plan.count]])
+    assert_attention_close(got, want, TOL[fp8], REL, f"grouped prefill fp8={fp8} {qh}/{kvh} split={split}")
 
 
 def test_grouped_prefill_d128(dev):
@@ -86,7 +87,7 @@ def test_grouped_prefill_d128(dev):
                     v_scale=vs, launch=True)
     torch.cuda.synchronize()
     want = oracle_out(lay, 12, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
-    assert np.max(np.abs(out.cpu().numpy() - want)) < TOL[True]
+    assert_attention_close(out.cpu().numpy(), want, TOL[True], REL, "test_gpu_tile_groups 1")
 
 
 @pytest.mark.parametrize("fp8", [False, True])
@@ -121,4 +122,4 @@ def test_grouped_and_verify_tiles_page24(dev, fp8):
     want = oracle_out(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
     got = out.cpu().numpy()
     assert not np.any(got == 7.0)
-    assert np.max(np.abs(got - want)) < TOL[fp8]
+    assert_attention_close(got, want, TOL[fp8], REL, "test_gpu_tile_groups 2")

@@ -136,6 +136,26 @@ def test_psq4_blocks_match_reference_host_encoder():
             assert np.array_equal(codes, c), (x, lsq1)
 
 
+def test_psq8_blocks_match_reference_host_encoder():
+    """psq8_{maxabs,lsq1}_encode_block of the reference's psq8_kv.h (host branch,
+    compiled from the reference header into oracle/_ref) against the oracle's
+    PSQ8 block encoder in the host (sequential) summation order, on the same
+    seeded blocks as PSQ4 (normal, outliers, tiny, zero, one-hot, constant, huge)."""
+    r = ref_or_skip()
+    rng = np.random.default_rng(5)
+    n = 0
+    for x in blocks(rng, 400):
+        for lsq1 in (0, 1):
+            s = np.zeros(1, np.float32)
+            c = np.zeros(32, np.uint8)
+            r.ref_psq8_encode_block(x, lsq1, s, c)
+            sb, codes = oracle.psq_encode_block(x, 8, bool(lsq1), device_order=False)
+            assert sb == int(s.view(np.uint32)[0] >> 16), (x, lsq1)
+            assert np.array_equal(codes, c), (x, lsq1)
+            n += 1
+    assert n > 1000
+
+
 def test_psq4_packing_matches_reference():
     r = ref_or_skip()
     rng = np.random.default_rng(6)
