@@ -196,6 +196,22 @@ int psk_attention_paged_fp8_e4m3_split(const psk_paged_attention_args* a, const 
                                        const float* v_scale_pool, float* partials,
                                        uint32_t splits, uint32_t pages_per_split,
                                        void* stream);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): psk_attention_paged_fp8_e4m3_split followed by
+ * psk_attention_paged_split_reduce_ex in one call, with the split partials in a
+ * library-owned static device array of PSK_NOALLOC_SCRATCH_BYTES per GPU
+ * instead of a caller workspace. Calls no hipMalloc/hipFree. Returns
+ * hipErrorInvalidValue when the call's partials
+ * (psk_attention_split_partials_bytes(rows, q_heads, kv_heads, splits)) exceed
+ * PSK_NOALLOC_SCRATCH_BYTES. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race. */
+#define PSK_NOALLOC_SCRATCH_BYTES (32ull << 20)
+int psk_attention_paged_fp8_e4m3_split_noalloc(const psk_paged_attention_args* a,
+                                               const void* k_pool, const void* v_pool,
+                                               const float* k_scale_pool,
+                                               const float* v_scale_pool, uint32_t splits,
+                                               uint32_t pages_per_split, void* stream);
 /* Additive: BF16 split with an explicit pages_per_split, and the matching reduce. */
 int psk_attention_paged_bf16_split_ex(const psk_paged_attention_args* a, const void* k_pool,
                                       const void* v_pool, float* partials, uint32_t splits,

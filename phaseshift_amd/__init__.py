@@ -159,6 +159,7 @@ SIGNATURES = {
     "psk_attention_paged_bf16_split": [_P, _P, _P, _P, _U32, _P],
     "psk_attention_paged_bf16_split_reduce": [_P, _P, _U32, _P],
     "psk_attention_paged_fp8_e4m3_split": [_P, _P, _P, _P, _P, _P, _U32, _U32, _P],
+    "psk_attention_paged_fp8_e4m3_split_noalloc": [_P, _P, _P, _P, _P, _U32, _U32, _P],
     "psk_attention_paged_bf16_split_ex": [_P, _P, _P, _P, _U32, _U32, _P],
     "psk_attention_paged_split_reduce_ex": [_P, _P, _U32, _U32, _P],
     "psk_attention_split_partials_bytes": [_U32, _U32, _U32, _U32],

@@ -34,6 +34,7 @@
 #include <phaseshift_kv/paged_attention.h>
 
 #include <cfloat>
+#include <mutex>
 
 namespace psk {
 namespace {
@@ -1299,3 +1300,70 @@ hipError_t launch_attention_paged_split_reduce_ex(const PagedAttentionCommonArgs
 }
 
 }  // namespace ps::kernel
+
+// ------------------------------------------- allocation-free split decode
+// FP8 split-K decode plus its combine with the split partials in a
+// library-owned device array instead of a caller workspace, for callers that
+// cannot allocate device memory (code under HIP graph capture, serving loops,
+// harnesses that forbid hipMalloc). Each GPU the library runs on holds its own
+// copy of the array for the life of the process. Every call on a GPU shares
+// that GPU's array: calls that overlap on one GPU (two streams, two threads)
+// race on it. Nothing in it needs clearing: the split kernel writes every
+// partial the combine reads.
+namespace {
+
+constexpr uint64_t kNoAllocScratchBytes = PSK_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The array's device address on the current device, looked up once per
+// device. In host code `scratch` is only a host-side stand-in for the symbol:
+// kernels receive the address returned here, never the name.
+hipError_t scratch_for_current_device(float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int psk_attention_paged_fp8_e4m3_split_noalloc(const psk_paged_attention_args* a,
+                                                          const void* k_pool, const void* v_pool,
+                                                          const float* k_scale_pool,
+                                                          const float* v_scale_pool,
+                                                          uint32_t splits, uint32_t pages_per_split,
+                                                          void* stream) {
+    if (a == nullptr || k_pool == nullptr || v_pool == nullptr || k_scale_pool == nullptr ||
+        v_scale_pool == nullptr)
+        return hipErrorInvalidValue;
+    hipError_t e = psk::validate_common(*a);
+    if (e != hipSuccess) return e;
+    if (splits == 0u || splits > psk::kMaxSplits) return hipErrorInvalidValue;
+    // the partials of this call must fit the array
+    if (psk_attention_split_partials_bytes(a->rows, a->q_heads, a->kv_heads, splits) >
+        kNoAllocScratchBytes)
+        return hipErrorInvalidValue;
+    if (!psk::mfma_shape_ok(*a, 1, k_pool, v_pool)) return hipErrorNotSupported;
+    float* parts = nullptr;
+    e = scratch_for_current_device(&parts);
+    if (e != hipSuccess) return e;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const psk::DecodeParams p =
+        psk::make(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, parts, splits, pages_per_split);
+    e = psk::launch_decode<psk::kFmtFp8>(p, st);
+    if (e != hipSuccess) return e;
+    return psk::launch_reduce(p, st);
+}
