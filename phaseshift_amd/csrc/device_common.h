@@ -102,6 +102,12 @@ __device__ __forceinline__ f16x8 fp8x8_to_f16x8(uint32_t w0, uint32_t w1) {
     return __builtin_bit_cast(f16x8, r);
 }
 
+// Packs 4 floats into 4 E4M3 bytes (hardware RNE; callers keep |x| <= 448).
+__device__ __forceinline__ uint32_t e4m3x4_rne(float a, float b, float c, float d) {
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+}
+
 // Two floats -> f16 pair (round to nearest even).
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
@@ -117,6 +123,27 @@ __device__ __forceinline__ float group_max(float x) {
 #pragma unroll
     for (int o = W / 2; o >= 1; o >>= 1) x = __builtin_fmaxf(x, __shfl_xor(x, o, 64));
     return x;
+}
+
+// Combine x with the value of lane ^ 16 (lane ^ 32) without the LDS crossbar:
+// v_permlane16_swap (v_permlane32_swap) with both operands x returns, in its
+// two results, x of the lane and of its partner in some order, so a
+// symmetric combine of the two is the pairwise reduction.
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ float wave_sum(float x) {

@@ -295,6 +295,52 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
             }
         }
     }
+    // PSQ4: the score product runs on the fp8 MFMA with the K codes as the
+    // E4M3 bytes of their cb10 values (exact), so no K value is converted.
+    // Q goes in as E4M3 hi + lo parts of q * 2^sh (sh = 8 - E for the head's
+    // max|q| = m * 2^E, m in [0.5, 1)): hi = RNE(q * 2^sh), lo = RNE(q * 2^sh
+    // - hi), which keep q to 2^-8 relative (the residual is exact in fp32);
+    // the scores take the factor qinv = 2^-sh. Byte j of an operand is
+    // element j of the bf16 operand it replaces (same dims, same order).
+    constexpr bool kQ8 = FMT == kFmtPsq4;
+    uint64_t q8h[kQ8 ? NS : 1], q8l[kQ8 ? NS : 1];
+    float qinv = 1.0f;
+    if constexpr (kQ8) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const u32x4 w = __builtin_bit_cast(u32x4, qf[s]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fabsf(__uint_as_float(w[k] << 16)),
+                                                             __builtin_fabsf(__uint_as_float(w[k] & 0xFFFF0000u))));
+        }
+        amax = max_xor32(max_xor16(amax));   // the head's lanes (n, g = 0..3)
+        const int sh = (amax > 0.0f && amax <= 3.0e38f) ? 8 - __builtin_amdgcn_frexp_expf(amax) : 0;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const u32x4 w = __builtin_bit_cast(u32x4, qf[s]);
+            uint32_t hw[2], lw[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float y[4], r[4];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    y[2 * t] = __builtin_ldexpf(__uint_as_float(w[2 * h + t] << 16), sh);
+                    y[2 * t + 1] = __builtin_ldexpf(__uint_as_float(w[2 * h + t] & 0xFFFF0000u), sh);
+                }
+                hw[h] = e4m3x4_rne(y[0], y[1], y[2], y[3]);
+                r[0] = y[0] - __builtin_amdgcn_cvt_f32_fp8((int)hw[h], 0);
+                r[1] = y[1] - __builtin_amdgcn_cvt_f32_fp8((int)hw[h], 1);
+                r[2] = y[2] - __builtin_amdgcn_cvt_f32_fp8((int)hw[h], 2);
+                r[3] = y[3] - __builtin_amdgcn_cvt_f32_fp8((int)hw[h], 3);
+                lw[h] = e4m3x4_rne(r[0], r[1], r[2], r[3]);
+            }
+            q8h[s] = (uint64_t)hw[0] | ((uint64_t)hw[1] << 32);
+            q8l[s] = (uint64_t)lw[0] | ((uint64_t)lw[1] << 32);
+        }
+        qinv = __builtin_ldexpf(1.0f, -sh);
+    }
 
     const uint64_t layer_base = (uint64_t)a.layer * a.elems_per_layer;
     const uint64_t scale_layer = (uint64_t)a.layer * a.num_pages;
@@ -453,6 +499,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
 #pragma unroll
                     for (int s = 0; s < NS; ++s) {
                         bf16x8 kf;
+                        [[maybe_unused]] long kf8 = 0;
                         if constexpr (FMT == kFmtPsq8) {
                             // bytes 32s + 8g .. +8 of token n
                             const u32x2 w = kLineLayout
@@ -468,16 +515,19 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                             const uint32_t x = kLineLayout
                                 ? *reinterpret_cast<const uint32_t*>(kb + k_line + ((16u * s) ^ k_x))
                                 : *reinterpret_cast<const uint32_t*>(kb + 256 * s + 16 * n + 4 * g);
-                            const uint32_t lo = psq4_e4m3x4(x, false), hi = psq4_e4m3x4(x, true);
-                            u32x4 r;
-                            r[0] = fp8x2_to_bf16x2(lo, false);
-                            r[1] = fp8x2_to_bf16x2(lo, true);
-                            r[2] = fp8x2_to_bf16x2(hi, false);
-                            r[3] = fp8x2_to_bf16x2(hi, true);
-                            kf = __builtin_bit_cast(bf16x8, r);
+                            const uint64_t ka = (uint64_t)psq4_e4m3x4(x, false) |
+                                                ((uint64_t)psq4_e4m3x4(x, true) << 32);
+                            kf8 = (long)ka;
                         }
-                        const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            kf, qf[s], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        f32x4 part;
+                        if constexpr (kQ8) {
+                            part = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+                                kf8, (long)q8h[s], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            part = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(kf8, (long)q8l[s], part, 0, 0, 0);
+                        } else {
+                            part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                kf, qf[s], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        }
                         const u32x4 kw = *reinterpret_cast<const u32x4*>(kscl + 64 * (s >> 1));
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
@@ -525,13 +575,12 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const bool ok = c + hf * 16 + 4u * g + (uint32_t)r < te;
-                    s2[hf][r] = ok ? sc[hf][r] * (p.scale_log2 * kscale[r]) : -INFINITY;
+                    s2[hf][r] = ok ? sc[hf][r] * (p.scale_log2 * (kQ8 ? qinv : kscale[r])) : -INFINITY;
                     vsc[hf][r] = vscale[r];
                     mx = __builtin_fmaxf(mx, s2[hf][r]);
                 }
             }
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = max_xor32(max_xor16(mx));   // lane permutes, no LDS round trip
             const float m_new = __builtin_fmaxf(m_run, mx);
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
@@ -667,8 +716,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     const uint32_t q0 = kvh * qpk;
     if constexpr (kIndep) {
         if (!active) return;
-        const float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-        const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
+        const float l_all = sum_xor32(sum_xor16(l_run));
         if (n >= qpk) return;
         if (p.partials == nullptr) {
             // An invalid page leaves this row's output unwritten.
@@ -704,8 +752,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     } else {
         // ---- merge the 4 waves: per wave m[16], l[16], O[qpk][D] in LDS
         if (bad) bad_shared = 1u;
-        const float l_tot = l_run + __shfl_xor(l_run, 16, 64);
-        const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
+        const float l_all = sum_xor32(sum_xor16(l_run));
         __syncthreads();
         float* fm = reinterpret_cast<float*>(lds);
         float* fl = fm + kWaves * 16;

@@ -78,11 +78,6 @@ __device__ __forceinline__ bf16x8 q8(const uint16_t* q, bool ok) {
 
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 
-// Packs 4 floats into 4 E4M3 bytes (hardware RNE; |x| <= 448 here).
-__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
-    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
-}
 
 // FP8 QK^T on v_mfma_f32_16x16x128_f8f6f4: Q of one (row, head) as E4M3
 // hi + lo parts of q * 2^sh, sh = 8 - E with max|q| = m * 2^E (m in
@@ -126,12 +121,12 @@ __device__ __forceinline__ float q_split_e4m3(const uint16_t* qrow, bool ok, uin
             float y[4], r[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) y[t] = __builtin_ldexpf(x[i][4 * k + t], sh);
-            h[k] = f32x4_to_e4m3(y[0], y[1], y[2], y[3]);
+            h[k] = e4m3x4_rne(y[0], y[1], y[2], y[3]);
             r[0] = y[0] - __builtin_amdgcn_cvt_f32_fp8((int)h[k], 0);
             r[1] = y[1] - __builtin_amdgcn_cvt_f32_fp8((int)h[k], 1);
             r[2] = y[2] - __builtin_amdgcn_cvt_f32_fp8((int)h[k], 2);
             r[3] = y[3] - __builtin_amdgcn_cvt_f32_fp8((int)h[k], 3);
-            l[k] = f32x4_to_e4m3(r[0], r[1], r[2], r[3]);
+            l[k] = e4m3x4_rne(r[0], r[1], r[2], r[3]);
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -151,7 +146,7 @@ template <int FMT, int D>
 constexpr int tile_stage_bytes() {
     return 2 * 2 * (16 * code_bytes<FMT, D>() + 128) + (FMT != kFmtBf16 ? 2 * 2 * 256 : 0);
 }
-constexpr int kTileStages = 4;
+constexpr int kTileStages = 4;   // two pairs of chunks (see the main loop)
 
 // kAl16: page_tokens % 16 == 0, so every page-aligned 16-token half lies in one
 // page and its page id, base address and in-page offset are wave-uniform.
@@ -547,6 +542,10 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 };
                 f32x4 acc[HPW];
                 i32x8 cur = kread(0);
+                // Raised wave priority over each MFMA cluster: the SIMD's other
+                // wave then fills the VALU while this one streams its MFMAs
+                // (measured: prefill launch of config 5 1035 -> 998 us).
+                __builtin_amdgcn_s_setprio(1);
 #pragma unroll
                 for (int u = 0; u < H * NJ; ++u) {
                     i32x8 nxt = cur;
@@ -571,6 +570,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                     }
                     cur = nxt;
                 }
+                __builtin_amdgcn_s_setprio(0);
             } else if constexpr (NS % 2 == 0) {
                 // K in pairs of K-steps (16 B of FP8 or 2 x 16 B of BF16 per
                 // lane), each pair's LDS read issued one pair ahead so that its
@@ -675,8 +675,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                         s2[hf][r] = tok_ok[hf][r] ? sc[i][hf][r] * (p.scale_log2 * kscale[hf][r]) : -INFINITY;
                         mx = __builtin_fmaxf(mx, s2[hf][r]);
                     }
-                mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-                mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+                mx = max_xor32(max_xor16(mx));   // lane permutes, no LDS round trip
                 mx *= qinv[i];
                 // m_run is the row's softmax reference: it moves only when a
                 // score exceeds it by more than kLazyMaxSlack (then P <= 2^slack)
@@ -801,6 +800,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 return r;
             };
             VRaw vcur = vread(0);
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int pr = 0; pr < NDB / 2; ++pr) {
                 VRaw vnxt = vcur;
@@ -828,37 +828,42 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 }
                 vcur = vnxt;
             }
+            __builtin_amdgcn_s_setprio(0);
         };
 
-        // One step: after this wave's DMAs of chunk c landed (vmcnt leaves the
-        // next chunk's DPW outstanding) the barrier makes every wave's DMAs of
-        // c visible and guarantees every wave finished the chunk before c, so
-        // its stage may be refilled with the chunk two ahead. __restrict__
-        // tells the compiler that the DMA into `next` and the reads of `cur`
-        // touch different LDS; their real ordering is the wait + barrier.
-        auto step = [&](uint32_t c, uint8_t* __restrict__ next,
-                        const uint8_t* __restrict__ cur) __attribute__((always_inline)) {
-            issue(c + (kTileStages - 1u) * CT, next);
-            // chunks past this wave's rows add nothing to them
+        // Two chunks per barrier (measured: config 5's prefill launch 999 ->
+        // 973 us against one chunk per barrier with three in flight): pair p
+        // sits in stages 2(p&1), +1; after the wait + barrier the pair has
+        // landed and every wave is done with pair p - 1, whose stages take
+        // pair p + 1, in flight while pair p is computed. __restrict__ tells
+        // the compiler that the DMAs into `next` and the reads of `cur` touch
+        // different LDS; their real ordering is the wait + barrier.
+        static_assert(kTileStages == 4, "two pairs of chunk stages");
+        issue(ts, stages);
+        issue(ts + CT, stages + STAGE);
+        auto step2 = [&](uint32_t c, uint8_t* __restrict__ next, const uint8_t* __restrict__ cur)
+                         __attribute__((always_inline)) {
+            issue(c + 2 * CT, next);
+            issue(c + 3 * CT, next + STAGE);
             if (computes && c < wave_vis) {
                 if (c + CT <= wave_vis_min && c + CT <= te)
                     consume(c, cur, std::true_type{});
                 else
                     consume(c, cur, std::false_type{});
             }
+            const uint32_t c1 = c + CT;
+            if (computes && c1 < te && c1 < wave_vis) {
+                if (c1 + CT <= wave_vis_min && c1 + CT <= te)
+                    consume(c1, cur + STAGE, std::true_type{});
+                else
+                    consume(c1, cur + STAGE, std::false_type{});
+            }
         };
-
-        // kTileStages - 1 chunks in flight: the DMAs of chunk k go out
-        // kTileStages - 1 steps before it is consumed
-        constexpr uint32_t kAhead = kTileStages - 1;
-#pragma unroll
-        for (uint32_t a_ = 0; a_ < kAhead; ++a_) issue(ts + a_ * CT, stages + a_ * STAGE);
-        uint32_t sc = 0;   // stage of the chunk at c
-        for (uint32_t c = ts; c < te; c += CT) {
-            wait_vmcnt_barrier<(kAhead - 1) * DPW>();
-            const uint32_t sn = sc == 0u ? kTileStages - 1u : sc - 1u;   // stage of chunk c + kAhead
-            step(c, stages + sn * STAGE, stages + sc * STAGE);
-            sc = sc == kTileStages - 1u ? 0u : sc + 1u;
+        uint32_t sp = 0;
+        for (uint32_t c = ts; c < te; c += 2 * CT) {
+            wait_vmcnt_barrier<0>();
+            step2(c, stages + (sp ^ 1u) * 2 * STAGE, stages + sp * 2 * STAGE);
+            sp ^= 1u;
         }
         // The last steps issued chunks nobody reads: their DMAs must land
         // before the LDS is reused.
@@ -887,8 +892,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         if (!hv[i]) continue;
         const uint32_t gh = hbase + (uint32_t)i;
         const uint32_t head = kv_head * qpk + gh;
-        const float l_tot = l_run[i] + __shfl_xor(l_run[i], 16, 64);
-        const float l_all = l_tot + __shfl_xor(l_tot, 32, 64);
+        const float l_all = sum_xor32(sum_xor16(l_run[i]));
         if (part_row == nullptr) {
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {

@@ -73,6 +73,14 @@ def append_case(dev, fmt, lsq1, rows, kv_heads, D, seed, stride_pad=0):
     k_in[1, 40] = oracle.f32_to_bf16(np.array([-5.0], np.float32))[0]
     v_in[2, :32] = oracle.f32_to_bf16(np.full(32, 1e-30, np.float32))
     v_in[3, 64:96] = oracle.f32_to_bf16(np.full(32, 3.0, np.float32))
+    if fmt == 4:
+        # a block whose bf16 scale is subnormal (amax ~4.4e-38): 2/s overflows
+        # while 1/s is finite, the PSQ4 encoder's second form. (For PSQ8 at
+        # such amax 1/s itself overflows and the codes of x * inf are where the
+        # reference's host codec and its device converter differ, the
+        # non-finite case outside the bit-exact contract.)
+        k_in[3, 96:128] = oracle.f32_to_bf16(
+            (rng.uniform(0.3, 1.0, 32) * 4.5e-38 * np.where(rng.random(32) < 0.5, -1, 1)).astype(np.float32))
     return lay, slots, pos, k_in, v_in
 
 

@@ -114,12 +114,15 @@ def test_cb10_matches_reference():
 
 # ---------------------------------------------------------- block encoders
 def blocks(rng, n):
-    """Seeded 32-value blocks: normal, outliers, tiny, one-hot, zero, bf16 values."""
+    """Seeded 32-value blocks: normal, outliers, tiny (down to subnormal block scales),
+    one-hot, zero, bf16 values."""
     out = [rng.standard_normal(32) * s for s in rng.uniform(0.01, 30, n)]
     out += [np.where(rng.random(32) < 0.1, rng.standard_normal(32) * 50, rng.standard_normal(32))
             for _ in range(n // 4)]
     out += [rng.standard_normal(32) * 1e-30, np.zeros(32), np.eye(32)[5] * -3.0,
-            np.full(32, 7.25), rng.standard_normal(32) * 1e30]
+            np.full(32, 7.25), rng.standard_normal(32) * 1e30,
+            rng.standard_normal(32) * 3e-38,     # bf16-subnormal block scales: 1/s overflows
+            rng.uniform(0.3, 1.0, 32) * 4.5e-38]  # 1/s finite, 2/s overflows
     return [oracle.bf16_to_f32(oracle.f32_to_bf16(np.asarray(b, np.float32))) for b in out]
 
 
@@ -176,8 +179,13 @@ def test_maxabs_block_properties():
             if amax == 0.0 or s == 0.0:
                 assert s == 0.0 and not c.any()
                 continue
+            if s < 1.0 / float(np.finfo(np.float32).max):
+                # the reference's own arithmetic (x * (1/s)) degenerates here;
+                # the oracle follows it (checked against the reference above)
+                continue
             target = amax / (10.0 if fmt == 4 else 448.0)
-            assert abs(s - target) <= target * 2.0 ** -8 + 1e-45   # one bf16 rounding
+            # one bf16 rounding (absolute below the normal range: half a subnormal ulp)
+            assert abs(s - target) <= target * 2.0 ** -8 + 2.0 ** -134
             if fmt == 4:
                 # each code is the nearest codebook point to x/s (ties down),
                 # up to the rounding of |x| * (1/s) in f32
@@ -205,6 +213,11 @@ def test_lsq1_scale_is_least_squares_fit():
                 assert s1 == 0.0 and not c.any()
                 continue
             ls = num / den
+            if ls < 2.0 ** -126:
+                # subnormal scales: the f32 sums of subnormal products carry
+                # absolute, not relative, error; pinned by the reference
+                # comparison above instead
+                continue
             # the closed form, rounded to bf16 (f32 sums: a few ulps of slack)
             assert abs(s1 - ls) <= ls * (2.0 ** -8 + 1e-5)
             # device (butterfly) and host (sequential) orders agree to a bf16 ulp
