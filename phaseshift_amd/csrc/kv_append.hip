@@ -305,28 +305,19 @@ __device__ __forceinline__ float psq_bf16_round(float v) {
 // reference's chain for every float a >= 0, for every positive bf16 scale
 // (subnormals included) over a spread of x, and for 2^26 random (x, bf16
 // scale) pairs, checked on the CPU (tests/native/cb10_branchless.c).
-__device__ __forceinline__ uint32_t cb10_code(float x, float inv2) {
+__device__ __forceinline__ uint32_t cb10_code(float x, float inv) {
     // The code boundaries a > 0.5, 1.5, 2.5, 3.5, 5, 7, 9 of a = |x| * inv are
-    // thresholds on k = ceil(2a) = ceil(|x| * inv2), inv2 = 2 * inv (scaling
-    // by 2 commutes with the rounding of the product; below the normal range
-    // ceil gives 0 or 1, both code 0): code(k) for k = 0..19 in 3-bit fields;
-    // NaN and Inf give k = 19 (7). Callers pass inv2 = 2 * inv only where
-    // that is finite, see psq_codes.
-    constexpr uint64_t kLut = 0x0fb6d6db246d2240ull;
-    const float k = __builtin_fminf(__builtin_ceilf(__builtin_fabsf(x) * inv2), 19.0f);
-    const uint32_t m = (uint32_t)(kLut >> (3u * (uint32_t)k)) & 7u;
-    return m | (x < 0.0f ? 8u : 0u);   // -0.0 and NaN: no sign, as the reference
-}
-
-// The same code with the doubling after the product: exact also where 2 * inv
-// overflows while inv is finite (bf16-subnormal scales s <= 2^-127), where
-// the product doubles exactly whenever a is finite and overflows only where
-// a > 9 already gives code 7.
-__device__ __forceinline__ uint32_t cb10_code_tiny_scale(float x, float inv) {
+    // thresholds on k = ceil(2a): code(k) for k = 0..19 in 3-bit fields; NaN and
+    // Inf give k = 19 (7). The doubling follows the product: it is exact
+    // whenever a is finite and overflows only where a > 9 already gives 7,
+    // while a precomputed 2 * inv overflows for bf16-subnormal scales s <=
+    // 2^-127 whose 1/s is finite. (Measured at 2^16 rows: LSQ1 append 109.8
+    // us against 107.0 with 2 * inv, and 111.7 when a per-block branch picks
+    // 2 * inv where it is finite.)
     constexpr uint64_t kLut = 0x0fb6d6db246d2240ull;
     const float k = __builtin_fminf(__builtin_ceilf((__builtin_fabsf(x) * inv) * 2.0f), 19.0f);
     const uint32_t m = (uint32_t)(kLut >> (3u * (uint32_t)k)) & 7u;
-    return m | (x < 0.0f ? 8u : 0u);
+    return m | (x < 0.0f ? 8u : 0u);   // -0.0 and NaN: no sign, as the reference
 }
 
 // Codes of the 32 values for scale s (all 0 unless s > 0): PSQ4 cb10 codes of
@@ -337,16 +328,8 @@ __device__ __forceinline__ void psq_codes(const float (&x)[32], float s, uint32_
     const float inv = 1.0f / s;
     const uint32_t keep = s > 0.0f ? 0xFFFFFFFFu : 0u;   // all codes 0 unless s > 0
     if constexpr (kPsq4) {
-        // one lane per block: the rare block of subnormal scale takes the
-        // exact slow form (a branch per lane, skipped when no lane needs it)
-        if (inv <= 0x1.fffffep+126f) {
-            const float inv2 = 2.0f * inv;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) c[i] = cb10_code(x[i], inv2) & keep;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; ++i) c[i] = cb10_code_tiny_scale(x[i], inv) & keep;
-        }
+        for (int i = 0; i < 32; ++i) c[i] = cb10_code(x[i], inv) & keep;
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i += 4) {

@@ -1,6 +1,5 @@
 /* Check: the branch-free cb10 code of the PSQ4 append kernel
- * (phaseshift_amd/csrc/kv_append.hip: k = min(ceil(|x| * (2 * inv)), 19) where
- * 2 * inv is finite, else min(ceil((|x| * inv) * 2), 19)
+ * (phaseshift_amd/csrc/kv_append.hip, cb10_code: k = min(ceil((|x| * inv) * 2), 19)
  * and a 3-bit lookup of k) equals the reference's comparison chain
  * (psq_device.h:22-31, restated as or_cb10_encode in oracle/ps_oracle.c):
  *   1. exhaustively for every float bit pattern x >= 0 at inv = 1 (including
@@ -22,8 +21,7 @@ uint8_t or_cb10_encode(float x, float inv_scale);
 
 static uint32_t lut_code(float x, float inv) {
     const uint64_t lut = 0x0fb6d6db246d2240ull;   /* code(k), k = 0..19, 3 bits each */
-    const float k = inv <= 0x1.fffffep+126f ? fminf(ceilf(fabsf(x) * (2.0f * inv)), 19.0f)
-                                            : fminf(ceilf((fabsf(x) * inv) * 2.0f), 19.0f);
+    const float k = fminf(ceilf((fabsf(x) * inv) * 2.0f), 19.0f);
     const uint32_t m = (uint32_t)(lut >> (3u * (uint32_t)k)) & 7u;
     return m | (x < 0.0f ? 8u : 0u);
 }
