@@ -186,7 +186,7 @@ def run_decode(torch, ops, st, steps, warmup, dev, splits=None, pps=None):
     return step_ms, t1.ms() / steps, t2.ms() / steps, nbytes_alg, splits, pps
 
 
-def run_append(torch, ops, rows, steps, warmup, dev, seed=7):
+def run_append(torch, ops, rows, steps, warmup, dev, seed=7, graph=False):
     H, D, P = 4, 256, 16
     rng = np.random.default_rng(seed)
     seqs = max(1, rows // P)
@@ -214,7 +214,28 @@ def run_append(torch, ops, rows, steps, warmup, dev, seed=7):
         for _ in range(steps):
             launch()
     ms = t.ms() / steps
-    return ms, rows * APPEND_BYTES_PER_ROW_FP8
+    if not graph:
+        return ms, rows * APPEND_BYTES_PER_ROW_FP8
+    # the same launches captured back to back in one HIP graph and replayed:
+    # the GPU-side cost per append without the host's per-launch work
+    n = 100
+    s = torch.cuda.Stream()
+    cg = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        launch()                      # first use outside the capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(cg, stream=s):
+            for _ in range(n):
+                launch()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        cg.replay()
+    torch.cuda.synchronize()
+    t = Timer(torch)
+    with t:
+        for _ in range(steps):
+            cg.replay()
+    return ms, rows * APPEND_BYTES_PER_ROW_FP8, t.ms() / (steps * n)
 
 
 def run_psq(torch, ops, steps, warmup, dev):
@@ -911,6 +932,12 @@ def main():
                                       kernel_ms=round(ms, 5),
                                       GBps=round(nb / (ms * 1e-3) / 1e9, 1),
                                       frac_of_peak=round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+        # config 2 at decode batch size is launch-bound: the same append
+        # replayed from a captured graph shows its GPU-side cost per launch
+        _, nb, gms = run_append(torch, ops, 128, args.steps, args.warmup, dev, graph=True)
+        ap["rows_128_graph_replay"] = dict(tokens_per_s=round(128 / (gms * 1e-3), 1),
+                                           ms_per_append=round(gms, 5),
+                                           GBps=round(nb / (gms * 1e-3) / 1e9, 1))
         extra["kv_append_fp8"] = ap
 
     if "psq" in only:

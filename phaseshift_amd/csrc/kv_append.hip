@@ -78,11 +78,14 @@ __device__ __forceinline__ bool fast_div_ok(float scale) {
 }
 
 // Fast path: head_dim % 8 == 0, head_dim <= 8 * L, every access aligned. A
-// wave runs kUnroll groups of 64/L tasks. The kUnroll slot/position loads go
-// out first, then all input loads, then the block-table loads (which wait
-// only for slot/position), so the HBM reads overlap the lookup chain
-// (reference skip rules: kv_append.hip:31-55).
-constexpr int kUnroll = 4;
+// wave runs kUnroll groups of 64/L tasks. The slot/position loads go out
+// first, then the input loads, then the block-table loads (which wait only
+// for slot/position), so the HBM reads overlap the lookup chain (reference
+// skip rules: kv_append.hip:31-55). One group per wave measured fastest at
+// every size, by GPU time per launch from a replayed graph: 128 rows 7.38 ->
+// 3.07 us, 1024 rows 7.65 -> 3.49, 2^16 rows 77.4 -> 76.8 against four groups
+// per wave (the launch-bound small appends of decode steps gain most).
+constexpr int kUnroll = 1;
 
 template <bool kFp8>
 __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams p) {

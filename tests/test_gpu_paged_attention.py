@@ -57,7 +57,7 @@ def host(t):
 
 
 def run_gpu(lay, q_heads, q, slots, pos, bt, kp, vp, ks, vs, out_dtype=torch.float32, splits=1,
-            pages_per_split=0, kind="decode", out=None, q_pad=0, out_pad=0):
+            pages_per_split=0, kind="decode", out=None, q_pad=0, out_pad=0, layer=0):
     """q_pad / out_pad > 0: Q and the output are column slices of wider row-major
     buffers, so q_row_stride and output_row_stride exceed q_heads * head_dim
     (the strided views paged_attention_dispatch.hip:415-416 passes). The pad
@@ -81,7 +81,7 @@ def run_gpu(lay, q_heads, q, slots, pos, bt, kp, vp, ks, vs, out_dtype=torch.flo
     if splits > 1:
         nbytes = ops.split_partials_bytes(rows, q_heads, lay.kv_heads, splits)
         partials = torch.empty(nbytes // 4, dtype=torch.float32, device=kp.device)
-    ops.paged_attention(g, 0, dq, out, to_dev(np.asarray(slots, np.uint32)),
+    ops.paged_attention(g, layer, dq, out, to_dev(np.asarray(slots, np.uint32)),
                         to_dev(np.asarray(pos, np.uint32)), to_dev(bt), kp, vp, q_heads,
                         ks, vs, splits=splits, pages_per_split=pages_per_split,
                         partials=partials, kind=kind)
@@ -91,8 +91,9 @@ def run_gpu(lay, q_heads, q, slots, pos, bt, kp, vp, ks, vs, out_dtype=torch.flo
     return out.float().cpu().numpy() if out.dtype != torch.float32 else out.cpu().numpy()
 
 
-def oracle_out(lay, q_heads, q, slots, pos, bt, kp, vp, ks, vs, workers=8):
-    g = dict(lay.geom, q_heads=q_heads, block_table_stride=bt.shape[1], max_sequences=bt.shape[0])
+def oracle_out(lay, q_heads, q, slots, pos, bt, kp, vp, ks, vs, workers=8, layer=0):
+    g = dict(lay.geom, q_heads=q_heads, block_table_stride=bt.shape[1], max_sequences=bt.shape[0],
+             layer=layer)
     return oracle_attention_parallel(g, q, slots, pos, bt, host(kp), host(vp), host(ks), host(vs),
                                      1.0 / math.sqrt(lay.head_dim), workers=workers)
 
@@ -360,3 +361,33 @@ def test_padded_q_and_output_strides(dev, fp8):
     got = run_gpu(lay, 24, qv, vslots, vpos, bt, kp, vp, ks, vs, kind="prefill", q_pad=128,
                   out_pad=8)
     close(got, want_v, fp8, f"padded tile fp8={fp8}")
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_layer_offset_in_multi_layer_pool(dev, fp8):
+    """Pools of 3 attention layers, attention on layer 2 (and layer 1): every
+    kernel adds the layer's offset to K/V and scale addresses (reference
+    paged_kv_pool.cpp:64-75: [layers][pages][page_tokens][kv_heads][head_dim]).
+    Decode unsplit and split, and a verify block on the tile kernel, each
+    against the oracle on the same layer; the other layers hold different
+    random values, so a wrong offset reads the wrong layer."""
+    rng = np.random.default_rng(321 + fp8)
+    lens = [2100, 600, 37]
+    lay = paged_layout(rng, lens + [1200 + 16], 16, 4, 256, num_layers=3, spare_pages=2)
+    kp, vp, ks, vs = make_pools(lay, fp8, 321 + fp8, dev)
+    bt = lay.block_tables
+    q = bf16_normal(rng, (3, 24 * 256))
+    slots = np.arange(3, dtype=np.uint32)
+    pos = np.asarray(lens, np.uint32) - 1
+    vslots = np.full(16, 3, np.uint32)
+    vpos = np.arange(1200, 1216, dtype=np.uint32)
+    qv = bf16_normal(rng, (16, 24 * 256))
+    for layer in (2, 1):
+        want = oracle_out(lay, 24, q, slots, pos, bt, kp, vp, ks, vs, layer=layer)
+        for splits, pps in ((1, 0), (4, 0), (7, 16)):
+            got = run_gpu(lay, 24, q, slots, pos, bt, kp, vp, ks, vs, splits=splits,
+                          pages_per_split=pps, layer=layer)
+            close(got, want, fp8, f"layer {layer} fp8={fp8} {splits}/{pps}")
+        want_v = oracle_out(lay, 24, qv, vslots, vpos, bt, kp, vp, ks, vs, layer=layer)
+        got = run_gpu(lay, 24, qv, vslots, vpos, bt, kp, vp, ks, vs, kind="prefill", layer=layer)
+        close(got, want_v, fp8, f"layer {layer} tile fp8={fp8}")

@@ -232,22 +232,23 @@ def attn_case(dev, fmt, lens, qh, kvh, D, P=16, seed=0, spare=2):
 
 
 def run_attn(dev, lay, fmt, qh, q, slots, pos, bt, pools, splits=1, pps=0, kind="decode",
-             out_dtype=torch.float32):
+             out_dtype=torch.float32, layer=0):
     rows = q.shape[0]
     out = torch.full((rows, qh * lay.head_dim), 7.0, dtype=out_dtype, device=dev)
     partials = None
     if splits > 1:
         nbytes = ops.split_partials_bytes(rows, qh, lay.kv_heads, splits)
         partials = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
-    ops.paged_attention_psq(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+    ops.paged_attention_psq(geom_of(lay), layer, to_dev(q), out, to_dev(slots), to_dev(pos),
                             to_dev(bt), *pools, qh, fmt, splits=splits, pages_per_split=pps,
                             partials=partials, kind=kind)
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
 
 
-def oracle_attn(lay, fmt, qh, q, slots, pos, bt, pools):
-    g = dict(lay.geom, q_heads=qh, block_table_stride=bt.shape[1], max_sequences=bt.shape[0])
+def oracle_attn(lay, fmt, qh, q, slots, pos, bt, pools, layer=0):
+    g = dict(lay.geom, q_heads=qh, block_table_stride=bt.shape[1], max_sequences=bt.shape[0],
+             layer=layer)
     kc, vc, ks, vs = (to_host(t) for t in pools)
     return oracle_attention_psq_parallel(g, q, slots, pos, bt, kc, vc, ks, vs, fmt,
                                          1.0 / math.sqrt(lay.head_dim))
@@ -531,3 +532,47 @@ def test_psq_pool_reserved_bytes_and_page_copy(dev, fmt):
         assert np.array_equal(c[:, dst], a[:, src]), k
     with pytest.raises(Exception):
         state.KVPool(4, 16, 1, 4, 100, kv_dtype=kvd)   # head_dim not a multiple of 32
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_layer_offset_append_and_attention(dev, fmt):
+    """A 3-layer PSQ pool: append (both estimators) into layer 1 bit-exact
+    against the oracle with the other layers' bytes untouched, then attention
+    on layer 1 (decode unsplit and split, a verify block on the tile kernel)
+    against the oracle on that layer; layers 0 and 2 hold other random codes."""
+    rng = np.random.default_rng(400 + fmt)
+    lens = [700, 1500 + 16]
+    lay = paged_layout(rng, lens, 16, 4, 256, num_layers=3, spare_pages=1)
+    g = geom_of(lay)
+    pools = dev_pools(lay, fmt, dev, seed=400 + fmt)
+    rows = 40   # tokens 660..699 of sequence 0 appended into layer 1
+    slots = np.zeros(rows, np.uint32)
+    pos = np.arange(660, 700, dtype=np.uint32)
+    k_in = bf16_normal(rng, (rows, 1024), 0.02)
+    v_in = bf16_normal(rng, (rows, 1024), 0.02)
+    for est in (0, 1):
+        before = [to_host(t).copy() for t in pools]
+        ops.kv_append_psq(g, 1, to_dev(k_in), to_dev(v_in), to_dev(slots), to_dev(pos),
+                          to_dev(lay.block_tables), *pools, fmt, est)
+        torch.cuda.synchronize()
+        want = [b.copy() for b in before]
+        geo = dict(lay.geom, layer=1, block_table_stride=lay.block_tables.shape[1],
+                   max_sequences=lay.block_tables.shape[0])
+        oracle.kv_append_psq(geo, k_in, v_in, slots, pos, lay.block_tables, *want, fmt, bool(est), True)
+        for name, gt, w, b in zip(("k codes", "v codes", "k scales", "v scales"),
+                                  [to_host(t) for t in pools], want, before):
+            assert np.array_equal(gt, w), (name, est)
+            assert not np.array_equal(w, b), name   # the append wrote something
+    q = bf16_normal(rng, (1, 24 * 256))
+    qs, qp = np.zeros(1, np.uint32), np.array([699], np.uint32)
+    bt = lay.block_tables
+    want = oracle_attn(lay, fmt, 24, q, qs, qp, bt, pools, layer=1)
+    for splits, pps in ((1, 0), (5, 16)):
+        got = run_attn(dev, lay, fmt, 24, q, qs, qp, bt, pools, splits, pps, layer=1)
+        assert_attention_close(got, want, TOL, REL, f"psq{fmt} layer 1 {splits}/{pps}")
+    qv = bf16_normal(rng, (16, 24 * 256))
+    vs_ = np.ones(16, np.uint32)
+    vp_ = np.arange(1500, 1516, dtype=np.uint32)
+    want_v = oracle_attn(lay, fmt, 24, qv, vs_, vp_, bt, pools, layer=1)
+    got = run_attn(dev, lay, fmt, 24, qv, vs_, vp_, bt, pools, kind="prefill", layer=1)
+    assert_attention_close(got, want_v, TOL, REL, f"psq{fmt} layer 1 tile")
