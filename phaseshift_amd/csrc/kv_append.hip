@@ -308,6 +308,7 @@ __device__ __forceinline__ float psq_bf16_round(float v) {
 // reference's chain for every float a >= 0, for every positive bf16 scale
 // (subnormals included) over a spread of x, and for 2^26 random (x, bf16
 // scale) pairs, checked on the CPU (tests/native/cb10_branchless.c).
+template <bool kSigned = true>
 __device__ __forceinline__ uint32_t cb10_code(float x, float inv) {
     // The code boundaries a > 0.5, 1.5, 2.5, 3.5, 5, 7, 9 of a = |x| * inv are
     // thresholds on k = ceil(2a): code(k) for k = 0..19 in 3-bit fields; NaN and
@@ -320,19 +321,29 @@ __device__ __forceinline__ uint32_t cb10_code(float x, float inv) {
     constexpr uint64_t kLut = 0x0fb6d6db246d2240ull;
     const float k = __builtin_fminf(__builtin_ceilf((__builtin_fabsf(x) * inv) * 2.0f), 19.0f);
     const uint32_t m = (uint32_t)(kLut >> (3u * (uint32_t)k)) & 7u;
+    if constexpr (!kSigned) return m;
     return m | (x < 0.0f ? 8u : 0u);   // -0.0 and NaN: no sign, as the reference
 }
 
 // Codes of the 32 values for scale s (all 0 unless s > 0): PSQ4 cb10 codes of
 // x * (1/s), PSQ8 SATFINITE E4M3 codes of x * (1/s) packed 4 per dword.
-template <bool kPsq4>
+// kMagnitude (PSQ4 only): the cb10 magnitude index of each value without its
+// sign, and no zeroing for s == 0 (the LSQ1 fit's first pass, whose decoded
+// values only enter |x| * |q| and q * q; with s == 0 every x is zero or NaN
+// and the fit ends at scale 0 either way).
+template <bool kPsq4, bool kMagnitude = false>
 __device__ __forceinline__ void psq_codes(const float (&x)[32], float s, uint32_t (&c)[32]) {
 #pragma clang fp contract(off)
     const float inv = 1.0f / s;
     const uint32_t keep = s > 0.0f ? 0xFFFFFFFFu : 0u;   // all codes 0 unless s > 0
     if constexpr (kPsq4) {
+        if constexpr (kMagnitude) {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) c[i] = cb10_code(x[i], inv) & keep;
+            for (int i = 0; i < 32; ++i) c[i] = cb10_code<false>(x[i], inv);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) c[i] = cb10_code(x[i], inv) & keep;
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i += 4) {
@@ -401,7 +412,11 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
     for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
     float s = amax > 0.0f ? psq_bf16_round(amax * (kPsq4 ? 0.1f : (1.0f / 448.0f))) : 0.0f;
     uint32_t c[32];
-    psq_codes<kPsq4>(x, s, c);
+    // LSQ1 (PSQ4): the first pass needs only the magnitudes; x * q with the
+    // signed q equals |x| * |q| bit for bit (the sign of a zero product aside,
+    // which cannot change a sum that has a nonzero term or the scale 0 of
+    // one that has none)
+    psq_codes<kPsq4, kPsq4 && kLsq1>(x, s, c);
 
     if constexpr (kLsq1) {
         // num = sum x q, den = sum q q over the decoded codes, in the
@@ -420,7 +435,7 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
             const float q[4] = {q01[0], q01[1], q23[0], q23[1]};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                nm[i + j] = x[i + j] * q[j];
+                nm[i + j] = (kPsq4 ? __builtin_fabsf(x[i + j]) : x[i + j]) * q[j];
                 dn[i + j] = q[j] * q[j];
             }
         }
