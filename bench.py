@@ -243,7 +243,7 @@ def run_psq(torch, ops, steps, warmup, dev):
     32768, 24/4 heads, hd256, page 16; planner-chosen split + combine) and the
     append of 2^16 rows (MaxAbs and LSQ1)."""
     import ctypes as C
-    from phaseshift_amd import KV_PSQ4, KV_PSQ8, check, lib
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8, check, lib, state
     L = lib()
     s = torch.cuda.current_stream().cuda_stream
     res = {}
@@ -340,8 +340,9 @@ def run_psq(torch, ops, steps, warmup, dev):
         torch.cuda.empty_cache()
 
         # prefill: config 5's 8 chunks of 512 causal rows (contexts U[2k, 16k]
-        # before the chunk) on the PSQ tile kernel, and the same rows on the
-        # PSQ decode kernel (the row-by-row path the tiles replace)
+        # before the chunk) through the step planner (grouped PSQ tiles), the
+        # reference's prefill launcher (implicit 16-row tiles, one head per
+        # wave) and the PSQ decode kernel (the row-by-row path tiles replace)
         rng = np.random.default_rng(5005)
         pre = rng.integers(2048, 16385, 8)
         lens = pre + 512
@@ -367,10 +368,17 @@ def run_psq(torch, ops, steps, warmup, dev):
         btd = torch.from_numpy(btp).to(dev)
         flops = float(sum(int(p0) * 512 + 512 * 513 // 2 for p0 in pre)) * QH * D * 4
         pt = {}
-        for kind, reps in (("prefill", steps), ("decode", 2)):
+        pa = ops.attention_args(gp, 0, q, out, pslots, ppos, btd, QH)
+        preqs = [(512 * i, 512, 2, int(lens[i])) for i in range(8)]
+        ppart = torch.empty((64 << 20) // 4, dtype=torch.float32, device=dev)
+        for kind, reps in (("planner", steps), ("prefill", max(2, steps // 4)), ("decode", 2)):
             def launch():
-                ops.paged_attention_psq(gp, 0, q, out, pslots, ppos, btd, kc, vc, ks, vs, QH, fmt,
-                                        kind=kind)
+                if kind == "planner":
+                    state.plan_step(pa, KV_PSQ4 if fmt == 4 else KV_PSQ8, preqs, int(lens.max()),
+                                    ppart.numel() * 4, ppart, kc, vc, ks, vs, launch=True)
+                else:
+                    ops.paged_attention_psq(gp, 0, q, out, pslots, ppos, btd, kc, vc, ks, vs, QH, fmt,
+                                            kind=kind)
 
             warm(torch, launch, 1 if kind == "decode" else warmup)
             t = Timer(torch)
@@ -379,10 +387,11 @@ def run_psq(torch, ops, steps, warmup, dev):
                     launch()
             pt[kind] = t.ms() / reps
         res[f"psq{fmt}_prefill_cfg5_chunks"] = dict(
-            rows=prow, tile_ms=round(pt["prefill"], 4), decode_path_ms=round(pt["decode"], 4),
-            tile_tflops=round(flops / (pt["prefill"] * 1e-3) / 1e12, 1),
-            speedup=round(pt["decode"] / pt["prefill"], 2))
-        del kc, vc, ks, vs, q, out
+            rows=prow, tile_ms=round(pt["planner"], 4),
+            tile_tflops=round(flops / (pt["planner"] * 1e-3) / 1e12, 1),
+            reference_launcher_ms=round(pt["prefill"], 4), decode_path_ms=round(pt["decode"], 4),
+            speedup=round(pt["decode"] / pt["planner"], 2))
+        del kc, vc, ks, vs, q, out, ppart
         torch.cuda.empty_cache()
     return res
 

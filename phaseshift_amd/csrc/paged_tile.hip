@@ -922,6 +922,458 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     }
 }
 
+// Grouped PSQ prefill tiles. Workgroup = (4 consecutive tiles of one
+// sequence, head pair, kv_head, split), 4 waves, wave w on tile w and both
+// heads of the pair (as the FP8 grouped tiles). Each 32-token chunk's PSQ
+// codes and block scales reach LDS by DMA; the workgroup then dequantizes
+// the chunk once, every K and V value to bf16(code value x block scale), into
+// a bf16 chunk in the BF16 tile layout, and the waves run the bf16 MFMA
+// score and PV products on it. The dequantization is shared by the 8
+// (tile, head) products of the workgroup instead of being repeated per head,
+// and no per-block scaling of scores or P remains.
+//
+// Chunk k: wait + barrier A (its codes landed; every wave is done with the
+// bf16 chunk k - 1), DMAs of chunk k + CS - 1 into code stage (k - 1) % CS,
+// dequantization of chunk k, barrier B, scores + softmax + PV of chunk k.
+template <int FMT>
+constexpr int pg_code_stages() { return FMT == kFmtPsq4 ? 3 : 2; }
+
+template <int FMT, int D>
+constexpr size_t tile_pg_lds_bytes() {
+    return (size_t)kTilePageWindow * 4 + (size_t)pg_code_stages<FMT>() * tile_stage_bytes<FMT, D>() +
+           (size_t)tile_stage_bytes<kFmtBf16, D>();
+}
+
+template <int FMT, int D, bool kAl16>
+__global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const TileParams p) {
+    constexpr int RT = kTileGroup;
+    constexpr int HPW = 2;
+    constexpr int H = 2;
+    constexpr int CT = 32;
+    constexpr int CB = code_bytes<FMT, D>();          // code bytes of one token's head slice
+    constexpr int NL = CB / 64;                       // 16 B DMA pieces per lane per half
+    constexpr int NS = D / 32;                        // K-steps (= 32-value blocks)
+    constexpr int NDB = D / 16;
+    constexpr int SW = D / 64;                        // scale dwords per token
+    constexpr int HSC = 16 * CB + 128;                // code half stride
+    constexpr int KVC = H * HSC;
+    constexpr int SC_BYTES = H * 256;
+    constexpr int CSTAGE = tile_stage_bytes<FMT, D>();
+    constexpr int CS = pg_code_stages<FMT>();
+    constexpr int HSB = 16 * 2 * D + 128;             // bf16 half stride
+    constexpr int KVB_BYTES = H * HSB;
+    constexpr int DPW = NL + 1;
+    constexpr int kWinBytes = (int)kTilePageWindow * 4;
+    constexpr int QD = D / 4;                         // dims one lane dequantizes per token row
+    static_assert(RT == 4 && NS % 2 == 0 && D % 128 == 0, "geometry");
+
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ uint32_t bad_lds;
+    __shared__ uint32_t group_vis;
+
+    const psk_paged_attention_args& a = p.a;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, w = tid >> 6;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t qpk = a.q_heads / a.kv_heads;
+
+    const uint32_t split = blockIdx.x % p.splits;
+    uint32_t rest = blockIdx.x / p.splits;
+    const uint32_t hparts = (qpk + HPW - 1u) / HPW;
+    const uint32_t hpart = rest % hparts;
+    rest /= hparts;
+    const uint32_t kv_head = rest % a.kv_heads;
+    const uint32_t group = rest / a.kv_heads;
+    if (p.n_tiles == 0u || group * RT >= p.n_tiles) return;
+    const uint32_t g0 = p.tile_begin[group * RT];
+    if (g0 >= a.rows) return;
+    const uint32_t slot = a.row_sequence_slots[g0];
+    if (slot >= a.max_sequences) return;
+    const uint32_t tile = group * RT + w;
+    const bool have = tile < p.n_tiles;
+    const uint32_t r0 = have ? p.tile_begin[tile] : g0;
+    uint32_t nrows = have ? p.tile_rows[tile] : 0u;
+    if (r0 >= a.rows) nrows = 0u;
+    nrows = min(nrows, a.rows - min(r0, a.rows));
+
+    const uint64_t cap = (uint64_t)a.block_table_stride * a.page_tokens;
+    const uint32_t row = r0 + n;
+    bool row_ok = n < nrows && a.row_sequence_slots[min(row, a.rows - 1u)] == slot;
+    uint32_t vis = 0;
+    if (row_ok) {
+        const uint64_t v64 = (uint64_t)a.row_positions[row] + 1u;
+        row_ok = v64 <= cap;
+        vis = row_ok ? (uint32_t)v64 : 0u;
+    }
+    uint32_t wave_vis = vis;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) wave_vis = max(wave_vis, (uint32_t)__shfl_xor((int)wave_vis, o, 64));
+    uint32_t wave_vis_min = row_ok ? vis : 0xFFFFFFFFu;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1)
+        wave_vis_min = min(wave_vis_min, (uint32_t)__shfl_xor((int)wave_vis_min, o, 64));
+    if (tid == 0) group_vis = 0u;
+    __syncthreads();
+    if (lane == 0) atomicMax(&group_vis, wave_vis);
+    __syncthreads();
+    const uint32_t vis_max = group_vis;
+    if (vis_max == 0u) return;   // uniform over the workgroup
+    const uint32_t P = a.page_tokens;
+    const uint32_t pc = (vis_max + P - 1u) / P;
+    const uint32_t per = p.pages_per_split != 0u ? p.pages_per_split : (pc + p.splits - 1u) / p.splits;
+    const uint32_t pb = split * per;
+    if (pb >= pc) return;
+    const uint32_t pe = (split == p.splits - 1u) ? pc : min(pc, pb + per);
+    const uint32_t t_begin = pb * P, t_end = min(pe * P, vis_max);
+    const uint32_t* bt = a.block_tables + (uint64_t)slot * a.block_table_stride;
+    const uint64_t scale_layer = (uint64_t)a.layer * a.num_pages;
+    // everything above is uniform over the workgroup: all waves reach the
+    // barriers below
+    const uint32_t hbase = hpart * HPW;
+    const bool computes = wave_vis > 0u;
+    bool hv[HPW];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) hv[i] = hbase + (uint32_t)i < qpk;
+    if (tid == 0) bad_lds = 0u;
+
+    // Q fragments as in the BF16 tiles: K-step s, dims 32s + 8g .. +8
+    bf16x8 qf[HPW][NS];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+        const uint32_t head = kv_head * qpk + (hv[i] ? hbase + (uint32_t)i : 0u);
+        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
+                               (uint64_t)(row_ok ? row : r0) * a.q_row_stride + (uint64_t)head * D;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) qf[i][s] = q8(qrow + s * 32 + (int)g * 8, row_ok && hv[i]);
+    }
+    float m_run[HPW], l_run[HPW];
+    f32x4 o[HPW][NDB];
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[i][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    // BF16 transposing V reads: token 4g + (n>>2) of each half, dims +4(n&3)
+    const uint32_t tr_off = 16u * (4u * g + (n >> 2)) + 256u * ((n >> 1) & 1u) + 8u * (n & 1u);
+
+    uint32_t* const win = reinterpret_cast<uint32_t*>(lds);
+    uint8_t* const cstages = lds + kWinBytes;
+    uint8_t* const bst = cstages + CS * CSTAGE;       // the bf16 chunk
+    const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
+    // dequantization: token row dr = tid / 4 (kind, half, token), dims
+    // [QD dq, QD (dq + 1))
+    const uint32_t dr = tid >> 2, dq = tid & 3u;
+    const uint32_t d_kind = dr >> 5, d_half = (dr >> 4) & 1u, d_tok = dr & 15u;
+
+    for (uint32_t wp = pb; wp < pe; wp += kTilePageWindow) {
+        const uint32_t wp_end = min(pe, wp + kTilePageWindow);
+        __syncthreads();
+        for (uint32_t i = tid; i < wp_end - wp; i += RT * 64u) win[i] = bt[wp + i];
+        __syncthreads();
+        const uint32_t ts = max(wp * P, t_begin);
+        const uint32_t te = min(wp_end * P, t_end);
+        if (ts >= te) continue;
+        const uint32_t t_last = te - 1u;
+        const uint32_t K = (te - ts + CT - 1u) / CT;
+        const uint32_t tok_bytes = a.kv_heads * (uint32_t)CB;
+        // wave wu: stream (K | V, half wu % 2) of chunk ci: NL code pieces and
+        // dword g of each token's block scales (lane groups past SW repeat one)
+        auto issue = [&](uint32_t ci, uint8_t* st) __attribute__((always_inline)) {
+            const uint32_t c = ts + ci * CT;
+            const uint32_t hf = wu % (uint32_t)H;
+            const uint32_t kind = wu / (uint32_t)H;
+            const uint32_t tau = min(c + hf * 16u + n, t_last);
+            uint32_t page, off;
+            if constexpr (kAl16) {
+                const uint32_t hb = min(c + hf * 16u, t_last);
+                const uint32_t pi = hb / P;
+                page = __builtin_amdgcn_readfirstlane(win[pi - wp]);
+                off = tau - pi * P;
+            } else {
+                page = win[tau / P - wp];
+                off = tau % P;
+            }
+            const bool inv = page >= a.num_pages;
+            if (inv) bad_lds = 1u;
+            const uint32_t pg = inv ? 0u : page;
+            const uint64_t slice0 = ((scale_layer + pg) * P * a.kv_heads + kv_head) * (uint64_t)CB;
+            const uint8_t* src = (kind == 0u ? p.k_pool : p.v_pool) + slice0;
+            uint8_t* dst = st + kind * KVC + hf * HSC;
+            const uint32_t lo = off * tok_bytes + g * 16u;
+#pragma unroll
+            for (int i = 0; i < NL; ++i) load_lds<16>(src + (lo + i * 64u), dst + i * 1024);
+            const uint64_t si = ((scale_layer + pg) * P + off) * a.kv_heads + kv_head;
+            const uint8_t* sbase = reinterpret_cast<const uint8_t*>(kind == 0u ? p.k_scale : p.v_scale);
+            load_lds<4>(sbase + si * (2u * D / 32u) + 4u * min(g, (uint32_t)SW - 1u),
+                        st + 2 * KVC + kind * SC_BYTES + hf * 256);
+        };
+        // code stage st -> bf16 chunk: this lane's token row, QD dims
+        auto dequant = [&](const uint8_t* st, uint8_t* bo) __attribute__((always_inline)) {
+            const uint8_t* cb = st + d_kind * KVC + d_half * HSC + 16u * d_tok;
+            const uint8_t* sc = st + 2 * KVC + d_kind * SC_BYTES + d_half * 256 + 4u * d_tok;
+            uint8_t* ob = bo + d_kind * KVB_BYTES + d_half * HSB + 16u * d_tok;
+#pragma unroll
+            for (int bl = 0; bl < QD / 32; ++bl) {
+                const uint32_t s = dq * (QD / 32) + bl;   // block
+                const uint32_t sw = *reinterpret_cast<const uint32_t*>(sc + 64u * (s >> 1));
+                const float scl = __uint_as_float((s & 1u) ? (sw & 0xFFFF0000u) : (sw << 16));
+                // the block's 32 values as E4M3 bytes, dims 32s + 0 .. 31
+                uint32_t e[8];
+                if constexpr (FMT == kFmtPsq8) {
+                    // bytes 32s .. +32 of the token: pieces (32s + 16j) / 16
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const uint32_t b = 32u * s + 16u * (uint32_t)j;
+                        const u32x4 x = *reinterpret_cast<const u32x4*>(cb + 1024u * (b >> 6) +
+                                                                        256u * ((b & 63u) >> 4));
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) e[4 * j + k] = x[k];
+                    }
+                } else {
+                    // bytes 16s .. +16: byte i low nibble = dim 32s + i, high = 32s + 16 + i
+                    const uint32_t b = 16u * s;
+                    const u32x4 x = *reinterpret_cast<const u32x4*>(cb + 1024u * (b >> 6) + 256u * ((b & 63u) >> 4));
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        e[k] = psq4_e4m3x4(x[k], false);
+                        e[4 + k] = psq4_e4m3x4(x[k], true);
+                    }
+                }
+                // bf16(value x scale): 32 values = 4 16 B pieces of the bf16 row
+#pragma unroll
+                for (int pc2 = 0; pc2 < 4; ++pc2) {
+                    u32x4 r;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t x = e[2 * pc2 + h];
+                        const f32x2 lo2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)x, false);
+                        const f32x2 hi2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)x, true);
+                        r[2 * h] = pack_bf16x2(lo2[0] * scl, lo2[1] * scl);
+                        r[2 * h + 1] = pack_bf16x2(hi2[0] * scl, hi2[1] * scl);
+                    }
+                    const uint32_t b = 64u * s + 16u * (uint32_t)pc2;   // bf16 row byte
+                    *reinterpret_cast<u32x4*>(ob + 1024u * (b >> 6) + 256u * ((b & 63u) >> 4)) = r;
+                }
+            }
+        };
+        // scores, causal online softmax and PV of the bf16 chunk at c
+        auto consume = [&](uint32_t c, const uint8_t* bi, auto full_tag) __attribute__((always_inline)) {
+            constexpr bool kFull = decltype(full_tag)::value;
+            constexpr int NP = NS / 2;
+            f32x4 sc[HPW][H];
+            struct KRaw {
+                u32x4 a, b;
+            };
+            auto kread = [&](int u) __attribute__((always_inline)) {
+                const uint8_t* kb = bi + (u / NP) * HSB + 16 * lane;
+                KRaw r;
+                r.a = *reinterpret_cast<const u32x4*>(kb + 1024 * (2 * (u % NP)));
+                r.b = *reinterpret_cast<const u32x4*>(kb + 1024 * (2 * (u % NP) + 1));
+                return r;
+            };
+            f32x4 acc[HPW];
+            KRaw cur = kread(0);
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int u = 0; u < H * NP; ++u) {
+                KRaw nxt = cur;
+                if (u + 1 < H * NP) nxt = kread(u + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                const int sp = u % NP;
+                if (sp == 0) {
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                }
+                const bf16x8 k0 = __builtin_bit_cast(bf16x8, cur.a);
+                const bf16x8 k1 = __builtin_bit_cast(bf16x8, cur.b);
+#pragma unroll
+                for (int i = 0; i < HPW; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[i][2 * sp], acc[i], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < HPW; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[i][2 * sp + 1], acc[i], 0, 0, 0);
+                if (sp == NP - 1) {
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i) sc[i][u / NP] = acc[i];
+                }
+                cur = nxt;
+            }
+            __builtin_amdgcn_s_setprio(0);
+            bool tok_ok[H][4];
+#pragma unroll
+            for (int hf = 0; hf < H; ++hf)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t tau = c + hf * 16 + 4 * g + r;
+                    tok_ok[hf][r] = kFull || (tau < vis && tau < te);
+                }
+            u32x4 pf[HPW];
+#pragma unroll
+            for (int i = 0; i < HPW; ++i) {
+                float s2[H][4];
+                float mx = -INFINITY;
+#pragma unroll
+                for (int hf = 0; hf < H; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        s2[hf][r] = tok_ok[hf][r] ? sc[i][hf][r] * p.scale_log2 : -INFINITY;
+                        mx = __builtin_fmaxf(mx, s2[hf][r]);
+                    }
+                mx = max_xor32(max_xor16(mx));
+                const bool moved = mx > m_run[i] + kLazyMaxSlack;
+                const float m_new = moved ? mx : m_run[i];
+                const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+                const float alpha = moved ? __builtin_amdgcn_exp2f(m_run[i] - m_use) : 1.0f;
+                float pv[H][4], psum = 0.0f;
+#pragma unroll
+                for (int hf = 0; hf < H; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = __builtin_amdgcn_exp2f(s2[hf][r] - m_use);
+                        psum += e;
+                        pv[hf][r] = e;
+                    }
+                l_run[i] = l_run[i] * alpha + psum;
+                m_run[i] = m_new;
+                if (__any(moved)) {
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) o[i][db] *= alpha;
+                }
+                // P as one bf16 operand
+                pf[i][0] = pack_bf16x2(pv[0][0], pv[0][1]);
+                pf[i][1] = pack_bf16x2(pv[0][2], pv[0][3]);
+                pf[i][2] = pack_bf16x2(pv[1][0], pv[1][1]);
+                pf[i][3] = pack_bf16x2(pv[1][2], pv[1][3]);
+            }
+            // O^T += V^T P^T, V^T fragments by transposing reads, in pairs of
+            // output blocks read one pair ahead
+            const uint8_t* vb = bi + KVB_BYTES + tr_off;
+            auto vread = [&](int db) __attribute__((always_inline)) {
+                const i16x4 x0 = tr16(vb + 512 * db);
+                const i16x4 x1 = tr16(vb + HSB + 512 * db);
+                return (u32x4){__builtin_bit_cast(u32x2, x0)[0], __builtin_bit_cast(u32x2, x0)[1],
+                               __builtin_bit_cast(u32x2, x1)[0], __builtin_bit_cast(u32x2, x1)[1]};
+            };
+            u32x4 vc[2] = {vread(0), vread(1)};
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int pr = 0; pr < NDB / 2; ++pr) {
+                u32x4 vn[2] = {vc[0], vc[1]};
+                if (pr + 1 < NDB / 2) {
+                    vn[0] = vread(2 * pr + 2);
+                    vn[1] = vread(2 * pr + 3);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const bf16x8 vf = __builtin_bit_cast(bf16x8, vc[j]);
+#pragma unroll
+                    for (int i = 0; i < HPW; ++i)
+                        o[i][2 * pr + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            vf, __builtin_bit_cast(bf16x8, pf[i]), o[i][2 * pr + j], 0, 0, 0);
+                }
+                vc[0] = vn[0];
+                vc[1] = vn[1];
+            }
+            __builtin_amdgcn_s_setprio(0);
+        };
+
+        // chunk k: barrier A, DMAs of chunk k + CS - 1, dequantization,
+        // barrier B, compute. __restrict__ tells the compiler that the DMAs
+        // into `next` and the reads of `cur` touch different LDS; their real
+        // ordering is the wait + barrier.
+        auto step = [&](uint32_t k, uint8_t* __restrict__ next, const uint8_t* __restrict__ cur,
+                        uint8_t* __restrict__ bchunk) __attribute__((always_inline)) {
+            issue(k + (uint32_t)CS - 1u, next);
+            dequant(cur, bchunk);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            const uint32_t c = ts + k * CT;
+            if (computes && c < wave_vis) {
+                if (c + CT <= wave_vis_min && c + CT <= te)
+                    consume(c, bchunk, std::true_type{});
+                else
+                    consume(c, bchunk, std::false_type{});
+            }
+        };
+#pragma unroll
+        for (int l = 0; l < CS - 1; ++l) issue((uint32_t)l, cstages + l * CSTAGE);
+        for (uint32_t k = 0; k < K; ++k) {
+            // chunk k landed (CS - 2 later chunks outstanding); every wave is
+            // done with the bf16 chunk and with code stage (k - 1) % CS
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((CS - 2) * DPW) : "memory");
+            step(k, cstages + ((k + (uint32_t)CS - 1u) % (uint32_t)CS) * CSTAGE, cstages + (k % (uint32_t)CS) * CSTAGE,
+                 bst);
+        }
+        wait_vmcnt<0>();   // the DMAs of chunks nobody reads
+    }
+    __syncthreads();
+    if (!computes) return;
+    float* part_row = nullptr;
+    if (p.partials != nullptr)
+        part_row = p.partials + ((uint64_t)(row * a.kv_heads + kv_head) * p.splits + split) *
+                                    (uint64_t)(qpk * (2u + kPagedAttentionHeadLimit));
+    if (bad_lds != 0u) {
+        if (part_row != nullptr && row_ok && g == 0) {
+#pragma unroll
+            for (int i = 0; i < HPW; ++i)
+                if (hv[i]) part_row[hbase + i] = __builtin_nanf("");
+        }
+        return;
+    }
+    if (!row_ok || t_begin >= vis) return;
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+        if (!hv[i]) continue;
+        const uint32_t gh = hbase + (uint32_t)i;
+        const uint32_t head = kv_head * qpk + gh;
+        const float l_all = sum_xor32(sum_xor16(l_run[i]));
+        if (part_row == nullptr) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const uint64_t oi = (uint64_t)row * a.output_row_stride + (uint64_t)head * D + db * 16 + 4 * g;
+                if (a.output_dtype == PSK_OUT_F32) {
+                    *reinterpret_cast<f32x4*>(static_cast<float*>(a.output) + oi) = o[i][db] / l_all;
+                } else {
+                    uint16_t* dst = static_cast<uint16_t*>(a.output) + oi;
+                    u32x2 pk;
+                    pk[0] = pack_bf16x2(o[i][db][0] / l_all, o[i][db][1] / l_all);
+                    pk[1] = pack_bf16x2(o[i][db][2] / l_all, o[i][db][3] / l_all);
+                    *reinterpret_cast<u32x2*>(dst) = pk;
+                }
+            }
+        } else {
+            if (g == 0) {
+                part_row[gh] = m_run[i] * 0.69314718055994531f;
+                part_row[qpk + gh] = l_all;
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+                *reinterpret_cast<f32x4*>(part_row + 2u * qpk + gh * kPagedAttentionHeadLimit + db * 16 + 4 * g) =
+                    o[i][db];
+        }
+    }
+}
+
+template <int FMT, int D, bool kAl16>
+hipError_t launch_tile_pg_t(const TileParams& p, uint64_t grid, hipStream_t stream) {
+    constexpr size_t lds_bytes = tile_pg_lds_bytes<FMT, D>();
+    static std::atomic<uint64_t> lds_ready{0};
+    const hipError_t attr =
+        allow_full_lds(reinterpret_cast<const void*>(&paged_tile_psq_group_kernel<FMT, D, kAl16>), lds_ready);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((paged_tile_psq_group_kernel<FMT, D, kAl16>), dim3((uint32_t)grid), dim3(256), lds_bytes,
+                       stream, p);
+    return hipGetLastError();
+}
+
+template <int FMT, int D>
+hipError_t launch_tile_pg(const TileParams& p, uint64_t grid, hipStream_t stream) {
+    return (p.a.page_tokens & 15u) == 0u ? launch_tile_pg_t<FMT, D, true>(p, grid, stream)
+                                         : launch_tile_pg_t<FMT, D, false>(p, grid, stream);
+}
+
 // kv_dtype: PSK_KV_*. PSQ: head_dim 128 or 256 (every (token, head) code
 // slice then starts on 16 B), scale pools 4 B aligned (checked by the
 // launchers that take them).
@@ -973,7 +1425,9 @@ hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream
 // one per tile, each on two heads of the group's head part, so each converted
 // K/V fragment feeds two MFMAs and two workgroups put 2 waves on every SIMD.
 // Wave counts that load the SIMDs unevenly (3 waves per workgroup) lose: the
-// chunk barrier waits on the doubly loaded SIMDs.
+// chunk barrier waits on the doubly loaded SIMDs. PSQ grouped launches go to
+// paged_tile_psq_group_kernel (the same workgroup shape on a shared bf16
+// dequantization of each chunk).
 template <int FMT, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
@@ -984,6 +1438,16 @@ hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
             const uint64_t grid = groups * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits;
             if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
             return launch_tile_t2<FMT, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
+        }
+    }
+    // PSQ grouped prefill tiles: one shared dequantization per chunk, then
+    // bf16 MFMAs (paged_tile_psq_group_kernel)
+    if constexpr (fmt_psq<FMT>()) {
+        if (p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u) {
+            const uint64_t groups = (tiles + kTileGroup - 1) / kTileGroup;
+            const uint64_t grid = groups * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits;
+            if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
+            return launch_tile_pg<FMT, D>(p, grid, stream);
         }
     }
     // PSQ: one head per wave only (its per-block scaling does not fit two
@@ -1111,6 +1575,14 @@ hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dty
 // kv_dtype: PSK_KV_*.
 uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q_per_kv) {
     const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
+    if ((kv_dtype == PSK_KV_PSQ4_W32 || kv_dtype == PSK_KV_PSQ8_W32) && q_per_kv > 4u && q_per_kv <= 6u) {
+        // grouped PSQ tiles: code stages + one bf16 chunk, 4 two-head waves
+        const size_t lds = kv_dtype == PSK_KV_PSQ4_W32
+                               ? (D == 256 ? tile_pg_lds_bytes<kFmtPsq4, 256>() : tile_pg_lds_bytes<kFmtPsq4, 128>())
+                               : (D == 256 ? tile_pg_lds_bytes<kFmtPsq8, 256>() : tile_pg_lds_bytes<kFmtPsq8, 128>());
+        const uint32_t by_lds = (uint32_t)((160u * 1024u) / (lds + 64u));
+        return by_lds < 2u ? (by_lds == 0u ? 1u : by_lds) : 2u;
+    }
     const size_t cb = kv_dtype == PSK_KV_BF16 ? 2 * D : kv_dtype == PSK_KV_PSQ4_W32 ? D / 2 : D;
     const size_t stage = 2 * 2 * (16 * cb + 128) + (kv_dtype != PSK_KV_BF16 ? 2 * 2 * 256 : 0);
     const size_t lds = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * stage + 64;
@@ -1123,10 +1595,9 @@ uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q
     return n == 0u ? 1u : n;
 }
 
-// Tiles per workgroup the step planner should group a prefill launch into
-// (PSQ tiles are not grouped). kv_dtype: PSK_KV_*.
-uint32_t tile_group_size(uint32_t q_per_kv, uint32_t kv_dtype) {
-    if (kv_dtype == PSK_KV_PSQ4_W32 || kv_dtype == PSK_KV_PSQ8_W32) return 1u;
+// Tiles per workgroup the step planner should group a prefill launch into:
+// kTileGroup for GQA groups of 5-6 heads, every KV format.
+uint32_t tile_group_size(uint32_t q_per_kv, uint32_t /*kv_dtype*/) {
     return q_per_kv > 4u && q_per_kv <= 6u ? (uint32_t)kTileGroup : 1u;
 }
 

@@ -576,3 +576,63 @@ def test_layer_offset_append_and_attention(dev, fmt):
     want_v = oracle_attn(lay, fmt, 24, qv, vs_, vp_, bt, pools, layer=1)
     got = run_attn(dev, lay, fmt, 24, qv, vs_, vp_, bt, pools, kind="prefill", layer=1)
     assert_attention_close(got, want_v, TOL, REL, f"psq{fmt} layer 1 tile")
+
+
+# ------------------------------------------------------- grouped prefill tiles
+
+def psq_grouped_step(dev, fmt, qh, kvh, D, P, split, seed):
+    """One planner step over PSQ pools whose prefill requests go to the
+    grouped tile kernel (GQA groups of 5-6 heads): 328 rows (the last group
+    padded, a partial last tile), 136 rows from position 0, 128 rows, a
+    16-row verify block and decode rows between them."""
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8, state
+    rng = np.random.default_rng(seed)
+    spec = [(1500, 328, 2), (900, 1, 0), (0, 136, 2), (2100, 1, 0), (700, 128, 2), (333, 16, 1)]
+    lens = [p + n for p, n, _ in spec]
+    lay = paged_layout(rng, lens, P, kvh, D, spare_pages=2)
+    pools = dev_pools(lay, fmt, dev, seed=seed)
+    slots, pos, reqs, row = [], [], [], 0
+    for s, (p, n, cls) in enumerate(spec):
+        slots += [s] * n
+        pos += list(range(p, p + n))
+        reqs.append((row, n, cls, p + n))
+        row += n
+    slots, pos = np.array(slots, np.uint32), np.array(pos, np.uint32)
+    q = bf16_normal(rng, (row, qh * D))
+    out = torch.full((row, qh * D), 7.0, dtype=torch.float32, device=dev)
+    a = ops.attention_args(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                           to_dev(lay.block_tables), qh)
+    nbytes = (64 << 20) if split else 0
+    part = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=dev) if split else None
+    plan = state.plan_step(a, KV_PSQ4 if fmt == 4 else KV_PSQ8, reqs, max(lens), nbytes, part,
+                           *pools, launch=True)
+    torch.cuda.synchronize()
+    want = oracle_attn(lay, fmt, qh, q, slots, pos, lay.block_tables, pools)
+    return plan, out.cpu().numpy(), want
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("qh,kvh", [(24, 4), (20, 4)])   # 6 heads per group; 5 (a half-empty head part)
+@pytest.mark.parametrize("split", [False, True])
+def test_grouped_prefill_tiles_vs_oracle(dev, fmt, qh, kvh, split):
+    """Grouped PSQ prefill tiles (one shared bf16 dequantization of every K/V
+    chunk, as the reference's PSQ prefill kernel rounds K and V to bf16),
+    split and unsplit, every row against the fp32 oracle."""
+    plan, got, want = psq_grouped_step(dev, fmt, qh, kvh, 256, 16, split, 90 + fmt + qh + split)
+    tiles = [k for k in plan.kernels[:plan.count] if k.kind == 1]
+    assert len(tiles) == 2                      # verify block and the prefill group launch
+    pre = max(tiles, key=lambda k: k.rows)
+    assert (pre.splits > 1) == split
+    assert not np.any(got == 7.0)
+    assert_attention_close(got, want, TOL, REL, f"test_gpu_psq 13 {(fmt, qh, split)}")
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("D,P", [(128, 16), (256, 24)])
+def test_grouped_prefill_tiles_d128_page24(dev, fmt, D, P):
+    """The grouped PSQ tiles at head_dim 128 and at page 24 (16-token halves
+    straddle pages)."""
+    qh, kvh = (12, 2) if D == 128 else (24, 4)
+    plan, got, want = psq_grouped_step(dev, fmt, qh, kvh, D, P, False, 95 + fmt + D + P)
+    assert not np.any(got == 7.0)
+    assert_attention_close(got, want, TOL, REL, f"test_gpu_psq 14 {(fmt, D, P)}")
