@@ -1062,10 +1062,12 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
     uint8_t* const cstages = lds + kWinBytes;
     uint8_t* const bst = cstages + CS * CSTAGE;       // the bf16 chunk
     const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
-    // dequantization: token row dr = tid / 4 (kind, half, token), dims
-    // [QD dq, QD (dq + 1))
-    const uint32_t dr = tid >> 2, dq = tid & 3u;
-    const uint32_t d_kind = dr >> 5, d_half = (dr >> 4) & 1u, d_tok = dr & 15u;
+    // dequantization: wave w takes (kind, half) = (w / 2, w % 2), lane (t, q)
+    // token t, dims [QD q, QD (q + 1)). The LDS serves 8 lanes of a 16 B
+    // access per clock; they are 8 tokens of one 16 B column, whose rows sit
+    // 16 B apart, so the 8 accesses hit distinct banks.
+    const uint32_t dq = g;
+    const uint32_t d_kind = w >> 1, d_half = w & 1u, d_tok = n;
 
     for (uint32_t wp = pb; wp < pe; wp += kTilePageWindow) {
         const uint32_t wp_end = min(pe, wp + kTilePageWindow);
