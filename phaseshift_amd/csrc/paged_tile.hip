@@ -926,14 +926,18 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
 // sequence, head pair, kv_head, split), 4 waves, wave w on tile w and both
 // heads of the pair (as the FP8 grouped tiles). Each 32-token chunk's PSQ
 // codes and block scales reach LDS by DMA; the workgroup then dequantizes
-// the chunk once, every K and V value to bf16(code value x block scale), into
-// a bf16 chunk in the BF16 tile layout, and the waves run the bf16 MFMA
-// score and PV products on it. The dequantization is shared by the 8
-// (tile, head) products of the workgroup instead of being repeated per head,
-// and no per-block scaling of scores or P remains.
+// the chunk once, every K and V value to f16(code value x block scale), into
+// an f16 chunk in the BF16 tile layout (16-bit values), and the waves run the
+// f16 MFMA score and PV products on it (Q and P as f16). The dequantization
+// is shared by the 8 (tile, head) products of the workgroup instead of being
+// repeated per head, and no per-block scaling of scores or P remains.
+// The scale's power of two rides on the E4M3 -> f16 conversion and its
+// mantissa (exact in f16) multiplies the f16 pairs, so each value is
+// rounded once, to f16 (11 bits; values below f16's normal range, 2^-14,
+// keep fewer bits).
 //
 // Chunk k: wait + barrier A (its codes landed; every wave is done with the
-// bf16 chunk k - 1), DMAs of chunk k + CS - 1 into code stage (k - 1) % CS,
+// f16 chunk k - 1), DMAs of chunk k + CS - 1 into code stage (k - 1) % CS,
 // dequantization of chunk k, barrier B, scores + softmax + PV of chunk k.
 template <int FMT>
 constexpr int pg_code_stages() { return FMT == kFmtPsq4 ? 3 : 2; }
@@ -960,7 +964,7 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
     constexpr int SC_BYTES = H * 256;
     constexpr int CSTAGE = tile_stage_bytes<FMT, D>();
     constexpr int CS = pg_code_stages<FMT>();
-    constexpr int HSB = 16 * 2 * D + 128;             // bf16 half stride
+    constexpr int HSB = 16 * 2 * D + 128;             // f16 half stride
     constexpr int KVB_BYTES = H * HSB;
     constexpr int DPW = NL + 1;
     constexpr int kWinBytes = (int)kTilePageWindow * 4;
@@ -1036,15 +1040,22 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
     for (int i = 0; i < HPW; ++i) hv[i] = hbase + (uint32_t)i < qpk;
     if (tid == 0) bad_lds = 0u;
 
-    // Q fragments as in the BF16 tiles: K-step s, dims 32s + 8g .. +8
-    bf16x8 qf[HPW][NS];
+    // Q fragments as f16, in the BF16 tiles' order: K-step s, dims 32s + 8g .. +8
+    f16x8 qf[HPW][NS];
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
         const uint32_t head = kv_head * qpk + (hv[i] ? hbase + (uint32_t)i : 0u);
         const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
                                (uint64_t)(row_ok ? row : r0) * a.q_row_stride + (uint64_t)head * D;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) qf[i][s] = q8(qrow + s * 32 + (int)g * 8, row_ok && hv[i]);
+        for (int s = 0; s < NS; ++s) {
+            const u32x4 w = __builtin_bit_cast(u32x4, q8(qrow + s * 32 + (int)g * 8, row_ok && hv[i]));
+            u32x4 h;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                h[k] = pack_f16x2(__uint_as_float(w[k] << 16), __uint_as_float(w[k] & 0xFFFF0000u));
+            qf[i][s] = __builtin_bit_cast(f16x8, h);
+        }
     }
     float m_run[HPW], l_run[HPW];
     f32x4 o[HPW][NDB];
@@ -1060,7 +1071,7 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
 
     uint32_t* const win = reinterpret_cast<uint32_t*>(lds);
     uint8_t* const cstages = lds + kWinBytes;
-    uint8_t* const bst = cstages + CS * CSTAGE;       // the bf16 chunk
+    uint8_t* const bst = cstages + CS * CSTAGE;       // the f16 chunk
     const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
     // dequantization: wave w takes (kind, half) = (w / 2, w % 2), lane (t, q)
     // token t, dims [QD q, QD (q + 1)). The LDS serves 8 lanes of a 16 B
@@ -1111,7 +1122,7 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
             load_lds<4>(sbase + si * (2u * D / 32u) + 4u * min(g, (uint32_t)SW - 1u),
                         st + 2 * KVC + kind * SC_BYTES + hf * 256);
         };
-        // code stage st -> bf16 chunk: this lane's token row, QD dims
+        // code stage st -> f16 chunk: this lane's token row, QD dims
         auto dequant = [&](const uint8_t* st, uint8_t* bo) __attribute__((always_inline)) {
             const uint8_t* cb = st + d_kind * KVC + d_half * HSC + 16u * d_tok;
             const uint8_t* sc = st + 2 * KVC + d_kind * SC_BYTES + d_half * 256 + 4u * d_tok;
@@ -1120,7 +1131,12 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
             for (int bl = 0; bl < QD / 32; ++bl) {
                 const uint32_t s = dq * (QD / 32) + bl;   // block
                 const uint32_t sw = *reinterpret_cast<const uint32_t*>(sc + 64u * (s >> 1));
-                const float scl = __uint_as_float((s & 1u) ? (sw & 0xFFFF0000u) : (sw << 16));
+                const uint32_t sb = (s & 1u) ? (sw & 0xFFFF0000u) : (sw << 16);   // the scale, f32 bits
+                // scale = 2^e x m: 2^e rides on the conversion, m in [1, 2)
+                // (exact in f16) multiplies the f16 pairs
+                const float s_pow2 = __uint_as_float(sb & 0x7F800000u);
+                const uint32_t m2 = pack_f16x2(__uint_as_float((sb & 0x807FFFFFu) | 0x3F800000u),
+                                               __uint_as_float((sb & 0x807FFFFFu) | 0x3F800000u));
                 // the block's 32 values as E4M3 bytes, dims 32s + 0 .. 31
                 uint32_t e[8];
                 if constexpr (FMT == kFmtPsq8) {
@@ -1143,24 +1159,24 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
                         e[4 + k] = psq4_e4m3x4(x[k], true);
                     }
                 }
-                // bf16(value x scale): 32 values = 4 16 B pieces of the bf16 row
+                // f16(value x scale): 32 values = 4 16 B pieces of the f16 row
 #pragma unroll
                 for (int pc2 = 0; pc2 < 4; ++pc2) {
                     u32x4 r;
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         const uint32_t x = e[2 * pc2 + h];
-                        const f32x2 lo2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)x, false);
-                        const f32x2 hi2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)x, true);
-                        r[2 * h] = pack_bf16x2(lo2[0] * scl, lo2[1] * scl);
-                        r[2 * h + 1] = pack_bf16x2(hi2[0] * scl, hi2[1] * scl);
+                        const f16x2 lo2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, s_pow2, false);
+                        const f16x2 hi2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, s_pow2, true);
+                        r[2 * h] = __builtin_bit_cast(uint32_t, lo2 * __builtin_bit_cast(f16x2, m2));
+                        r[2 * h + 1] = __builtin_bit_cast(uint32_t, hi2 * __builtin_bit_cast(f16x2, m2));
                     }
-                    const uint32_t b = 64u * s + 16u * (uint32_t)pc2;   // bf16 row byte
+                    const uint32_t b = 64u * s + 16u * (uint32_t)pc2;   // f16 row byte
                     *reinterpret_cast<u32x4*>(ob + 1024u * (b >> 6) + 256u * ((b & 63u) >> 4)) = r;
                 }
             }
         };
-        // scores, causal online softmax and PV of the bf16 chunk at c
+        // scores, causal online softmax and PV of the f16 chunk at c
         auto consume = [&](uint32_t c, const uint8_t* bi, auto full_tag) __attribute__((always_inline)) {
             constexpr bool kFull = decltype(full_tag)::value;
             constexpr int NP = NS / 2;
@@ -1188,14 +1204,14 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
 #pragma unroll
                     for (int i = 0; i < HPW; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
                 }
-                const bf16x8 k0 = __builtin_bit_cast(bf16x8, cur.a);
-                const bf16x8 k1 = __builtin_bit_cast(bf16x8, cur.b);
+                const f16x8 k0 = __builtin_bit_cast(f16x8, cur.a);
+                const f16x8 k1 = __builtin_bit_cast(f16x8, cur.b);
 #pragma unroll
                 for (int i = 0; i < HPW; ++i)
-                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[i][2 * sp], acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qf[i][2 * sp], acc[i], 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < HPW; ++i)
-                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[i][2 * sp + 1], acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qf[i][2 * sp + 1], acc[i], 0, 0, 0);
                 if (sp == NP - 1) {
 #pragma unroll
                     for (int i = 0; i < HPW; ++i) sc[i][u / NP] = acc[i];
@@ -1243,11 +1259,11 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
 #pragma unroll
                     for (int db = 0; db < NDB; ++db) o[i][db] *= alpha;
                 }
-                // P as one bf16 operand
-                pf[i][0] = pack_bf16x2(pv[0][0], pv[0][1]);
-                pf[i][1] = pack_bf16x2(pv[0][2], pv[0][3]);
-                pf[i][2] = pack_bf16x2(pv[1][0], pv[1][1]);
-                pf[i][3] = pack_bf16x2(pv[1][2], pv[1][3]);
+                // P as one f16 operand
+                pf[i][0] = pack_f16x2(pv[0][0], pv[0][1]);
+                pf[i][1] = pack_f16x2(pv[0][2], pv[0][3]);
+                pf[i][2] = pack_f16x2(pv[1][0], pv[1][1]);
+                pf[i][3] = pack_f16x2(pv[1][2], pv[1][3]);
             }
             // O^T += V^T P^T, V^T fragments by transposing reads, in pairs of
             // output blocks read one pair ahead
@@ -1270,11 +1286,11 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const bf16x8 vf = __builtin_bit_cast(bf16x8, vc[j]);
+                    const f16x8 vf = __builtin_bit_cast(f16x8, vc[j]);
 #pragma unroll
                     for (int i = 0; i < HPW; ++i)
-                        o[i][2 * pr + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            vf, __builtin_bit_cast(bf16x8, pf[i]), o[i][2 * pr + j], 0, 0, 0);
+                        o[i][2 * pr + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            vf, __builtin_bit_cast(f16x8, pf[i]), o[i][2 * pr + j], 0, 0, 0);
                 }
                 vc[0] = vn[0];
                 vc[1] = vn[1];
@@ -1303,7 +1319,7 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
         for (int l = 0; l < CS - 1; ++l) issue((uint32_t)l, cstages + l * CSTAGE);
         for (uint32_t k = 0; k < K; ++k) {
             // chunk k landed (CS - 2 later chunks outstanding); every wave is
-            // done with the bf16 chunk and with code stage (k - 1) % CS
+            // done with the f16 chunk and with code stage (k - 1) % CS
             asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((CS - 2) * DPW) : "memory");
             step(k, cstages + ((k + (uint32_t)CS - 1u) % (uint32_t)CS) * CSTAGE, cstages + (k % (uint32_t)CS) * CSTAGE,
                  bst);
@@ -1428,7 +1444,7 @@ hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream
 // K/V fragment feeds two MFMAs and two workgroups put 2 waves on every SIMD.
 // Wave counts that load the SIMDs unevenly (3 waves per workgroup) lose: the
 // chunk barrier waits on the doubly loaded SIMDs. PSQ grouped launches go to
-// paged_tile_psq_group_kernel (the same workgroup shape on a shared bf16
+// paged_tile_psq_group_kernel (the same workgroup shape on a shared f16
 // dequantization of each chunk).
 template <int FMT, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
@@ -1443,7 +1459,7 @@ hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
         }
     }
     // PSQ grouped prefill tiles: one shared dequantization per chunk, then
-    // bf16 MFMAs (paged_tile_psq_group_kernel)
+    // f16 MFMAs (paged_tile_psq_group_kernel)
     if constexpr (fmt_psq<FMT>()) {
         if (p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u) {
             const uint64_t groups = (tiles + kTileGroup - 1) / kTileGroup;
