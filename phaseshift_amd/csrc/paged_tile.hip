@@ -161,8 +161,8 @@ constexpr int tile_waves_per_simd(int hpw) { return hpw == 1 ? 3 : 2; }
 template <int FMT, int D, int NW, int HPW, int RT, bool kAl16>
 __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_kernel(const TileParams p) {
     static_assert(RT == 1 || RT == NW, "grouped tiles: one wave per tile");
-    constexpr int KVB = FMT == kFmtBf16 ? 2 : 1;   // bytes per value (PSQ4: codes of 2 values per byte)
-    constexpr bool kPsq = fmt_psq<FMT>();
+    static_assert(FMT == kFmtBf16 || FMT == kFmtFp8, "PSQ tiles: paged_tile_psq_group_kernel");
+    constexpr int KVB = FMT == kFmtBf16 ? 2 : 1;   // bytes per value
     constexpr int CB = code_bytes<FMT, D>();       // K (V) bytes of one token's head slice
     constexpr int WH = NW / RT;          // waves along the heads of one tile
     constexpr int H = 2;                 // 16-token halves per chunk
@@ -178,10 +178,6 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     constexpr int KV_BYTES = H * HALF_STRIDE;
     constexpr int SC_BYTES = KVB == 1 ? H * 256 : 0;
     constexpr int STAGE = tile_stage_bytes<FMT, D>();
-    // PSQ: dwords of block scales per (token, head); byte offsets of one
-    // (token, head) slice's codes and scales are its slice index times CB and
-    // times 2 * D / 32
-    constexpr int SW = D / 64;
     // DMA instructions of one chunk (K, V, then FP8 k/v scales), dealt
     // round-robin over the NW waves; every wave issues DPW of them (the
     // remainder repeats earlier ones, which rewrite identical bytes), so the
@@ -309,17 +305,10 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         } else {
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                if constexpr (FMT == kFmtPsq4) {
-                    // K-step s = block s: dims 4g.. and 16 + 4g.. (nibbles)
-                    qf[i][s] = load_q4x2(qrow + s * 32 + (int)g * 4, row_ok && hv[i]);
-                } else {
-                    // BF16, PSQ8 (K-step s = block s): dims 32s + 8g..; FP8:
-                    // the 16 B of 64-dim block s/2 split in two K-steps
-                    const int d0 = (FMT == kFmtBf16 || FMT == kFmtPsq8)
-                                       ? s * 32 + (int)g * 8
-                                       : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
-                    qf[i][s] = q8(qrow + d0, row_ok && hv[i]);
-                }
+                // BF16: dims 32s + 8g..; FP8: the 16 B of 64-dim block s/2
+                // split in two K-steps
+                const int d0 = FMT == kFmtBf16 ? s * 32 + (int)g * 8 : (s >> 1) * 64 + (int)g * 16 + (s & 1) * 8;
+                qf[i][s] = q8(qrow + d0, row_ok && hv[i]);
             }
         }
     }
@@ -367,28 +356,17 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         if (ts >= te) continue;
         const uint32_t t_last = te - 1u;
 
-        // Byte offset of the (page pg, token 0, kv_head) slice in a code
-        // pool, and the bytes between consecutive tokens' slices. PSQ slices
-        // are indexed like their scales: ((layer * pages + pg) * P + off) *
-        // kv_heads + kv_head, CB bytes each.
+        // Byte offset of the (page pg, token 0, kv_head) slice in a pool, and
+        // the bytes between consecutive tokens' slices
         auto slice_base = [&](uint32_t pg) __attribute__((always_inline)) -> uint64_t {
-            if constexpr (kPsq)
-                return ((scale_layer + pg) * P * a.kv_heads + kv_head) * (uint64_t)CB;
-            else
-                return (layer_base + (uint64_t)pg * a.elems_per_page + (uint64_t)kv_head * D) * KVB;
+            return (layer_base + (uint64_t)pg * a.elems_per_page + (uint64_t)kv_head * D) * KVB;
         };
-        const uint32_t tok_bytes = kPsq ? a.kv_heads * (uint32_t)CB : a.elems_per_token * (uint32_t)KVB;
-        // Source of this lane's scale DMA for the token at (pg, off): FP8 its
-        // f32 scale; PSQ dword g of its block scales (lanes past the last
-        // dword repeat it)
+        const uint32_t tok_bytes = a.elems_per_token * (uint32_t)KVB;
+        // Source of this lane's FP8 scale DMA for the token at (pg, off)
         auto scale_src = [&](uint32_t kind, uint32_t pg, uint32_t off) __attribute__((always_inline)) {
             const uint64_t si = ((scale_layer + pg) * P + off) * a.kv_heads + kv_head;
             const float* base = kind == 0u ? k_scale : v_scale;
-            if constexpr (kPsq)
-                return static_cast<const void*>(reinterpret_cast<const uint8_t*>(base) + si * (2u * D / 32u) +
-                                                4u * min(g, (uint32_t)SW - 1u));
-            else
-                return static_cast<const void*>(base + si);
+            return static_cast<const void*>(base + si);
         };
 
         // This wave's DMAs of the chunk at c into stage st (branch-free;
@@ -479,57 +457,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         auto consume = [&](uint32_t c, const uint8_t* st, auto full_tag) __attribute__((always_inline)) {
             constexpr bool kFull = decltype(full_tag)::value;
             f32x4 sc[HPW][H];
-            if constexpr (kPsq) {
-                // K-step s = block s: the block's partial scores times its K
-                // scale of each token 4g + r (bf16 -> f32 by shift); every
-                // converted K fragment feeds the MFMAs of all HPW heads
-#pragma unroll
-                for (int hf = 0; hf < H; ++hf) {
-                    const uint8_t* kb = st + hf * HALF_STRIDE;
-                    const uint8_t* kscl = st + 2 * KV_BYTES + hf * 256 + 16 * g;
-                    f32x4 acc[HPW];
-#pragma unroll
-                    for (int s = 0; s < NS; ++s) {
-                        // one K-step at a time: unbounded hoisting of the
-                        // LDS reads across steps spills registers
-                        __builtin_amdgcn_sched_barrier(0);
-                        bf16x8 kf;
-                        if constexpr (FMT == kFmtPsq8) {
-                            // bytes 32s + 8g .. +8 of token n
-                            const u32x2 w = *reinterpret_cast<const u32x2*>(
-                                kb + 1024 * (s >> 1) + 16 * (16 * (2 * (s & 1) + (int)(g >> 1)) + (int)n) +
-                                8 * (int)(g & 1u));
-                            kf = fp8x8_to_bf16x8(w[0], w[1]);
-                        } else {
-                            // bytes 16s + 4g .. +4 of token n: dims 4g.. (low
-                            // nibbles) and 16 + 4g.. (high nibbles) of block s
-                            const uint32_t x = *reinterpret_cast<const uint32_t*>(kb + 256 * s + 16 * n + 4 * g);
-                            const uint32_t lo = psq4_e4m3x4(x, false), hi = psq4_e4m3x4(x, true);
-                            u32x4 r;
-                            r[0] = fp8x2_to_bf16x2(lo, false);
-                            r[1] = fp8x2_to_bf16x2(lo, true);
-                            r[2] = fp8x2_to_bf16x2(hi, false);
-                            r[3] = fp8x2_to_bf16x2(hi, true);
-                            kf = __builtin_bit_cast(bf16x8, r);
-                        }
-                        const u32x4 kw = *reinterpret_cast<const u32x4*>(kscl + 64 * (s >> 1));
-                        float ksc[4];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            ksc[r] = __uint_as_float((s & 1) ? (kw[r] & 0xFFFF0000u) : (kw[r] << 16));
-#pragma unroll
-                        for (int i = 0; i < HPW; ++i) {
-                            const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                kf, qf[i][s], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                acc[i][r] = s == 0 ? part[r] * ksc[r] : __builtin_fmaf(part[r], ksc[r], acc[i][r]);
-                        }
-                    }
-#pragma unroll
-                    for (int i = 0; i < HPW; ++i) sc[i][hf] = acc[i];
-                }
-            } else if constexpr (kF8Mfma) {
+            if constexpr (kF8Mfma) {
                 // 128 dims per MFMA: the lane's 16 B of blocks 2j and 2j + 1
                 // (one half), read one step ahead of the MFMAs they feed
                 constexpr int NJ = D / 128;
@@ -661,7 +589,6 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 }
             }
             u32x4 pf[HPW], pl[HPW];
-            float pw[kPsq ? HPW : 1][H][4];   // PSQ: P before the per-block V scales
 #pragma unroll
             for (int i = 0; i < HPW; ++i) {
                 // scores in log2 units are s2 * qinv[i]: qinv > 0 scales the
@@ -698,12 +625,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
 #pragma unroll
                     for (int db = 0; db < NDB; ++db) o[i][db] *= alpha;
                 }
-                if constexpr (kPsq) {
-#pragma unroll
-                    for (int hf = 0; hf < H; ++hf)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) pw[i][hf][r] = pv[hf][r];
-                } else if constexpr (KVB == 1) {
+                if constexpr (KVB == 1) {
                     // FP8: P (v_scale folded in) as one f16 operand (11 mantissa
                     // bits); V as f16 (E4M3 values are exact in f16)
                     pf[i][0] = pack_f16x2(pv[0][0], pv[0][1]);
@@ -724,60 +646,6 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
             // V is read in pairs of output blocks, each pair's transposing LDS
             // reads issued one pair ahead of the previous pair's MFMAs.
             const uint8_t* vb = st + KV_BYTES + tr_off;
-            if constexpr (kPsq) {
-                // Per block b: P times the block's V scale of each of the
-                // lane's tokens (4g + r of both halves), one bf16 P operand per
-                // head; the block's V^T fragments are converted once for all
-                // heads (PSQ8: output blocks 2b, 2b + 1; PSQ4: byte i of the
-                // block holds dims i and 16 + i).
-                const uint8_t* vscl = st + 2 * KV_BYTES + SC_BYTES + 16 * g;
-#pragma unroll
-                for (int b = 0; b < NS; ++b) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    const u32x4 w0 = *reinterpret_cast<const u32x4*>(vscl + 64 * (b >> 1));
-                    const u32x4 w1 = *reinterpret_cast<const u32x4*>(vscl + 256 + 64 * (b >> 1));
-                    float vs0[4], vs1[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        vs0[r] = __uint_as_float((b & 1) ? (w0[r] & 0xFFFF0000u) : (w0[r] << 16));
-                        vs1[r] = __uint_as_float((b & 1) ? (w1[r] & 0xFFFF0000u) : (w1[r] << 16));
-                    }
-                    bf16x8 pb[HPW];
-#pragma unroll
-                    for (int i = 0; i < HPW; ++i) {
-                        u32x4 ph;
-                        ph[0] = pack_bf16x2(pw[i][0][0] * vs0[0], pw[i][0][1] * vs0[1]);
-                        ph[1] = pack_bf16x2(pw[i][0][2] * vs0[2], pw[i][0][3] * vs0[3]);
-                        ph[2] = pack_bf16x2(pw[i][1][0] * vs1[0], pw[i][1][1] * vs1[1]);
-                        ph[3] = pack_bf16x2(pw[i][1][2] * vs1[2], pw[i][1][3] * vs1[3]);
-                        pb[i] = __builtin_bit_cast(bf16x8, ph);
-                    }
-                    if constexpr (FMT == kFmtPsq8) {
-#pragma unroll
-                        for (int h = 0; h < 2; ++h) {
-                            const i32x2 w = tr8(vb + 256 * (2 * b + h));
-                            const bf16x8 vf = fp8x8_to_bf16x8((uint32_t)w[0], (uint32_t)w[1]);
-#pragma unroll
-                            for (int i = 0; i < HPW; ++i)
-                                o[i][2 * b + h] =
-                                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[i], o[i][2 * b + h], 0, 0, 0);
-                        }
-                    } else {
-                        const i32x2 w = tr8(vb + 256 * b);
-                        const bf16x8 vlo = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)w[0], false),
-                                                           psq4_e4m3x4((uint32_t)w[1], false));
-                        const bf16x8 vhi = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)w[0], true),
-                                                           psq4_e4m3x4((uint32_t)w[1], true));
-#pragma unroll
-                        for (int i = 0; i < HPW; ++i) {
-                            o[i][2 * b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vlo, pb[i], o[i][2 * b], 0, 0, 0);
-                            o[i][2 * b + 1] =
-                                __builtin_amdgcn_mfma_f32_16x16x32_bf16(vhi, pb[i], o[i][2 * b + 1], 0, 0, 0);
-                        }
-                    }
-                }
-                return;
-            }
             static_assert(NDB % 2 == 0, "output blocks in pairs");
             struct VRaw {
                 u32x4 x[2];
@@ -948,10 +816,12 @@ constexpr size_t tile_pg_lds_bytes() {
            (size_t)tile_stage_bytes<kFmtBf16, D>();
 }
 
-template <int FMT, int D, bool kAl16>
-__global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const TileParams p) {
-    constexpr int RT = kTileGroup;
-    constexpr int HPW = 2;
+// RT == kTileGroup (grouped prefill): wave w owns tile w of the group and
+// the HPW = 2 heads of the workgroup's head pair. RT == 1 (verify blocks,
+// implicit tiles, other group sizes): the NW waves own HPW = 1 head each of
+// one tile. The first 4 waves issue the DMAs and dequantize.
+template <int FMT, int D, int NW, int HPW, int RT, bool kAl16>
+__global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_psq_group_kernel(const TileParams p) {
     constexpr int H = 2;
     constexpr int CT = 32;
     constexpr int CB = code_bytes<FMT, D>();          // code bytes of one token's head slice
@@ -969,7 +839,8 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
     constexpr int DPW = NL + 1;
     constexpr int kWinBytes = (int)kTilePageWindow * 4;
     constexpr int QD = D / 4;                         // dims one lane dequantizes per token row
-    static_assert(RT == 4 && NS % 2 == 0 && D % 128 == 0, "geometry");
+    static_assert((RT == NW && HPW == 2) || (RT == 1 && HPW == 1), "tile geometry");
+    static_assert(NW >= 4 && NS % 2 == 0 && D % 128 == 0, "geometry");
 
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ uint32_t bad_lds;
@@ -983,20 +854,35 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
 
     const uint32_t split = blockIdx.x % p.splits;
     uint32_t rest = blockIdx.x / p.splits;
-    const uint32_t hparts = (qpk + HPW - 1u) / HPW;
-    const uint32_t hpart = rest % hparts;
-    rest /= hparts;
+    uint32_t hpart = 0;
+    if constexpr (RT > 1) {
+        const uint32_t hparts = (qpk + HPW - 1u) / HPW;
+        hpart = rest % hparts;
+        rest /= hparts;
+    }
     const uint32_t kv_head = rest % a.kv_heads;
     const uint32_t group = rest / a.kv_heads;
-    if (p.n_tiles == 0u || group * RT >= p.n_tiles) return;
-    const uint32_t g0 = p.tile_begin[group * RT];
+    // the group's first tile names the sequence (workgroup-uniform)
+    uint32_t g0;
+    if (p.n_tiles != 0u) {
+        if (group * RT >= p.n_tiles) return;
+        g0 = p.tile_begin[group * RT];
+    } else {
+        g0 = group * RT * kTileRows;
+    }
     if (g0 >= a.rows) return;
     const uint32_t slot = a.row_sequence_slots[g0];
     if (slot >= a.max_sequences) return;
-    const uint32_t tile = group * RT + w;
-    const bool have = tile < p.n_tiles;
-    const uint32_t r0 = have ? p.tile_begin[tile] : g0;
-    uint32_t nrows = have ? p.tile_rows[tile] : 0u;
+    const uint32_t tile = group * RT + (RT > 1 ? w : 0u);
+    uint32_t r0, nrows;
+    if (p.n_tiles != 0u) {
+        const bool have = tile < p.n_tiles;
+        r0 = have ? p.tile_begin[tile] : g0;
+        nrows = have ? p.tile_rows[tile] : 0u;
+    } else {
+        r0 = tile * kTileRows;
+        nrows = r0 < a.rows ? min((uint32_t)kTileRows, a.rows - r0) : 0u;
+    }
     if (r0 >= a.rows) nrows = 0u;
     nrows = min(nrows, a.rows - min(r0, a.rows));
 
@@ -1016,11 +902,15 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1)
         wave_vis_min = min(wave_vis_min, (uint32_t)__shfl_xor((int)wave_vis_min, o, 64));
-    if (tid == 0) group_vis = 0u;
-    __syncthreads();
-    if (lane == 0) atomicMax(&group_vis, wave_vis);
-    __syncthreads();
-    const uint32_t vis_max = group_vis;
+    uint32_t vis_max = wave_vis;   // RT == 1: every wave holds the tile's rows
+    if constexpr (RT > 1) {
+        // the workgroup streams the longest visible range of its tiles
+        if (tid == 0) group_vis = 0u;
+        __syncthreads();
+        if (lane == 0) atomicMax(&group_vis, wave_vis);
+        __syncthreads();
+        vis_max = group_vis;
+    }
     if (vis_max == 0u) return;   // uniform over the workgroup
     const uint32_t P = a.page_tokens;
     const uint32_t pc = (vis_max + P - 1u) / P;
@@ -1033,8 +923,8 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
     const uint64_t scale_layer = (uint64_t)a.layer * a.num_pages;
     // everything above is uniform over the workgroup: all waves reach the
     // barriers below
-    const uint32_t hbase = hpart * HPW;
-    const bool computes = wave_vis > 0u;
+    const uint32_t hbase = RT > 1 ? hpart * HPW : w * HPW;   // first head (group index)
+    const bool computes = hbase < qpk && wave_vis > 0u;
     bool hv[HPW];
 #pragma unroll
     for (int i = 0; i < HPW; ++i) hv[i] = hbase + (uint32_t)i < qpk;
@@ -1083,7 +973,7 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
     for (uint32_t wp = pb; wp < pe; wp += kTilePageWindow) {
         const uint32_t wp_end = min(pe, wp + kTilePageWindow);
         __syncthreads();
-        for (uint32_t i = tid; i < wp_end - wp; i += RT * 64u) win[i] = bt[wp + i];
+        for (uint32_t i = tid; i < wp_end - wp; i += NW * 64u) win[i] = bt[wp + i];
         __syncthreads();
         const uint32_t ts = max(wp * P, t_begin);
         const uint32_t te = min(wp_end * P, t_end);
@@ -1094,6 +984,7 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
         // wave wu: stream (K | V, half wu % 2) of chunk ci: NL code pieces and
         // dword g of each token's block scales (lane groups past SW repeat one)
         auto issue = [&](uint32_t ci, uint8_t* st) __attribute__((always_inline)) {
+            if (NW > 4 && wu >= 4u) return;
             const uint32_t c = ts + ci * CT;
             const uint32_t hf = wu % (uint32_t)H;
             const uint32_t kind = wu / (uint32_t)H;
@@ -1124,6 +1015,7 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
         };
         // code stage st -> f16 chunk: this lane's token row, QD dims
         auto dequant = [&](const uint8_t* st, uint8_t* bo) __attribute__((always_inline)) {
+            if (NW > 4 && wu >= 4u) return;
             const uint8_t* cb = st + d_kind * KVC + d_half * HSC + 16u * d_tok;
             const uint8_t* sc = st + 2 * KVC + d_kind * SC_BYTES + d_half * 256 + 4u * d_tok;
             uint8_t* ob = bo + d_kind * KVB_BYTES + d_half * HSB + 16u * d_tok;
@@ -1374,22 +1266,22 @@ __global__ __launch_bounds__(256, 2) void paged_tile_psq_group_kernel(const Tile
     }
 }
 
-template <int FMT, int D, bool kAl16>
+template <int FMT, int D, int NW, int HPW, int RT, bool kAl16>
 hipError_t launch_tile_pg_t(const TileParams& p, uint64_t grid, hipStream_t stream) {
     constexpr size_t lds_bytes = tile_pg_lds_bytes<FMT, D>();
     static std::atomic<uint64_t> lds_ready{0};
-    const hipError_t attr =
-        allow_full_lds(reinterpret_cast<const void*>(&paged_tile_psq_group_kernel<FMT, D, kAl16>), lds_ready);
+    const hipError_t attr = allow_full_lds(
+        reinterpret_cast<const void*>(&paged_tile_psq_group_kernel<FMT, D, NW, HPW, RT, kAl16>), lds_ready);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((paged_tile_psq_group_kernel<FMT, D, kAl16>), dim3((uint32_t)grid), dim3(256), lds_bytes,
-                       stream, p);
+    hipLaunchKernelGGL((paged_tile_psq_group_kernel<FMT, D, NW, HPW, RT, kAl16>), dim3((uint32_t)grid),
+                       dim3(NW * 64), lds_bytes, stream, p);
     return hipGetLastError();
 }
 
-template <int FMT, int D>
+template <int FMT, int D, int NW, int HPW, int RT>
 hipError_t launch_tile_pg(const TileParams& p, uint64_t grid, hipStream_t stream) {
-    return (p.a.page_tokens & 15u) == 0u ? launch_tile_pg_t<FMT, D, true>(p, grid, stream)
-                                         : launch_tile_pg_t<FMT, D, false>(p, grid, stream);
+    return (p.a.page_tokens & 15u) == 0u ? launch_tile_pg_t<FMT, D, NW, HPW, RT, true>(p, grid, stream)
+                                         : launch_tile_pg_t<FMT, D, NW, HPW, RT, false>(p, grid, stream);
 }
 
 // kv_dtype: PSK_KV_*. PSQ: head_dim 128 or 256 (every (token, head) code
@@ -1450,35 +1342,23 @@ template <int FMT, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     const uint64_t tiles = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1) / kTileRows;
-    if constexpr (!fmt_psq<FMT>()) {
-        if (p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u) {
-            const uint64_t groups = (tiles + kTileGroup - 1) / kTileGroup;
-            const uint64_t grid = groups * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits;
-            if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-            return launch_tile_t2<FMT, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
-        }
-    }
-    // PSQ grouped prefill tiles: one shared dequantization per chunk, then
-    // f16 MFMAs (paged_tile_psq_group_kernel)
-    if constexpr (fmt_psq<FMT>()) {
-        if (p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u) {
-            const uint64_t groups = (tiles + kTileGroup - 1) / kTileGroup;
-            const uint64_t grid = groups * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits;
-            if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-            return launch_tile_pg<FMT, D>(p, grid, stream);
-        }
-    }
-    // PSQ: one head per wave only (its per-block scaling does not fit two
-    // heads' accumulators and Q fragments in 256 registers); a grouped tile
-    // list runs tile by tile (padding tiles have no rows and exit)
-    const uint64_t grid = tiles * p.a.kv_heads * p.splits;
+    const bool grouped = p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u;
+    const uint64_t grid = grouped ? (tiles + kTileGroup - 1) / kTileGroup * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits
+                                  : tiles * p.a.kv_heads * p.splits;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    if (qpk <= 4u) return launch_tile_t2<FMT, D, 4, 1>(p, grid, stream);
-    if (qpk <= 6u) return launch_tile_t2<FMT, D, 6, 1>(p, grid, stream);
-    if constexpr (fmt_psq<FMT>())
-        return launch_tile_t2<FMT, D, 8, 1>(p, grid, stream);
-    else
+    if constexpr (fmt_psq<FMT>()) {
+        // PSQ: one shared f16 dequantization per chunk, then f16 MFMAs
+        // (paged_tile_psq_group_kernel); ungrouped one head per wave
+        if (grouped) return launch_tile_pg<FMT, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
+        if (qpk <= 4u) return launch_tile_pg<FMT, D, 4, 1, 1>(p, grid, stream);
+        if (qpk <= 6u) return launch_tile_pg<FMT, D, 6, 1, 1>(p, grid, stream);
+        return launch_tile_pg<FMT, D, 8, 1, 1>(p, grid, stream);
+    } else {
+        if (grouped) return launch_tile_t2<FMT, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
+        if (qpk <= 4u) return launch_tile_t2<FMT, D, 4, 1>(p, grid, stream);
+        if (qpk <= 6u) return launch_tile_t2<FMT, D, 6, 1>(p, grid, stream);
         return launch_tile_t2<FMT, D, 4, 2>(p, grid, stream);
+    }
 }
 
 template <int FMT>
@@ -1593,21 +1473,25 @@ hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dty
 // kv_dtype: PSK_KV_*.
 uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q_per_kv) {
     const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
-    if ((kv_dtype == PSK_KV_PSQ4_W32 || kv_dtype == PSK_KV_PSQ8_W32) && q_per_kv > 4u && q_per_kv <= 6u) {
-        // grouped PSQ tiles: code stages + one bf16 chunk, 4 two-head waves
-        const size_t lds = kv_dtype == PSK_KV_PSQ4_W32
-                               ? (D == 256 ? tile_pg_lds_bytes<kFmtPsq4, 256>() : tile_pg_lds_bytes<kFmtPsq4, 128>())
-                               : (D == 256 ? tile_pg_lds_bytes<kFmtPsq8, 256>() : tile_pg_lds_bytes<kFmtPsq8, 128>());
-        const uint32_t by_lds = (uint32_t)((160u * 1024u) / (lds + 64u));
-        return by_lds < 2u ? (by_lds == 0u ? 1u : by_lds) : 2u;
-    }
-    const size_t cb = kv_dtype == PSK_KV_BF16 ? 2 * D : kv_dtype == PSK_KV_PSQ4_W32 ? D / 2 : D;
-    const size_t stage = 2 * 2 * (16 * cb + 128) + (kv_dtype != PSK_KV_BF16 ? 2 * 2 * 256 : 0);
-    const size_t lds = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * stage + 64;
-    const uint32_t by_lds = (uint32_t)((160u * 1024u) / lds);
     const bool psq = kv_dtype == PSK_KV_PSQ4_W32 || kv_dtype == PSK_KV_PSQ8_W32;
-    const uint32_t hpw = q_per_kv <= 4u || psq ? 1u : 2u;
-    const uint32_t nw = q_per_kv <= 4u ? 4u : psq ? (q_per_kv <= 6u ? 6u : 8u) : (q_per_kv + hpw - 1u) / hpw;
+    size_t lds;
+    if (psq) {
+        // code stages + one f16 chunk
+        lds = kv_dtype == PSK_KV_PSQ4_W32
+                  ? (D == 256 ? tile_pg_lds_bytes<kFmtPsq4, 256>() : tile_pg_lds_bytes<kFmtPsq4, 128>())
+                  : (D == 256 ? tile_pg_lds_bytes<kFmtPsq8, 256>() : tile_pg_lds_bytes<kFmtPsq8, 128>());
+    } else {
+        const size_t cb = kv_dtype == PSK_KV_BF16 ? 2 * D : D;
+        const size_t stage = 2 * 2 * (16 * cb + 128) + (kv_dtype != PSK_KV_BF16 ? 2 * 2 * 256 : 0);
+        lds = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * stage;
+    }
+    const uint32_t by_lds = (uint32_t)((160u * 1024u) / (lds + 64u));
+    // waves: groups of 5-6 heads run grouped (4 two-head waves); otherwise up
+    // to 4 heads one per wave (4 waves), 5-6 one per wave (6), 7-8 two per
+    // wave (4; PSQ one per wave, 8)
+    const bool grouped = q_per_kv > 4u && q_per_kv <= 6u;
+    const uint32_t hpw = grouped || (q_per_kv > 6u && !psq) ? 2u : 1u;
+    const uint32_t nw = grouped || q_per_kv <= 4u ? 4u : q_per_kv <= 6u ? 6u : psq ? 8u : 4u;
     const uint32_t by_waves = 4u * (uint32_t)tile_waves_per_simd((int)hpw) / nw;
     const uint32_t n = by_lds < by_waves ? by_lds : by_waves;
     return n == 0u ? 1u : n;
