@@ -947,6 +947,14 @@ def main():
         ap["rows_128_graph_replay"] = dict(tokens_per_s=round(128 / (gms * 1e-3), 1),
                                            ms_per_append=round(gms, 5),
                                            GBps=round(nb / (gms * 1e-3) / 1e9, 1))
+        # the row sweep 2^12 .. 2^17: where the append leaves the launch-bound
+        # regime for the HBM-bound one
+        sweep = {}
+        for lg in range(12, 18):
+            ms, nb = run_append(torch, ops, 1 << lg, args.steps, args.warmup, dev)
+            sweep[f"rows_2^{lg}"] = dict(kernel_ms=round(ms, 5), tokens_per_s=round((1 << lg) / (ms * 1e-3), 1),
+                                         frac_of_peak=round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+        ap["row_sweep"] = sweep
         extra["kv_append_fp8"] = ap
 
     if "psq" in only:
