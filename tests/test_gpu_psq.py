@@ -636,3 +636,18 @@ def test_grouped_prefill_tiles_d128_page24(dev, fmt, D, P):
     plan, got, want = psq_grouped_step(dev, fmt, qh, kvh, D, P, False, 95 + fmt + D + P)
     assert not np.any(got == 7.0)
     assert_attention_close(got, want, TOL, REL, f"test_gpu_psq 14 {(fmt, D, P)}")
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("split", [False, True])
+def test_invalid_page_leaves_grouped_prefill_rows_unwritten(dev, fmt, split):
+    """The grouped and ungrouped PSQ tiles meet an invalid page: the rows of
+    its request stay unwritten; the other rows of the step are exact."""
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8
+    from tests.test_gpu_tile_groups import invalid_page_step
+    got, want = invalid_page_step(
+        dev, KV_PSQ4 if fmt == 4 else KV_PSQ8, split, 41 + fmt + 2 * split,
+        lambda lay: dev_pools(lay, fmt, dev, seed=41 + fmt),
+        lambda lay, q, s, p, bt, pools: oracle_attn(lay, fmt, 24, q, s, p, bt, pools))
+    assert not np.any(got == 7.0)
+    assert_attention_close(got, want, TOL, REL, f"test_gpu_psq 15 {(fmt, split)}")

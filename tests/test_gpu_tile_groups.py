@@ -11,7 +11,7 @@ import torch
 
 import phaseshift_amd as P
 from phaseshift_amd import ops, state
-from tests.kvcase import assert_attention_close, bf16_normal, paged_layout, to_dev
+from tests.kvcase import INVALID, assert_attention_close, bf16_normal, paged_layout, to_dev
 from tests.test_gpu_paged_attention import REL, TOL, make_pools, oracle_out
 
 pytestmark = pytest.mark.gpu
@@ -123,3 +123,49 @@ def test_grouped_and_verify_tiles_page24(dev, fp8):
     got = out.cpu().numpy()
     assert not np.any(got == 7.0)
     assert_attention_close(got, want, TOL[fp8], REL, "test_gpu_tile_groups 2")
+
+
+def invalid_page_step(dev, kvd, split, seed, pools_fn, oracle_fn):
+    """A step whose first prefill request meets an invalid page (every row of
+    it sees the page): its rows stay unwritten, split or not (a split that
+    meets the page marks its partials and the combine skips the row), while
+    the decode row, the verify block and the other prefill request are exact."""
+    rng = np.random.default_rng(seed)
+    spec = [(3000, 160, 2), (40, 1, 0), (2500, 96, 2), (700, 16, 1)]
+    lens = [p + n for p, n, _ in spec]
+    lay = paged_layout(rng, lens, 16, 4, 256, spare_pages=2)
+    pools = pools_fn(lay)
+    bt = lay.block_tables.copy()
+    bt[0, 10] = INVALID
+    slots, pos, reqs, row = [], [], [], 0
+    for s, (p, n, cls) in enumerate(spec):
+        slots += [s] * n
+        pos += list(range(p, p + n))
+        reqs.append((row, n, cls, p + n))
+        row += n
+    slots, pos = np.array(slots, np.uint32), np.array(pos, np.uint32)
+    q = bf16_normal(rng, (row, 24 * 256))
+    g = ops.PoolGeometry(1, lay.num_pages, 16, 4, 256)
+    out = torch.full((row, 24 * 256), 7.0, dtype=torch.float32, device=dev)
+    a = ops.attention_args(g, 0, to_dev(q), out, to_dev(slots), to_dev(pos), to_dev(bt), 24)
+    nbytes = (64 << 20) if split else 0
+    part = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=dev) if split else None
+    plan = state.plan_step(a, kvd, reqs, max(lens), nbytes, part, *pools, launch=True)
+    torch.cuda.synchronize()
+    pre = max((k for k in plan.kernels[:plan.count] if k.kind == 1), key=lambda k: k.rows)
+    assert (pre.splits > 1) == split
+    got = out.cpu().numpy()
+    assert np.all(got[:160] == 7.0)
+    want = oracle_fn(lay, q[160:], slots[160:], pos[160:], bt, pools)
+    return got[160:], want
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("split", [False, True])
+def test_invalid_page_leaves_prefill_rows_unwritten(dev, fp8, split):
+    got, want = invalid_page_step(
+        dev, P.KV_FP8 if fp8 else P.KV_BF16, split, 31 + fp8 + 2 * split,
+        lambda lay: make_pools(lay, fp8, 31 + fp8, dev),
+        lambda lay, q, s, p, bt, pools: oracle_out(lay, 24, q, s, p, bt, *pools))
+    assert not np.any(got == 7.0)
+    assert_attention_close(got, want, TOL[fp8], REL, f"test_gpu_tile_groups 3 {(fp8, split)}")
