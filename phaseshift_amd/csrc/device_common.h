@@ -184,6 +184,9 @@ __device__ __forceinline__ void load_lds(const void* src, uint8_t* dst) {
 
 // Waits until at most N vector-memory operations of this wave are
 // outstanding. The memory clobber keeps every load and LDS access on its side.
+// The pipelines count their own DMAs into N, so a loop that waits this way
+// must issue no other vector-memory operation (register spills to scratch
+// included): the kernels' chunk loops are kept free of spills.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
