@@ -146,6 +146,12 @@ __device__ __forceinline__ float sum_xor32(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The value of lane ^ 8 (within each 16-lane row; DPP row rotate by 8).
+__device__ __forceinline__ uint32_t row_ror8(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float row_ror8(float x) { return __uint_as_float(row_ror8(__float_as_uint(x))); }
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);

@@ -203,7 +203,11 @@ constexpr int stage_bytes() {
 // head slices of each token row) and need no merge. Otherwise the 4 waves
 // share one (row, kv_head, split) item, take its chunks round robin and merge
 // through LDS at the end (used when the independent grid cannot fill the GPU).
-template <int FMT, int D, bool kIndep, int NW>
+// PK (PSQ4, q_per_kv <= 8): the score MFMA's 16 columns carry the group's
+// heads twice, columns n and n + 8 both head n, and take the two 16-token
+// halves of a chunk, so that every lane holds useful scores of one half
+// (see consume_pk).
+template <int FMT, int D, bool kIndep, int NW, bool PK = false>
 __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_kernel(const DecodeParams p) {
     constexpr uint32_t NT = NW * 64;   // threads of the workgroup
     static_assert(kIndep || NW == kWaves, "the shared-item merge uses 4 waves");
@@ -279,10 +283,12 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     // Q fragments: lane (n, g) holds head n, the dims that lane group g covers
     // in each K-step (the dims the K DMA below puts in that lane's 16 bytes).
     bf16x8 qf[NS];
+    static_assert(!PK || FMT == kFmtPsq4, "packed columns: PSQ4");
+    const uint32_t qn = PK ? (n & 7u) : n;   // this lane's head (column)
     {
-        const bool hv = n < qpk;
+        const bool hv = qn < qpk;
         const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + (uint64_t)row * a.q_row_stride +
-                               (uint64_t)(kvh * qpk + (hv ? n : 0u)) * D;
+                               (uint64_t)(kvh * qpk + (hv ? qn : 0u)) * D;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             if constexpr (FMT == kFmtPsq4) {
@@ -685,6 +691,92 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
             }
         };
 
+        // PK: scores, softmax and PV of the chunk at c with one accumulator
+        // per lane. Column n of the score MFMAs is head n & 7 for 16-token
+        // half n >> 3: each K-step runs the two halves' K fragments against
+        // the same Q operand (heads in columns n and n + 8) and keeps, per
+        // lane, the product of its own half, so the per-block K scales, the
+        // softmax and the per-block V scales touch 4 useful values per lane
+        // instead of 8 with 10 of 16 columns idle. The PV operand of head
+        // column n takes its 4 P values of half 0 and lane n + 8's of half 1.
+        auto consume_pk = [&](uint32_t c, const uint8_t* st) __attribute__((always_inline)) {
+            const uint32_t half = n >> 3;
+            const uint8_t* kscl = st + 2 * KV_BYTES + half * 256 + 16 * g;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                f32x4 part[H];
+#pragma unroll
+                for (int hf = 0; hf < H; ++hf) {
+                    // bytes 16s + 4g .. +4 of token n: dims 4g.. (low nibbles)
+                    // and 16 + 4g.. (high nibbles) of block s
+                    const uint32_t x = *reinterpret_cast<const uint32_t*>(st + hf * HALF_STRIDE + 256 * s + 16 * n + 4 * g);
+                    const long ka = (long)((uint64_t)psq4_e4m3x4(x, false) | ((uint64_t)psq4_e4m3x4(x, true) << 32));
+                    part[hf] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(ka, (long)q8h[s], (f32x4){0.f, 0.f, 0.f, 0.f},
+                                                                          0, 0, 0);
+                    part[hf] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(ka, (long)q8l[s], part[hf], 0, 0, 0);
+                }
+                const u32x4 kw = *reinterpret_cast<const u32x4*>(kscl + 64 * (s >> 1));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float ksc = __uint_as_float((s & 1) ? (kw[r] & 0xFFFF0000u) : (kw[r] << 16));
+                    const float pr = half != 0u ? part[1][r] : part[0][r];
+                    acc[r] = s == 0 ? pr * ksc : __builtin_fmaf(pr, ksc, acc[r]);
+                }
+            }
+            // online softmax (log2 units) for head n & 7 over tokens 16 half + 4g + r
+            float s2[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool ok = c + 16u * half + 4u * g + (uint32_t)r < te;
+                s2[r] = ok ? acc[r] * (p.scale_log2 * qinv) : -INFINITY;
+                mx = __builtin_fmaxf(mx, s2[r]);
+            }
+            mx = max_xor32(max_xor16(mx));
+            mx = __builtin_fmaxf(mx, row_ror8(mx));   // the other half
+            const float m_new = __builtin_fmaxf(m_run, mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+            float pv[4], psum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pv[r] = __builtin_amdgcn_exp2f(s2[r] - m_use);
+                psum += pv[r];
+            }
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+            if (__any(alpha != 1.0f)) {
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+            }
+            // O^T += V^T P^T per block b: P times the block's V scale of each
+            // of the lane's tokens, one bf16 operand (own half, then lane
+            // n ^ 8's half; columns 8-15 of O are never written)
+            const uint8_t* vscl = st + 2 * KV_BYTES + SC_BYTES + half * 256 + 16 * g;
+            const uint8_t* vb = st + KV_BYTES + tr_off;
+#pragma unroll
+            for (int b = 0; b < NS; ++b) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(vscl + 64 * (b >> 1));
+                float f[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    f[r] = pv[r] * __uint_as_float((b & 1) ? (w[r] & 0xFFFF0000u) : (w[r] << 16));
+                const uint32_t own0 = pack_bf16x2(f[0], f[1]), own1 = pack_bf16x2(f[2], f[3]);
+                const u32x4 ph = {own0, own1, row_ror8(own0), row_ror8(own1)};
+                const bf16x8 pf = __builtin_bit_cast(bf16x8, ph);
+                // byte i of block b for 8 tokens: dim i (low nibble) and dim
+                // 16 + i (high nibble)
+                const i32x2 vw = lds_read_tr8(vb + 256 * b);
+                const bf16x8 vlo = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)vw[0], false),
+                                                   psq4_e4m3x4((uint32_t)vw[1], false));
+                const bf16x8 vhi = fp8x8_to_bf16x8(psq4_e4m3x4((uint32_t)vw[0], true),
+                                                   psq4_e4m3x4((uint32_t)vw[1], true));
+                o[2 * b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vlo, pf, o[2 * b], 0, 0, 0);
+                o[2 * b + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vhi, pf, o[2 * b + 1], 0, 0, 0);
+            }
+        };
+
         // One pipeline step: the DMAs of the next chunk go out before the
         // wait for chunk c, so the wave keeps two chunks in flight while it
         // computes. The __restrict__ parameters tell the compiler that the
@@ -696,7 +788,10 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                         const uint8_t* __restrict__ cur) __attribute__((always_inline)) {
             issue(c + kStride, next);
             wait_vmcnt<kStepOps>();
-            consume(c, cur);
+            if constexpr (PK)
+                consume_pk(c, cur);
+            else
+                consume(c, cur);
         };
 
         issue(cb, stage0);
@@ -716,7 +811,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     const uint32_t q0 = kvh * qpk;
     if constexpr (kIndep) {
         if (!active) return;
-        const float l_all = sum_xor32(sum_xor16(l_run));
+        const float l_all = sum_xor32(sum_xor16(PK ? l_run + row_ror8(l_run) : l_run));
         if (n >= qpk) return;
         if (p.partials == nullptr) {
             // An invalid page leaves this row's output unwritten.
@@ -752,7 +847,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     } else {
         // ---- merge the 4 waves: per wave m[16], l[16], O[qpk][D] in LDS
         if (bad) bad_shared = 1u;
-        const float l_all = sum_xor32(sum_xor16(l_run));
+        const float l_all = sum_xor32(sum_xor16(PK ? l_run + row_ror8(l_run) : l_run));
         __syncthreads();
         float* fm = reinterpret_cast<float*>(lds);
         float* fl = fm + kWaves * 16;
@@ -925,7 +1020,7 @@ size_t decode_workgroup_lds_bytes(uint32_t kv_dtype, uint32_t head_dim) {
 
 namespace {
 
-template <int FMT, int D, bool kIndep, int NW>
+template <int FMT, int D, bool kIndep, int NW, bool PK = false>
 hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     // block-table window + two pipeline stages per wave; the shared-item merge
@@ -939,10 +1034,10 @@ hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t st
         // gfx950 has 160 KB of LDS per CU; raise the per-kernel dynamic limit.
         static std::atomic<uint64_t> lds_ready{0};
         const hipError_t attr =
-            allow_full_lds(reinterpret_cast<const void*>(&paged_decode_kernel<FMT, D, kIndep, NW>), lds_ready);
+            allow_full_lds(reinterpret_cast<const void*>(&paged_decode_kernel<FMT, D, kIndep, NW, PK>), lds_ready);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((paged_decode_kernel<FMT, D, kIndep, NW>), dim3((uint32_t)grid),
+    hipLaunchKernelGGL((paged_decode_kernel<FMT, D, kIndep, NW, PK>), dim3((uint32_t)grid),
                        dim3(NW * 64), lds_bytes, stream, p);
     return hipGetLastError();
 }
@@ -954,6 +1049,13 @@ template <int FMT, int D>
 hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
     const uint64_t units = (uint64_t)p.a.rows * p.splits;
     const uint64_t groups = (p.a.kv_heads + kWaves - 1u) / kWaves;
+    if constexpr (FMT == kFmtPsq4) {
+        if (p.a.q_heads / p.a.kv_heads <= 8u) {
+            if (units * groups >= 128u)
+                return launch_decode_t2<FMT, D, true, kWaves, true>(p, units * groups, stream);
+            return launch_decode_t2<FMT, D, false, kWaves, true>(p, units * p.a.kv_heads, stream);
+        }
+    }
     if (units * groups >= 128u) return launch_decode_t2<FMT, D, true, kWaves>(p, units * groups, stream);
     return launch_decode_t2<FMT, D, false, kWaves>(p, units * p.a.kv_heads, stream);
 }
