@@ -19,6 +19,7 @@
 // head_dim 256 that is 32 lanes x 16 B per K and V, i.e. fully coalesced
 // 512 B reads and 256 B (FP8) or 512 B (BF16) writes per tensor per task.
 #include "device_common.h"
+#include "fastdiv.h"
 
 #include <phaseshift_kv/kv_append.h>
 
@@ -292,7 +293,14 @@ struct PsqAppendParams {
     uint32_t tasks;         // rows * 2 * head_blocks (< 2^31, checked by the launcher)
     uint32_t vec_in;        // 16 B input loads legal
     uint32_t vec_out;       // 16 B code stores legal
+    FastDiv div_head_blocks;
+    FastDiv div_page_tokens;
 };
+
+__device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv& f) {
+    const uint32_t t = __umulhi(n, f.m);
+    return (t + ((n - t) >> f.s1)) >> f.s2;
+}
 
 // psq_bf16_round (psq4_kv.h:9-18): round to bf16 by adding 0x7FFF plus the
 // kept LSB, then truncating.
@@ -308,21 +316,29 @@ __device__ __forceinline__ float psq_bf16_round(float v) {
 // reference's chain for every float a >= 0, for every positive bf16 scale
 // (subnormals included) over a spread of x, and for 2^26 random (x, bf16
 // scale) pairs, checked on the CPU (tests/native/cb10_branchless.c).
-template <bool kSigned = true>
-__device__ __forceinline__ uint32_t cb10_code(float x, float inv) {
-    // The code boundaries a > 0.5, 1.5, 2.5, 3.5, 5, 7, 9 of a = |x| * inv are
-    // thresholds on k = ceil(2a): code(k) for k = 0..19 in 3-bit fields; NaN and
-    // Inf give k = 19 (7). The doubling follows the product: it is exact
-    // whenever a is finite and overflows only where a > 9 already gives 7,
-    // while a precomputed 2 * inv overflows for bf16-subnormal scales s <=
-    // 2^-127 whose 1/s is finite. (Measured at 2^16 rows: LSQ1 append 109.8
-    // us against 107.0 with 2 * inv, and 111.7 when a per-block branch picks
-    // 2 * inv where it is finite.)
-    constexpr uint64_t kLut = 0x0fb6d6db246d2240ull;
-    const float k = __builtin_fminf(__builtin_ceilf((__builtin_fabsf(x) * inv) * 2.0f), 19.0f);
-    const uint32_t m = (uint32_t)(kLut >> (3u * (uint32_t)k)) & 7u;
-    if constexpr (!kSigned) return m;
-    return m | (x < 0.0f ? 8u : 0u);   // -0.0 and NaN: no sign, as the reference
+//
+// The code boundaries a > 0.5, 1.5, 2.5, 3.5, 5, 7, 9 are thresholds on
+// k = ceil(2a): the code is the number of T in {2, 4, 6, 8, 11, 15, 19} with
+// k >= T. With n = floor(max(-2a, -19)) = -min(k, 19) (NaN and Inf give -19,
+// a max operand that is NaN yields the other), the 64-bit shift of the pair
+// {lo = 0, hi = H} by n mod 64 = 64 - k (0 for k = 0) keeps in its low dword
+// exactly the bits 32 - T of H with k >= T, and the code is their popcount:
+// multiply, max, floor-convert, shift, bit count (the count's accumulator
+// adds the sign). -2a is |x| * (-2 * inv) where -2 * inv is finite, which
+// equals (|x| * inv) * -2 up to a subnormal a (code 0 either way); bf16
+// subnormal scales s <= 2^-127 have a finite 1/s but an infinite 2/s, and a
+// wave with such a block doubles after the product instead (exact whenever a
+// is finite, overflowing only where a > 9 already gives 7).
+constexpr uint32_t kCb10H = (1u << 30) | (1u << 28) | (1u << 26) | (1u << 24) | (1u << 21) |
+                           (1u << 17) | (1u << 13);
+
+__device__ __forceinline__ uint32_t cb10_bits(float y) {
+    // floor and convert in one instruction (the compiler emits two for
+    // (int)floorf); y is in [-19, 0], where a flushed denormal input gives
+    // n = 0 instead of -1, both code 0
+    int n;
+    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(n) : "v"(y));
+    return (uint32_t)(((uint64_t)kCb10H << 32) >> ((uint32_t)n & 63u));
 }
 
 // Codes of the 32 values for scale s (all 0 unless s > 0): PSQ4 cb10 codes of
@@ -331,20 +347,71 @@ __device__ __forceinline__ uint32_t cb10_code(float x, float inv) {
 // sign, and no zeroing for s == 0 (the LSQ1 fit's first pass, whose decoded
 // values only enter |x| * |q| and q * q; with s == 0 every x is zero or NaN
 // and the fit ends at scale 0 either way).
-template <bool kPsq4, bool kMagnitude = false>
-__device__ __forceinline__ void psq_codes(const float (&x)[32], float s, uint32_t (&c)[32]) {
+//
+// kNoNaN (PSQ4, the two passes of the LSQ1 fit): a NaN value's code does not
+// matter (the fit's first pass: its |x| q is NaN whatever q is, and the fit
+// ends at scale 0), or s > 0 implies the block has no NaN (the refit: a NaN
+// made the fitted scale 0). Then a wave whose blocks all have s == 0 or
+// -2 amax / s >= -32 drops the clamp: every n = floor(-2a) is then in [-32, 0]
+// (a shift of 64 - k >= 32 keeps the low dword right up to k = 32); with
+// s == 0, -2a is -inf or NaN, whose conversion (INT_MIN or 0) shifts by 0 and
+// gives code 0.
+//
+// 1/s: for a bf16 s in [2^-126, 2^126] (every lane of the wave), the hardware
+// reciprocal r (within one ulp of 1/s) refined by e = fma(-s, r, 1),
+// fma(e, r, r) is the correctly rounded 1/s, checked on the CPU for every such
+// bf16 s and each of the three floats within one ulp of 1/s
+// (tests/native/rcp_refine.c); other scales divide.
+__device__ __forceinline__ float bf16_scale_reciprocal(float s) {
+    if (__all(s >= 0x1p-126f && s <= 0x1p126f)) {
+        const float r = __builtin_amdgcn_rcpf(s);
+        return __builtin_fmaf(__builtin_fmaf(-s, r, 1.0f), r, r);
+    }
+    return 1.0f / s;
+}
+
+template <bool kPsq4, bool kMagnitude = false, bool kNoNaN = false>
+__device__ __forceinline__ void psq_codes(const float (&x)[32], float s, float amax, uint32_t (&c)[32]) {
 #pragma clang fp contract(off)
-    const float inv = 1.0f / s;
-    const uint32_t keep = s > 0.0f ? 0xFFFFFFFFu : 0u;   // all codes 0 unless s > 0
+    const float inv = bf16_scale_reciprocal(s);
     if constexpr (kPsq4) {
-        if constexpr (kMagnitude) {
+        const float inv2 = inv * -2.0f;   // -inf for s == 0
+        if constexpr (kNoNaN) {
+            const bool sp = s > 0.0f;
+            const uint32_t sg = !kMagnitude && sp ? 8u : 0u;   // the sign code bit, if any
+            if (__all(!sp || amax * inv2 >= -32.0f)) {
 #pragma unroll
-            for (int i = 0; i < 32; ++i) c[i] = cb10_code<false>(x[i], inv);
+                for (int i = 0; i < 32; ++i) {
+                    int n;
+                    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(n) : "v"(__builtin_fabsf(x[i]) * inv2));
+                    c[i] = (uint32_t)__builtin_popcount(
+                               (uint32_t)((uint64_t{kCb10H} << 32) >> ((uint32_t)n & 63u))) +
+                           (x[i] < 0.0f ? sg : 0u);
+                }
+                return;
+            }
+        }
+        // s == 0: every magnitude 0 through the clamp (lo = +0) and no signs,
+        // unless kMagnitude
+        const bool kp = kMagnitude || s > 0.0f;
+        const float lo = kp ? -19.0f : 0.0f;
+        const bool pre = !kp || __builtin_isfinite(inv2);   // -inf harmless under lo = +0
+        const uint32_t sg = !kMagnitude && kp ? 8u : 0u;
+        if (__all(pre)) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                c[i] = (uint32_t)__builtin_popcount(
+                           cb10_bits(__builtin_fmaxf(__builtin_fabsf(x[i]) * inv2, lo))) +
+                       (x[i] < 0.0f ? sg : 0u);
         } else {
 #pragma unroll
-            for (int i = 0; i < 32; ++i) c[i] = cb10_code(x[i], inv) & keep;
+            for (int i = 0; i < 32; ++i)
+                c[i] = (uint32_t)__builtin_popcount(
+                           cb10_bits(__builtin_fmaxf((__builtin_fabsf(x[i]) * inv) * -2.0f, lo))) +
+                       (x[i] < 0.0f ? sg : 0u);
         }
     } else {
+        const uint32_t keep = s > 0.0f ? 0xFFFFFFFFu : 0u;   // all codes 0 unless s > 0
 #pragma unroll
         for (int i = 0; i < 32; i += 4) {
             const uint32_t w = e4m3_encode_pair(x[i + 2] * inv, x[i + 3] * inv,
@@ -355,13 +422,23 @@ __device__ __forceinline__ void psq_codes(const float (&x)[32], float s, uint32_
     }
 }
 
-// Sum of v[0..31] in the order of the reference's 32-lane xor butterfly
-// (x += shfl_xor(x, o) for o = 16, 8, 4, 2, 1; kv_append.hip:293-299): the
-// tree (v[j] + v[j^16]), then ^8, ^4, ^2, ^1 on the partial sums.
-__device__ __forceinline__ float butterfly_sum32(float (&v)[32]) {
+// Sum of the products a[j] * b[j], j = 0..31, in the order of the reference's
+// 32-lane xor butterfly (x += shfl_xor(x, o) for o = 16, 8, 4, 2, 1;
+// kv_append.hip:293-299): the tree (p[j] + p[j^16]), then ^8, ^4, ^2, ^1 on
+// the partial sums. kFma: every product is exact in fp32 and none is negative,
+// so the first level p[j] + p[j + 16] is one FMA onto the second product (the
+// exact sum rounded once equals the add of the two rounded products, and an
+// overflowing product gives inf both ways; with mixed signs an overflow could
+// give inf where the adds give NaN).
+template <bool kFma>
+__device__ __forceinline__ float butterfly_dot32(const float (&a)[32], const float (&b)[32]) {
 #pragma clang fp contract(off)
+    float v[16];
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1)
+    for (int j = 0; j < 16; ++j)
+        v[j] = kFma ? __builtin_fmaf(a[j], b[j], a[j + 16] * b[j + 16]) : a[j] * b[j] + a[j + 16] * b[j + 16];
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1)
 #pragma unroll
         for (int j = 0; j < o; ++j) v[j] = v[j] + v[j + o];
     return v[0];
@@ -373,7 +450,7 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
     const psk_kv_append_args& a = p.a;
     const uint32_t task = blockIdx.x * 256u + threadIdx.x;
     if (task >= p.tasks) return;
-    const uint32_t rest = task / p.head_blocks;
+    const uint32_t rest = fastdiv(task, p.div_head_blocks);
     const uint32_t hb = task - rest * p.head_blocks;
     const bool is_v = (rest & 1u) != 0u;
     const uint32_t row = rest >> 1;
@@ -400,7 +477,7 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
         for (int i = 0; i < 32; ++i) x[i] = bf16_bits_to_f32(src[i]);
     }
     if (slot >= a.max_sequences) return;
-    const uint32_t lb = pos / a.page_tokens;
+    const uint32_t lb = fastdiv(pos, p.div_page_tokens);
     if (lb >= a.block_table_stride) return;
     const uint32_t page = a.block_tables[(uint64_t)slot * a.block_table_stride + lb];
     if (page >= a.num_pages) return;
@@ -416,35 +493,51 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
     // signed q equals |x| * |q| bit for bit (the sign of a zero product aside,
     // which cannot change a sum that has a nonzero term or the scale 0 of
     // one that has none)
-    psq_codes<kPsq4, kPsq4 && kLsq1>(x, s, c);
+    psq_codes<kPsq4, kPsq4 && kLsq1, kLsq1>(x, s, amax, c);
 
     if constexpr (kLsq1) {
         // num = sum x q, den = sum q q over the decoded codes, in the
         // reference's butterfly order; s1 = bf16(num / den), then re-encode
-        float nm[32], dn[32];
+        // The products x q and q q are exact in fp32: x is bf16 (8 significant
+        // bits, granularity 2^-133), q an E4M3 value (4 bits, granularity
+        // 2^-9), so a product has at most 12 significant bits on a grid of
+        // 2^-142, above fp32's 2^-149 (overflow gives inf either way).
+        float xa[32], qf[32];
+        uint32_t qq = 0u;   // PSQ4: sum q q as an integer
 #pragma unroll
         for (int i = 0; i < 32; i += 4) {
             // PSQ4: 4 codes -> their E4M3 bytes (cb10 magnitudes 0 1 2 3 4
             // 6 8 10 are exact in E4M3, code 8 is -0) -> f32 by the hardware
             // conversion, as PSQ8's codes
-            const uint32_t w = kPsq4 ? psq4_e4m3x4(c[i] | (c[i + 1] << 8) | (c[i + 2] << 16) | (c[i + 3] << 24),
-                                                   false)
-                                     : c[i >> 2];
+            // codes i..i+3 (each below 256) as the bytes of one dword, by three permutes
+            const uint32_t cb = __builtin_amdgcn_perm(__builtin_amdgcn_perm(c[i + 3], c[i + 2], 0x0C0C0400u),
+                                                      __builtin_amdgcn_perm(c[i + 1], c[i], 0x0C0C0400u),
+                                                      0x05040100u);
+            // (magnitude indices 0..7 select the bytes of the E4M3 table directly)
+            const uint32_t w = kPsq4 ? __builtin_amdgcn_perm(0x52504C48u, 0x44403800u, cb) : c[i >> 2];
             const f32x2 q01 = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
             const f32x2 q23 = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-            const float q[4] = {q01[0], q01[1], q23[0], q23[1]};
+            qf[i] = q01[0];
+            qf[i + 1] = q01[1];
+            qf[i + 2] = q23[0];
+            qf[i + 3] = q23[1];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                nm[i + j] = (kPsq4 ? __builtin_fabsf(x[i + j]) : x[i + j]) * q[j];
-                dn[i + j] = q[j] * q[j];
+            for (int j = 0; j < 4; ++j) xa[i + j] = kPsq4 ? __builtin_fabsf(x[i + j]) : x[i + j];
+            if constexpr (kPsq4) {
+                // magnitude indices -> the cb10 values as bytes, then a
+                // 4-byte dot product
+                const uint32_t qb = __builtin_amdgcn_perm(0x0A080604u, 0x03020100u, cb);
+                qq = __builtin_amdgcn_udot4(qb, qb, qq, false);
             }
         }
-        const float num = butterfly_sum32(nm);
-        const float den = butterfly_sum32(dn);
+        const float num = butterfly_dot32<kPsq4>(xa, qf);   // PSQ8: x q has signs
+        // PSQ4: every q q and partial sum is an integer below 2^24, so the
+        // butterfly's float sum is the exact integer sum in any order
+        const float den = kPsq4 ? (float)qq : butterfly_dot32<true>(qf, qf);
         const float sl = den > 0.0f ? num / den : 0.0f;
         float s1 = psq_bf16_round(sl);
         if (!(s1 > 0.0f)) s1 = 0.0f;
-        psq_codes<kPsq4>(x, s1, c);
+        psq_codes<kPsq4, false, true>(x, s1, amax, c);
         s = s1;
     }
 
@@ -452,15 +545,16 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
                          a.kv_heads) * p.bph + hb;
     uint8_t* code = is_v ? p.v_code : p.k_code;
     if constexpr (kPsq4) {
-        // byte j = code j | code j+16 << 4 (psq4_pack_codes, psq4_kv.h:73-77)
+        // byte j = code j | code j+16 << 4 (psq4_pack_codes, psq4_kv.h:73-77);
+        // every code is below 16 (a count of 7 bits plus the sign 8)
         u32x4 w;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-            uint32_t v = 0u;
+            uint32_t v = c[4 * d] | (c[4 * d + 16] << 4);
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
+            for (int b = 1; b < 4; ++b) {
                 const int j = 4 * d + b;
-                v |= ((c[j] & 0xFu) | ((c[j + 16] & 0xFu) << 4)) << (8 * b);
+                v |= (c[j] | (c[j + 16] << 4)) << (8 * b);
             }
             w[d] = v;
         }
@@ -567,6 +661,8 @@ hipError_t launch_psq(const psk_kv_append_args& c, bool psq4, uint8_t* kc, uint8
     p.v_scale = vs;
     p.bph = bph;
     p.head_blocks = c.kv_heads * bph;
+    p.div_head_blocks = make_fastdiv(p.head_blocks);
+    p.div_page_tokens = make_fastdiv(c.page_tokens);
     const uint64_t tasks = (uint64_t)c.rows * 2u * p.head_blocks;
     if (tasks >= (1ull << 31)) return hipErrorInvalidValue;
     p.tasks = (uint32_t)tasks;

@@ -10,6 +10,7 @@
  *      (where 2 / s overflows while 1 / s is finite), against 2048 x values
  *      each: 0, the code boundaries times s and their float neighbours, and
  *      random x of magnitude 2^-39 .. 2^13 times s.
+ * Both the lookup form and the kernel's popcount form (below) are checked.
  * Uses the same IEEE operations as the device code: fminf (NaN -> other
  * operand), ceilf, one rounding per multiply. */
 #include <math.h>
@@ -24,6 +25,37 @@ static uint32_t lut_code(float x, float inv) {
     const float k = fminf(ceilf((fabsf(x) * inv) * 2.0f), 19.0f);
     const uint32_t m = (uint32_t)(lut >> (3u * (uint32_t)k)) & 7u;
     return m | (x < 0.0f ? 8u : 0u);
+}
+
+/* The kernel's form: n = floor(max(-2a, -19)) = -min(k, 19), the 64-bit
+ * shift of {lo = 0, hi = H} by n mod 64, the popcount of the low dword; H has
+ * the bits 32 - T for the thresholds T = 2 4 6 8 11 15 19 of k. Where 2 * inv
+ * is finite the kernel may also use |x| * (-2 * inv) (pre2 = 1). */
+static uint32_t pop_code(float x, float inv, int pre2) {
+    const uint32_t h = (1u << 30) | (1u << 28) | (1u << 26) | (1u << 24) | (1u << 21) | (1u << 17) |
+                       (1u << 13);
+    const float y = fmaxf(pre2 ? fabsf(x) * (inv * -2.0f) : (fabsf(x) * inv) * -2.0f, -19.0f);
+    const int n = (int)floorf(y);
+    const uint64_t t = ((uint64_t)h << 32) >> ((uint32_t)n & 63u);
+    return (uint32_t)__builtin_popcount((uint32_t)t) + (x < 0.0f ? 8u : 0u);
+}
+
+/* Without the clamp (the kernel's LSQ1 passes, used when -2a >= -32 for the
+ * block's largest |x| and so for every x of the block). */
+static uint32_t pop_code_unclamped(float x, float inv) {
+    const uint32_t h = (1u << 30) | (1u << 28) | (1u << 26) | (1u << 24) | (1u << 21) | (1u << 17) |
+                       (1u << 13);
+    const int n = (int)floorf(fabsf(x) * (inv * -2.0f));
+    const uint64_t t = ((uint64_t)h << 32) >> ((uint32_t)n & 63u);
+    return (uint32_t)__builtin_popcount((uint32_t)t) + (x < 0.0f ? 8u : 0u);
+}
+
+static uint32_t check(float x, float inv, uint32_t want) {
+    uint32_t bad = lut_code(x, inv) != want;
+    bad |= (pop_code(x, inv, 0) != want) << 1;
+    if (isfinite(inv * 2.0f)) bad |= (pop_code(x, inv, 1) != want) << 2;
+    if (fabsf(x) * (inv * -2.0f) >= -32.0f) bad |= (pop_code_unclamped(x, inv) != want) << 3;
+    return bad;
 }
 
 static uint64_t rng_state = 0x9E3779B97F4A7C15ull;
@@ -42,8 +74,9 @@ int main(void) {
         float a;
         memcpy(&a, &u, 4);
         const uint32_t want = or_cb10_encode(a, 1.0f);
-        if (lut_code(a, 1.0f) != want) {
-            if (bad < 8) printf("mismatch a=%a (0x%08x): %u vs %u\n", a, u, lut_code(a, 1.0f), want);
+        const uint32_t m = check(a, 1.0f, want);
+        if (m) {
+            if (bad < 8) printf("mismatch a=%a (0x%08x): form mask %u, want %u\n", a, u, m, want);
             ++bad;
         }
     }
@@ -59,8 +92,9 @@ int main(void) {
         memcpy(&s, &sb, 4);
         const float inv = 1.0f / s;
         const uint32_t want = or_cb10_encode(x, inv);
-        if (lut_code(x, inv) != want) {
-            if (bad < 16) printf("mismatch x=%a s=%a: %u vs %u\n", x, s, lut_code(x, inv), want);
+        const uint32_t m = check(x, inv, want);
+        if (m) {
+            if (bad < 16) printf("mismatch x=%a s=%a: form mask %u, want %u\n", x, s, m, want);
             ++bad;
         }
     }
@@ -92,9 +126,9 @@ int main(void) {
                 if (st & 1u) x = -x;
             }
             const uint32_t want = or_cb10_encode(x, inv);
-            const uint32_t got = lut_code(x, inv);
-            if (got != want) {
-                if (bad < 24) printf("mismatch x=%a s=%a: %u vs %u\n", x, s, got, want);
+            const uint32_t m = check(x, inv, want);
+            if (m) {
+                if (bad < 24) printf("mismatch x=%a s=%a: form mask %u, want %u\n", x, s, m, want);
                 ++bad;
             }
         }

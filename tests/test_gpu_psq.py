@@ -81,6 +81,10 @@ def append_case(dev, fmt, lsq1, rows, kv_heads, D, seed, stride_pad=0):
         # non-finite case outside the bit-exact contract.)
         k_in[3, 96:128] = oracle.f32_to_bf16(
             (rng.uniform(0.3, 1.0, 32) * 4.5e-38 * np.where(rng.random(32) < 0.5, -1, 1)).astype(np.float32))
+        # NaNs of both signs inside a finite block (no sign bit in their codes,
+        # amax drops them) and a -0.0 (code 0, not 8)
+        v_in[4, 0:32] = oracle.f32_to_bf16(np.linspace(-2.0, 2.0, 32).astype(np.float32))
+        v_in[4, 5], v_in[4, 9], v_in[4, 17] = 0x7FC0, 0xFFC0, 0x8000
     return lay, slots, pos, k_in, v_in
 
 
