@@ -148,7 +148,9 @@ __device__ __forceinline__ float sum_xor32(float x) {
 
 // The value of lane ^ 8 (within each 16-lane row; DPP row rotate by 8).
 __device__ __forceinline__ uint32_t row_ror8(uint32_t x) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
+    // every lane of every row is written, so the instruction needs no prior
+    // value of its destination (mov_dpp leaves it undefined)
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, true);
 }
 __device__ __forceinline__ float row_ror8(float x) { return __uint_as_float(row_ror8(__float_as_uint(x))); }
 

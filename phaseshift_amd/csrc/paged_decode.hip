@@ -251,7 +251,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     const psk_paged_attention_args& a = p.a;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
-    const uint32_t wave = tid >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: scalar addressing
     const uint32_t n = lane & 15u;   // token (loads, S rows) or head (S cols, P, O)
     const uint32_t g = lane >> 4;    // lane group
 
@@ -346,6 +346,21 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
             q8l[s] = (uint64_t)lw[0] | ((uint64_t)lw[1] << 32);
         }
         qinv = __builtin_ldexpf(1.0f, -sh);
+    }
+    // PK: the Q operands with the columns of the other half zeroed (lanes
+    // n < 8 carry half 0's heads, lanes n >= 8 half 1's), so the two halves'
+    // score MFMAs accumulate into one result whose column n is the product of
+    // lane n's own half
+    uint64_t q8m[PK ? 2 : 1][PK ? 2 * NS : 1];
+    if constexpr (PK) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const bool mine = (n >> 3) == (uint32_t)hf;
+                q8m[hf][2 * s] = mine ? q8h[s] : 0u;
+                q8m[hf][2 * s + 1] = mine ? q8l[s] : 0u;
+            }
     }
 
     const uint64_t layer_base = (uint64_t)a.layer * a.elems_per_layer;
@@ -705,23 +720,21 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                f32x4 part[H];
+                f32x4 part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int hf = 0; hf < H; ++hf) {
                     // bytes 16s + 4g .. +4 of token n: dims 4g.. (low nibbles)
                     // and 16 + 4g.. (high nibbles) of block s
                     const uint32_t x = *reinterpret_cast<const uint32_t*>(st + hf * HALF_STRIDE + 256 * s + 16 * n + 4 * g);
                     const long ka = (long)((uint64_t)psq4_e4m3x4(x, false) | ((uint64_t)psq4_e4m3x4(x, true) << 32));
-                    part[hf] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(ka, (long)q8h[s], (f32x4){0.f, 0.f, 0.f, 0.f},
-                                                                          0, 0, 0);
-                    part[hf] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(ka, (long)q8l[s], part[hf], 0, 0, 0);
+                    part = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(ka, (long)q8m[hf][2 * s], part, 0, 0, 0);
+                    part = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(ka, (long)q8m[hf][2 * s + 1], part, 0, 0, 0);
                 }
                 const u32x4 kw = *reinterpret_cast<const u32x4*>(kscl + 64 * (s >> 1));
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float ksc = __uint_as_float((s & 1) ? (kw[r] & 0xFFFF0000u) : (kw[r] << 16));
-                    const float pr = half != 0u ? part[1][r] : part[0][r];
-                    acc[r] = s == 0 ? pr * ksc : __builtin_fmaf(pr, ksc, acc[r]);
+                    acc[r] = s == 0 ? part[r] * ksc : __builtin_fmaf(part[r], ksc, acc[r]);
                 }
             }
             // online softmax (log2 units) for head n & 7 over tokens 16 half + 4g + r
