@@ -85,6 +85,10 @@ def append_case(dev, fmt, lsq1, rows, kv_heads, D, seed, stride_pad=0):
         # amax drops them) and a -0.0 (code 0, not 8)
         v_in[4, 0:32] = oracle.f32_to_bf16(np.linspace(-2.0, 2.0, 32).astype(np.float32))
         v_in[4, 5], v_in[4, 9], v_in[4, 17] = 0x7FC0, 0xFFC0, 0x8000
+        # +-inf in a block: scale inf, 1/s = 0, finite values code 0, the
+        # infinities code 7 (NaN product) with their sign; LSQ1 keeps scale inf
+        v_in[5, 32:64] = oracle.f32_to_bf16(np.linspace(-1.0, 1.0, 32).astype(np.float32))
+        v_in[5, 40], v_in[5, 50] = 0x7F80, 0xFF80
     return lay, slots, pos, k_in, v_in
 
 
