@@ -58,10 +58,10 @@ def dev_pools(lay, fmt, dev, fill=True, seed=0):
 
 
 # ------------------------------------------------------------------ append
-def append_case(dev, fmt, lsq1, rows, kv_heads, D, seed, stride_pad=0):
+def append_case(dev, fmt, lsq1, rows, kv_heads, D, seed, stride_pad=0, page_tokens=16):
     rng = np.random.default_rng(seed)
     lens = [rows // 2 + 3, rows - rows // 2 - 3]
-    lay = paged_layout(rng, lens, 16, kv_heads, D, spare_pages=2)
+    lay = paged_layout(rng, lens, page_tokens, kv_heads, D, spare_pages=2)
     slots = np.repeat(np.arange(2, dtype=np.uint32), lens)
     pos = np.concatenate([np.arange(n, dtype=np.uint32) for n in lens])
     W = kv_heads * D + stride_pad
@@ -125,6 +125,20 @@ def test_append_bit_exact(dev, fmt, lsq1, kv_heads, D, rows, pad):
     want = oracle_append(lay, fmt, lsq1, k_in, v_in, slots, pos, lay.block_tables)
     for name, a, b in zip(("k codes", "v codes", "k scales", "v scales"), got, want):
         assert np.array_equal(a, b), name
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("page_tokens", [1, 7, 24, 64])
+def test_append_bit_exact_page_sizes(dev, fmt, page_tokens):
+    """Page sizes other than 16 (the kernel divides positions by a launch-time
+    constant), 5 kv heads (head_blocks 40), both estimators."""
+    for lsq1 in (False, True):
+        lay, slots, pos, k_in, v_in = append_case(dev, fmt, lsq1, 77, 5, 256, 700 + page_tokens + fmt,
+                                                  page_tokens=page_tokens)
+        got = run_append(dev, lay, fmt, lsq1, k_in, v_in, slots, pos, lay.block_tables)
+        want = oracle_append(lay, fmt, lsq1, k_in, v_in, slots, pos, lay.block_tables)
+        for name, a, b in zip(("k codes", "v codes", "k scales", "v scales"), got, want):
+            assert np.array_equal(a, b), (name, lsq1)
 
 
 @pytest.mark.parametrize("fmt", [4, 8])
