@@ -343,14 +343,8 @@ __device__ __forceinline__ uint32_t cb10_bits(float y) {
 
 // Codes of the 32 values for scale s (all 0 unless s > 0): PSQ4 cb10 codes of
 // x * (1/s), PSQ8 SATFINITE E4M3 codes of x * (1/s) packed 4 per dword.
-// kMagnitude (PSQ4 only): the cb10 magnitude index of each value without its
-// sign, and no zeroing for s == 0 (the LSQ1 fit's first pass, whose decoded
-// values only enter |x| * |q| and q * q; with s == 0 every x is zero or NaN
-// and the fit ends at scale 0 either way).
 //
-// kNoNaN (PSQ4, the two passes of the LSQ1 fit): a NaN value's code does not
-// matter (the fit's first pass: its |x| q is NaN whatever q is, and the fit
-// ends at scale 0), or s > 0 implies the block has no NaN (the refit: a NaN
+// kNoNaN (PSQ4, the LSQ1 refit): s > 0 implies the block has no NaN (a NaN
 // made the fitted scale 0). Then a wave whose blocks all have s == 0 or
 // -2 amax / s >= -32 drops the clamp: every n = floor(-2a) is then in [-32, 0]
 // (a shift of 64 - k >= 32 keeps the low dword right up to k = 32); with
@@ -370,7 +364,42 @@ __device__ __forceinline__ float bf16_scale_reciprocal(float s) {
     return 1.0f / s;
 }
 
-template <bool kPsq4, bool kMagnitude = false, bool kNoNaN = false>
+// PSQ4 LSQ1 fit, first pass: the decoded magnitude q (fp32) of each value's
+// cb10 code at scale s, looked up by n = floor(-2a) in a 33-entry LDS table
+// (q_lut[32 + n] = the cb10 value of code(k = -n)). Only |x| q and q q use
+// them: x q with the signed q equals |x| |q| bit for bit (a product's zero
+// sign aside, which cannot change a sum with a nonzero term, nor the scale 0
+// of one without), so no signs and no zeroing for s == 0 (the fit then ends
+// at scale 0 either way: every x is zero or NaN), and a NaN value's q does
+// not matter (its |x| q is NaN whatever q is, and so is the fitted scale,
+// which becomes 0). n stays in [-32, 0] on every path: without the clamp
+// where the wave's blocks all have -2 amax / s >= -32 (or s == 0, taken as
+// -2/s = 0, n = 0), else clamped at -19.
+__device__ __forceinline__ void psq4_first_pass_q(const float (&x)[32], float s, float amax,
+                                                  const float* q_lut, float (&q)[32]) {
+#pragma clang fp contract(off)
+    const float inv = bf16_scale_reciprocal(s);
+    const bool sp = s > 0.0f;
+    const float m2 = inv * -2.0f;
+    const float inv2 = sp ? m2 : 0.0f;
+    auto look = [&](float y) __attribute__((always_inline)) {
+        int n;
+        asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(n) : "v"(y));
+        return q_lut[32 + n];
+    };
+    if (__all(!sp || amax * inv2 >= -32.0f)) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = look(__builtin_fabsf(x[i]) * inv2);
+    } else if (__all(!sp || __builtin_isfinite(m2))) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = look(__builtin_fmaxf(__builtin_fabsf(x[i]) * inv2, -19.0f));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = look(__builtin_fmaxf((__builtin_fabsf(x[i]) * inv) * -2.0f, -19.0f));
+    }
+}
+
+template <bool kPsq4, bool kNoNaN = false>
 __device__ __forceinline__ void psq_codes(const float (&x)[32], float s, float amax, uint32_t (&c)[32]) {
 #pragma clang fp contract(off)
     const float inv = bf16_scale_reciprocal(s);
@@ -378,7 +407,7 @@ __device__ __forceinline__ void psq_codes(const float (&x)[32], float s, float a
         const float inv2 = inv * -2.0f;   // -inf for s == 0
         if constexpr (kNoNaN) {
             const bool sp = s > 0.0f;
-            const uint32_t sg = !kMagnitude && sp ? 8u : 0u;   // the sign code bit, if any
+            const uint32_t sg = sp ? 8u : 0u;   // the sign code bit, if any
             if (__all(!sp || amax * inv2 >= -32.0f)) {
 #pragma unroll
                 for (int i = 0; i < 32; ++i) {
@@ -391,12 +420,11 @@ __device__ __forceinline__ void psq_codes(const float (&x)[32], float s, float a
                 return;
             }
         }
-        // s == 0: every magnitude 0 through the clamp (lo = +0) and no signs,
-        // unless kMagnitude
-        const bool kp = kMagnitude || s > 0.0f;
+        // s == 0: every magnitude 0 through the clamp (lo = +0) and no signs
+        const bool kp = s > 0.0f;
         const float lo = kp ? -19.0f : 0.0f;
         const bool pre = !kp || __builtin_isfinite(inv2);   // -inf harmless under lo = +0
-        const uint32_t sg = !kMagnitude && kp ? 8u : 0u;
+        const uint32_t sg = kp ? 8u : 0u;
         if (__all(pre)) {
 #pragma unroll
             for (int i = 0; i < 32; ++i)
@@ -448,6 +476,16 @@ template <bool kPsq4, bool kLsq1>
 __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParams p) {
 #pragma clang fp contract(off)
     const psk_kv_append_args& a = p.a;
+    // PSQ4 LSQ1: q_lut[j] = the cb10 value of k = 32 - j (k = ceil(2a))
+    __shared__ float q_lut[kPsq4 && kLsq1 ? 33 : 1];
+    if constexpr (kPsq4 && kLsq1) {
+        if (threadIdx.x < 33u) {
+            const uint32_t k = 32u - threadIdx.x;
+            const uint32_t code = k == 0u ? 0u : (uint32_t)__builtin_popcount(kCb10H >> (32u - k));
+            q_lut[threadIdx.x] = (float)(code < 5u ? code : 2u * code - 4u);
+        }
+        __syncthreads();
+    }
     const uint32_t task = blockIdx.x * 256u + threadIdx.x;
     if (task >= p.tasks) return;
     const uint32_t rest = fastdiv(task, p.div_head_blocks);
@@ -489,11 +527,11 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
     for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[i]));
     float s = amax > 0.0f ? psq_bf16_round(amax * (kPsq4 ? 0.1f : (1.0f / 448.0f))) : 0.0f;
     uint32_t c[32];
-    // LSQ1 (PSQ4): the first pass needs only the magnitudes; x * q with the
-    // signed q equals |x| * |q| bit for bit (the sign of a zero product aside,
-    // which cannot change a sum that has a nonzero term or the scale 0 of
-    // one that has none)
-    psq_codes<kPsq4, kPsq4 && kLsq1, kLsq1>(x, s, amax, c);
+    [[maybe_unused]] float qf[32];   // PSQ4 LSQ1: the first pass's decoded magnitudes
+    if constexpr (kPsq4 && kLsq1)
+        psq4_first_pass_q(x, s, amax, q_lut, qf);
+    else
+        psq_codes<kPsq4>(x, s, amax, c);
 
     if constexpr (kLsq1) {
         // num = sum x q, den = sum q q over the decoded codes, in the
@@ -502,42 +540,36 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
         // bits, granularity 2^-133), q an E4M3 value (4 bits, granularity
         // 2^-9), so a product has at most 12 significant bits on a grid of
         // 2^-142, above fp32's 2^-149 (overflow gives inf either way).
-        float xa[32], qf[32];
-        uint32_t qq = 0u;   // PSQ4: sum q q as an integer
+        float xa[32];
+        if constexpr (!kPsq4) {
 #pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            // PSQ4: 4 codes -> their E4M3 bytes (cb10 magnitudes 0 1 2 3 4
-            // 6 8 10 are exact in E4M3, code 8 is -0) -> f32 by the hardware
-            // conversion, as PSQ8's codes
-            // codes i..i+3 (each below 256) as the bytes of one dword, by three permutes
-            const uint32_t cb = __builtin_amdgcn_perm(__builtin_amdgcn_perm(c[i + 3], c[i + 2], 0x0C0C0400u),
-                                                      __builtin_amdgcn_perm(c[i + 1], c[i], 0x0C0C0400u),
-                                                      0x05040100u);
-            // (magnitude indices 0..7 select the bytes of the E4M3 table directly)
-            const uint32_t w = kPsq4 ? __builtin_amdgcn_perm(0x52504C48u, 0x44403800u, cb) : c[i >> 2];
-            const f32x2 q01 = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
-            const f32x2 q23 = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-            qf[i] = q01[0];
-            qf[i + 1] = q01[1];
-            qf[i + 2] = q23[0];
-            qf[i + 3] = q23[1];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xa[i + j] = kPsq4 ? __builtin_fabsf(x[i + j]) : x[i + j];
-            if constexpr (kPsq4) {
-                // magnitude indices -> the cb10 values as bytes, then a
-                // 4-byte dot product
-                const uint32_t qb = __builtin_amdgcn_perm(0x0A080604u, 0x03020100u, cb);
-                qq = __builtin_amdgcn_udot4(qb, qb, qq, false);
+            for (int i = 0; i < 32; i += 4) {
+                // PSQ8: 4 E4M3 codes -> f32 by the hardware conversion
+                const f32x2 q01 = __builtin_amdgcn_cvt_pk_f32_fp8(c[i >> 2], false);
+                const f32x2 q23 = __builtin_amdgcn_cvt_pk_f32_fp8(c[i >> 2], true);
+                qf[i] = q01[0];
+                qf[i + 1] = q01[1];
+                qf[i + 2] = q23[0];
+                qf[i + 3] = q23[1];
             }
         }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xa[i] = kPsq4 ? __builtin_fabsf(x[i]) : x[i];
         const float num = butterfly_dot32<kPsq4>(xa, qf);   // PSQ8: x q has signs
         // PSQ4: every q q and partial sum is an integer below 2^24, so the
-        // butterfly's float sum is the exact integer sum in any order
-        const float den = kPsq4 ? (float)qq : butterfly_dot32<true>(qf, qf);
+        // butterfly's float sum is the exact sum in any order
+        float den;
+        if constexpr (kPsq4) {
+            den = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) den = __builtin_fmaf(qf[i], qf[i], den);
+        } else {
+            den = butterfly_dot32<true>(qf, qf);
+        }
         const float sl = den > 0.0f ? num / den : 0.0f;
         float s1 = psq_bf16_round(sl);
         if (!(s1 > 0.0f)) s1 = 0.0f;
-        psq_codes<kPsq4, false, true>(x, s1, amax, c);
+        psq_codes<kPsq4, true>(x, s1, amax, c);
         s = s1;
     }
 
