@@ -30,12 +30,6 @@
 // PSQ4 nibbles become E4M3 codes of the same value (v_perm table) and then
 // bf16 exactly, so no product is rounded before the fp32 accumulation.
 #include "device_common.h"
-#ifndef PSQ4_STAGES
-#define PSQ4_STAGES 2
-#endif
-#ifndef PSQ4_WPS
-#define PSQ4_WPS 2
-#endif
 
 #include <phaseshift_kv/paged_attention.h>
 
@@ -193,10 +187,7 @@ constexpr uint32_t kPageWindow = 1024;   // block-table entries staged in LDS pe
 template <int FMT>
 constexpr uint32_t page_window() { return FMT == kFmtPsq4 ? 512u : kPageWindow; }
 template <int FMT>
-constexpr int waves_per_simd() { return FMT == kFmtPsq4 ? PSQ4_WPS : 1; }
-// pipeline stages per wave (chunks in flight + the one being computed)
-template <int FMT>
-constexpr int decode_stages() { return FMT == kFmtPsq4 ? PSQ4_STAGES : 2; }
+constexpr int waves_per_simd() { return FMT == kFmtPsq4 ? 2 : 1; }
 
 // LDS bytes of one pipeline stage of one wave: K and V of a chunk (lane-major
 // DMA layout) and, FP8 and PSQ, the k/v scales of its tokens (256 B per
@@ -375,11 +366,8 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     const uint64_t layer_base = (uint64_t)a.layer * a.elems_per_layer;
     const uint64_t scale_layer = (uint64_t)a.layer * a.num_pages;
     uint32_t* const win = reinterpret_cast<uint32_t*>(lds);
-    constexpr int NSTG = decode_stages<FMT>();
-    uint8_t* const stage0 = lds + kWinBytes + (size_t)wave * NSTG * STAGE;
+    uint8_t* const stage0 = lds + kWinBytes + (size_t)wave * 2 * STAGE;
     uint8_t* const stage1 = stage0 + STAGE;
-    uint8_t* const stage2 = stage0 + (NSTG > 2 ? 2 : 0) * STAGE;
-    uint8_t* const stage3 = stage0 + (NSTG > 3 ? 3 : 0) * STAGE;
     bool bad = false;
 
     // tr-read address of this lane inside the V part of a stage; output block
@@ -811,8 +799,8 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
         // of this step's issue() outstanding.
         auto step = [&](uint32_t c, uint8_t* __restrict__ next,
                         const uint8_t* __restrict__ cur) __attribute__((always_inline)) {
-            issue(c + (NSTG - 1) * kStride, next);
-            wait_vmcnt<(NSTG - 1) * kStepOps>();
+            issue(c + kStride, next);
+            wait_vmcnt<kStepOps>();
             if constexpr (PK)
                 consume_pk(c, cur);
             else
@@ -820,45 +808,13 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
         };
 
         issue(cb, stage0);
-        if constexpr (NSTG == 2) {
-            for (;;) {
-                step(cb, stage1, stage0);
-                cb += kStride;
-                if (cb >= te) break;
-                step(cb, stage0, stage1);
-                cb += kStride;
-                if (cb >= te) break;
-            }
-        } else if constexpr (NSTG == 3) {
-            issue(cb + kStride, stage1);
-            for (;;) {
-                step(cb, stage2, stage0);
-                cb += kStride;
-                if (cb >= te) break;
-                step(cb, stage0, stage1);
-                cb += kStride;
-                if (cb >= te) break;
-                step(cb, stage1, stage2);
-                cb += kStride;
-                if (cb >= te) break;
-            }
-        } else {
-            issue(cb + kStride, stage1);
-            issue(cb + 2 * kStride, stage2);
-            for (;;) {
-                step(cb, stage3, stage0);
-                cb += kStride;
-                if (cb >= te) break;
-                step(cb, stage0, stage1);
-                cb += kStride;
-                if (cb >= te) break;
-                step(cb, stage1, stage2);
-                cb += kStride;
-                if (cb >= te) break;
-                step(cb, stage2, stage3);
-                cb += kStride;
-                if (cb >= te) break;
-            }
+        for (;;) {
+            step(cb, stage1, stage0);
+            cb += kStride;
+            if (cb >= te) break;
+            step(cb, stage0, stage1);
+            cb += kStride;
+            if (cb >= te) break;
         }
         // The last step issued a chunk nobody reads: its DMAs must land
         // before the stages are reused.
@@ -1072,8 +1028,7 @@ size_t decode_workgroup_lds_bytes(uint32_t kv_dtype, uint32_t head_dim) {
     const size_t cb = bf16 ? 2 * D : kv_dtype == PSK_KV_PSQ4_W32 ? D / 2 : D;
     const size_t stage = 2 * H * (16 * cb + 128) + (bf16 ? 0 : 2 * H * 256);
     const size_t win = kv_dtype == PSK_KV_PSQ4_W32 ? page_window<kFmtPsq4>() : kPageWindow;
-    const size_t nstg = kv_dtype == PSK_KV_PSQ4_W32 ? decode_stages<kFmtPsq4>() : 2;
-    return win * 4 + (size_t)kWaves * nstg * stage;
+    return win * 4 + (size_t)kWaves * 2 * stage;
 }
 
 namespace {
@@ -1083,7 +1038,7 @@ hipError_t launch_decode_t2(const DecodeParams& p, uint64_t grid, hipStream_t st
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     // block-table window + two pipeline stages per wave; the shared-item merge
     // later reuses the same LDS
-    const size_t v_bytes = (size_t)page_window<FMT>() * 4 + (size_t)NW * decode_stages<FMT>() * stage_bytes<FMT, D>();
+    const size_t v_bytes = (size_t)page_window<FMT>() * 4 + (size_t)NW * 2 * stage_bytes<FMT, D>();
     const size_t m_bytes = kIndep ? 0 : (size_t)NW * 32 * sizeof(float) +
                                             (size_t)NW * qpk * D * sizeof(float);
     const size_t lds_bytes = v_bytes > m_bytes ? v_bytes : m_bytes;
