@@ -487,46 +487,47 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
         }
         __syncthreads();
     }
-    // PSQ8 MaxAbs with dma_in: the wave's 64 blocks (whole (row, K|V) input
+    // MaxAbs with dma_in: the wave's 64 blocks (whole (row, K|V) input
     // segments of head_blocks x 64 B) reach LDS by four 16 B-per-lane DMAs,
     // instruction i lane l = chunk m = 64i + l of the wave's 4 KB (block m/4,
     // quarter m%4), so every instruction reads whole 128 B lines; lane l then
-    // reads its block at +64l. Lanes past the last task issue nothing.
-    // (Measured at 2^16 rows: PSQ8 MaxAbs 82.5 -> 71.7 us; the three heavier
-    // encoders lose 4-8 us that way against the per-lane 64 B loads.)
-    constexpr bool kDmaIn = !kPsq4 && !kLsq1;
+    // reads its block at +64l. The chunk's address is its block's input
+    // address, taken from the lane that owns the block. Lanes past the last
+    // task issue nothing. (Measured at 2^16 rows: PSQ8 MaxAbs 82.5 -> 70.5 us,
+    // PSQ4 MaxAbs 68.2 -> 67.5 us; both LSQ1 encoders lose 1-5 us that way: the
+    // wait for the whole 4 KB exposes the latency their longer arithmetic hid
+    // behind the per-lane 64 B loads.)
+    constexpr bool kDmaIn = !kLsq1;
     __shared__ __align__(16) uint8_t in_lds[kDmaIn ? 4 * 4096 : 16];
     const uint32_t lane = threadIdx.x & 63u;
     uint8_t* const wst = in_lds + (kDmaIn ? (threadIdx.x >> 6) * 4096u : 0u);
-    if (kDmaIn && p.dma_in) {
-        const uint32_t wbase = blockIdx.x * 256u + (threadIdx.x & ~63u);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t t = wbase + 16u * (uint32_t)i + (lane >> 2);
-            if (t < p.tasks) {
-                const uint32_t rt = fastdiv(t, p.div_head_blocks);
-                const uint32_t hbt = t - rt * p.head_blocks;
-                const bool vt = (rt & 1u) != 0u;
-                const uint16_t* srct = static_cast<const uint16_t*>(vt ? a.v_input : a.k_input) +
-                                       (uint64_t)(rt >> 1) * (vt ? a.v_row_stride : a.k_row_stride) +
-                                       (uint64_t)hbt * 32u + 8u * (lane & 3u);
-                load_lds<16, kCpolStream>(srct, wst + 1024 * i);
-            }
-        }
-    }
     const uint32_t task = blockIdx.x * 256u + threadIdx.x;
-    if (task >= p.tasks) return;
-    const uint32_t rest = fastdiv(task, p.div_head_blocks);
-    const uint32_t hb = task - rest * p.head_blocks;
+    const bool live = task < p.tasks;
+    const uint32_t rest = fastdiv(live ? task : 0u, p.div_head_blocks);
+    const uint32_t hb = (live ? task : 0u) - rest * p.head_blocks;
     const bool is_v = (rest & 1u) != 0u;
     const uint32_t row = rest >> 1;
+    const uint16_t* src = static_cast<const uint16_t*>(is_v ? a.v_input : a.k_input) +
+                          (uint64_t)row * (is_v ? a.v_row_stride : a.k_row_stride) +
+                          (uint64_t)hb * 32u;
+    if (kDmaIn && p.dma_in) {
+        const uint32_t wlast = p.tasks - (blockIdx.x * 256u + (threadIdx.x & ~63u));   // tasks left from the wave's first
+        const uint64_t sp = reinterpret_cast<uint64_t>(src);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t b = 16u * (uint32_t)i + (lane >> 2);
+            const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)sp, (int)b, 64);
+            const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(sp >> 32), (int)b, 64);
+            if (b < wlast)
+                load_lds<16, kCpolStream>(reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo) + 16u * (lane & 3u),
+                                          wst + 1024 * i);
+        }
+    }
+    if (!live) return;
 
     // row -> (page, offset), the reference skip rules (kv_append.hip:335-360)
     const uint32_t slot = a.row_sequence_slots[row];
     const uint32_t pos = a.row_positions[row];
-    const uint16_t* src = static_cast<const uint16_t*>(is_v ? a.v_input : a.k_input) +
-                          (uint64_t)row * (is_v ? a.v_row_stride : a.k_row_stride) +
-                          (uint64_t)hb * 32u;
     // input loads go out before the block-table load, which waits on slot
     float x[32];
     if (p.vec_in) {
