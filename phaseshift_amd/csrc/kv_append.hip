@@ -278,10 +278,11 @@ __global__ __launch_bounds__(256) void kv_append_generic_kernel(const AppendPara
 
 // ---------------------------------------------------------------- PSQ
 // One lane = one task = one 32-value block of one (row, K|V, kv head): the
-// block's 64 input bytes are four 16 B loads of that lane, so a wave reads 4
-// KB of consecutive input and every reduction of the block (amax, the LSQ1
-// sums) stays inside the lane. Tasks are ordered (row, K|V, head, block):
-// consecutive lanes read consecutive blocks and write consecutive code blocks.
+// block's 64 input bytes reach that lane (four 16 B loads, or the wave's 4 KB
+// staged in LDS by whole-line DMAs, see the kernel), and every reduction of
+// the block (amax, the LSQ1 sums) stays inside the lane. Tasks are ordered
+// (row, K|V, head, block): consecutive lanes read consecutive blocks and
+// write consecutive code blocks.
 struct PsqAppendParams {
     psk_kv_append_args a;
     uint8_t* k_code;
