@@ -140,3 +140,51 @@ def test_large_append_round_trip(dev):
     k = bf16_normal(rng, (rows, H * D), 0.01, 20.0)
     v = bf16_normal(rng, (rows, H * D), 0.01, 20.0)
     run_both(lay, 0, k, v, slots[perm], pos[perm], lay.block_tables, fp8=True)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_append_overwrites_positions(dev, fp8):
+    """A second append to positions already written replaces their K/V (and
+    FP8 scales) and leaves the rest of the pool as the first append wrote it
+    (the reference test's overwrite case, test_qwen35_mtp_kv_cache.hip:146-229):
+    two launches against the oracle applied in the same order."""
+    rng = np.random.default_rng(404)
+    lens = [40, 17]
+    lay = paged_layout(rng, lens, 16, 4, 256, spare_pages=2)
+    g = geom_of(lay)
+    og = dict(lay.geom, layer=0, block_table_stride=lay.block_tables.shape[1],
+              max_sequences=lay.block_tables.shape[0])
+    slots = np.repeat(np.arange(2), lens).astype(np.uint32)
+    pos = np.concatenate([np.arange(n) for n in lens]).astype(np.uint32)
+    k, v = bf16_normal(rng, (len(pos), 1024)), bf16_normal(rng, (len(pos), 1024))
+    # second launch: positions 15, 16 (a page boundary) and 39 of sequence 0,
+    # position 0 of sequence 1
+    slots2 = np.array([0, 0, 0, 1], np.uint32)
+    pos2 = np.array([15, 16, 39, 0], np.uint32)
+    k2, v2 = bf16_normal(rng, (4, 1024)), bf16_normal(rng, (4, 1024))
+    if fp8:
+        kp = np.full(lay.pool_elems, 0x3F, np.uint8)
+        ks = np.full(lay.scale_elems, -1.0, np.float32)
+    else:
+        kp = np.full(lay.pool_elems, 0x3F3F, np.uint16)
+        ks = None
+    vp, vs = kp.copy(), (None if ks is None else ks.copy())
+    dk, dv = to_dev(kp), to_dev(vp)
+    dks, dvs = (to_dev(ks), to_dev(vs)) if fp8 else (None, None)
+    bt = to_dev(lay.block_tables)
+    for kk, vv, ss, pp in ((k, v, slots, pos), (k2, v2, slots2, pos2)):
+        ops.kv_append(g, 0, to_dev(kk), to_dev(vv), to_dev(ss), to_dev(pp), bt, dk, dv, dks, dvs)
+        oracle.kv_append(og, kk, vv, ss, pp, lay.block_tables, kp, vp, ks, vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(dk), kp)
+    assert np.array_equal(to_host(dv), vp)
+    if fp8:
+        assert np.array_equal(to_host(dks).view(np.uint32), ks.view(np.uint32))
+        assert np.array_equal(to_host(dvs).view(np.uint32), vs.view(np.uint32))
+    # and the second launch did change the pool
+    kp1 = np.full_like(kp, 0x3F if fp8 else 0x3F3F)
+    vp1 = kp1.copy()
+    ks1 = None if ks is None else np.full_like(ks, -1.0)
+    vs1 = None if vs is None else ks1.copy()
+    oracle.kv_append(og, k, v, slots, pos, lay.block_tables, kp1, vp1, ks1, vs1)
+    assert not np.array_equal(kp1, kp)   # the second launch changed the pool
