@@ -512,7 +512,10 @@ __global__ __launch_bounds__(256) void kv_append_psq_kernel(const PsqAppendParam
                           (uint64_t)row * (is_v ? a.v_row_stride : a.k_row_stride) +
                           (uint64_t)hb * 32u;
     if (kDmaIn && p.dma_in) {
-        const uint32_t wlast = p.tasks - (blockIdx.x * 256u + (threadIdx.x & ~63u));   // tasks left from the wave's first
+        // tasks left from the wave's first (0 for a wave wholly past the end:
+        // it issues nothing, so no DMA outlives an exited wave)
+        const uint32_t wfirst = blockIdx.x * 256u + (threadIdx.x & ~63u);
+        const uint32_t wlast = wfirst < p.tasks ? p.tasks - wfirst : 0u;
         const uint64_t sp = reinterpret_cast<uint64_t>(src);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
