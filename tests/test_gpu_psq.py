@@ -285,6 +285,8 @@ def oracle_attn(lay, fmt, qh, q, slots, pos, bt, pools, layer=0):
     (8, 4, 64, [1, 70]),                                 # head_dim 64 (PSQ4: generic)
     (6, 2, 96, [50, 9]),                                 # head_dim 96: generic kernel
     (20, 1, 128, [70]),                                  # q_per_kv 20: generic kernel
+    (16, 1, 256, [300, 70]),                             # q_per_kv 16: MFMA kernel, unpacked columns
+    (12, 1, 128, [129, 33]),                             # q_per_kv 12, head_dim 128, unpacked
 ])
 def test_decode_matches_oracle(dev, fmt, qh, kvh, D, lens):
     _, lay, pools, q, slots, pos = attn_case(dev, fmt, lens, qh, kvh, D, seed=qh + D + fmt)
