@@ -5,8 +5,8 @@ and FP8, all against the fp32 oracle."""
 import numpy as np
 import pytest
 
-from tests.kvcase import INVALID, assert_attention_close
-from tests.test_gpu_paged_attention import REL, TOL, case, oracle_out, run_gpu
+from tests.kvcase import INVALID, REL_DECODE, assert_attention_close
+from tests.test_gpu_paged_attention import TOL, case, oracle_out, run_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -22,7 +22,7 @@ def test_many_short_units(dev, fp8):
     got = run_gpu(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs, splits=splits,
                   pages_per_split=pps)
     want = oracle_out(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
-    assert_attention_close(got, want, TOL[fp8], REL, "test_gpu_decode_many_units 1")
+    assert_attention_close(got, want, TOL[fp8], REL_DECODE, "test_gpu_decode_many_units 1")
 
 
 def test_many_units_long_rows(dev):
@@ -35,7 +35,7 @@ def test_many_units_long_rows(dev):
         assert splits <= 1024
         got = run_gpu(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs, splits=splits,
                       pages_per_split=pps)
-        assert_attention_close(got, want, TOL[True], REL, f"test_gpu_decode_many_units 2 {pps}")
+        assert_attention_close(got, want, TOL[True], REL_DECODE, f"test_gpu_decode_many_units 2 {pps}")
 
 
 def test_one_page_units_with_invalid_pages(dev):
@@ -51,4 +51,4 @@ def test_one_page_units_with_invalid_pages(dev):
     assert np.all(got[2] == 7.0) and np.all(got[9] == 7.0)
     keep = [i for i in range(12) if i not in (2, 9)]
     want = oracle_out(lay, 24, q[keep], slots[keep], pos[keep], bt, kp, vp, ks, vs)
-    assert_attention_close(got[keep], want, TOL[True], REL, "test_gpu_decode_many_units 3")
+    assert_attention_close(got[keep], want, TOL[True], REL_DECODE, "test_gpu_decode_many_units 3")

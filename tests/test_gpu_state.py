@@ -11,8 +11,8 @@ import torch
 import oracle
 import phaseshift_amd as P
 from phaseshift_amd import ops, state
-from tests.kvcase import (INVALID, assert_attention_close, bf16_normal, oracle_attention_parallel,
-                          to_dev, to_host)
+from tests.kvcase import (INVALID, REL_TILE, assert_attention_close, bf16_normal,
+                          oracle_attention_parallel, to_dev, to_host)
 
 pytestmark = pytest.mark.gpu
 
@@ -203,7 +203,8 @@ def test_config5_mixed_step(dev):
     bad = np.nonzero(err >= 5e-2)[0]
     print("rows over tolerance:", [(int(pick[i]), float(err[i])) for i in bad[:20]])
     assert np.max(err) < 5e-2
-    assert_attention_close(got, want, 5e-2, 1e-2, "config5 mixed step")
+    # decode, verify and prefill rows: FP8 KV, so the FP8 tile bound holds all
+    assert_attention_close(got, want, 5e-2, REL_TILE[True], "config5 mixed step")
     # ---- verify rollback: accept a random prefix of each 16-draft block
     free_before = pool.info().free_pages
     for i in range(n_ver):

@@ -11,8 +11,8 @@ import torch
 
 import phaseshift_amd as P
 from phaseshift_amd import ops, state
-from tests.kvcase import INVALID, assert_attention_close, bf16_normal, paged_layout, to_dev
-from tests.test_gpu_paged_attention import REL, TOL, make_pools, oracle_out
+from tests.kvcase import INVALID, REL_TILE, assert_attention_close, bf16_normal, paged_layout, to_dev
+from tests.test_gpu_paged_attention import TOL, make_pools, oracle_out
 
 pytestmark = pytest.mark.gpu
 
@@ -67,7 +67,7 @@ def test_grouped_prefill_vs_oracle(dev, fp8, qh, kvh, split):
                                     nan_rows[:8].tolist(), nan_heads,
                                     [(k.kind, k.row_begin, k.rows, k.splits, k.pages_per_split, k.side)
                                      for k in plan.kernels[:plan.count]])
-    assert_attention_close(got, want, TOL[fp8], REL, f"grouped prefill fp8={fp8} {qh}/{kvh} split={split}")
+    assert_attention_close(got, want, TOL[fp8], REL_TILE[fp8], f"grouped prefill fp8={fp8} {qh}/{kvh} split={split}")
 
 
 def test_grouped_prefill_d128(dev):
@@ -87,7 +87,7 @@ def test_grouped_prefill_d128(dev):
                     v_scale=vs, launch=True)
     torch.cuda.synchronize()
     want = oracle_out(lay, 12, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
-    assert_attention_close(out.cpu().numpy(), want, TOL[True], REL, "test_gpu_tile_groups 1")
+    assert_attention_close(out.cpu().numpy(), want, TOL[True], REL_TILE[True], "test_gpu_tile_groups 1")
 
 
 @pytest.mark.parametrize("fp8", [False, True])
@@ -122,7 +122,7 @@ def test_grouped_and_verify_tiles_page24(dev, fp8):
     want = oracle_out(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
     got = out.cpu().numpy()
     assert not np.any(got == 7.0)
-    assert_attention_close(got, want, TOL[fp8], REL, "test_gpu_tile_groups 2")
+    assert_attention_close(got, want, TOL[fp8], REL_TILE[fp8], "test_gpu_tile_groups 2")
 
 
 def invalid_page_step(dev, kvd, split, seed, pools_fn, oracle_fn):
@@ -168,4 +168,4 @@ def test_invalid_page_leaves_prefill_rows_unwritten(dev, fp8, split):
         lambda lay: make_pools(lay, fp8, 31 + fp8, dev),
         lambda lay, q, s, p, bt, pools: oracle_out(lay, 24, q, s, p, bt, *pools))
     assert not np.any(got == 7.0)
-    assert_attention_close(got, want, TOL[fp8], REL, f"test_gpu_tile_groups 3 {(fp8, split)}")
+    assert_attention_close(got, want, TOL[fp8], REL_TILE[fp8], f"test_gpu_tile_groups 3 {(fp8, split)}")

@@ -10,9 +10,9 @@ import torch
 
 import phaseshift_amd as P
 from phaseshift_amd import ops
-from tests.kvcase import (assert_attention_close, bf16_normal, oracle_attention_parallel, paged_layout,
-                          to_dev, to_host)
-from tests.test_gpu_paged_attention import REL, TOL, make_pools, oracle_out
+from tests.kvcase import (REL_BF16_OUT, REL_TILE, assert_attention_close, bf16_normal,
+                          oracle_attention_parallel, paged_layout, to_dev, to_host)
+from tests.test_gpu_paged_attention import TOL, make_pools, oracle_out
 
 pytestmark = pytest.mark.gpu
 
@@ -66,17 +66,17 @@ def test_tile_vs_oracle(dev, fp8, qh, kvh, D, prefix, chunk):
     lay, kp, vp, ks, vs, q, slots, pos = tile_case(qh + D + chunk, prefix, chunk, qh, kvh, D, fp8, dev)
     want = oracle_out(lay, qh, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
     got = run_tile(lay, qh, q, slots, pos, kp, vp, ks, vs)
-    assert_attention_close(got, want, TOL[fp8], REL, "test_gpu_tiles 1")
+    assert_attention_close(got, want, TOL[fp8], REL_TILE[fp8], "test_gpu_tiles 1")
     if prefix + chunk >= 512:
         got_s = run_tile(lay, qh, q, slots, pos, kp, vp, ks, vs, splits=8, pps=8)
-        assert_attention_close(got_s, want, TOL[fp8], REL, "test_gpu_tiles 2")
+        assert_attention_close(got_s, want, TOL[fp8], REL_TILE[fp8], "test_gpu_tiles 2")
 
 
 def test_tile_bf16_output_and_page64(dev):
     lay, kp, vp, ks, vs, q, slots, pos = tile_case(9, 3000, 40, 24, 4, 256, True, dev, P_=64)
     want = oracle_out(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
     got = run_tile(lay, 24, q, slots, pos, kp, vp, ks, vs, out_dtype=torch.bfloat16)
-    assert_attention_close(got, want, 5e-2, REL, "test_gpu_tiles 3")
+    assert_attention_close(got, want, 5e-2, REL_TILE[True] + REL_BF16_OUT, "test_gpu_tiles 3")
 
 
 def test_tile_rows_of_other_sequence_left_unwritten(dev):
@@ -91,4 +91,4 @@ def test_tile_rows_of_other_sequence_left_unwritten(dev):
     got = run_tile(lay, 24, q, slots, pos, kp, vp, ks, vs)
     assert np.all(got[10:] == 7.0)
     want = oracle_out(lay, 24, q[:10], slots[:10], pos[:10], lay.block_tables, kp, vp, ks, vs)
-    assert_attention_close(got[:10], want, 5e-2, REL, "test_gpu_tiles 4")
+    assert_attention_close(got[:10], want, 5e-2, REL_TILE[True], "test_gpu_tiles 4")

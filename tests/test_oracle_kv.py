@@ -99,8 +99,9 @@ def _attn_case(rng, lens, qh, kvh, D, P, fp8):
     return lay, g, q, kp, vp, ks, vs
 
 
-def _numpy_attention(lay, g, q, kp, vp, ks, vs, slots, pos, scale):
-    """float64 restatement: gather K/V per row, softmax, weighted sum."""
+def _numpy_attention(lay, g, q, kp, vp, ks, vs, slots, pos, scale, qf=None):
+    """float64 restatement: gather K/V per row, softmax, weighted sum. qf, if
+    given, replaces the bf16 Q by float values of the same shape."""
     qh, kvh, D, P = g["q_heads"], g["kv_heads"], g["head_dim"], g["page_tokens"]
     fp8 = kp.dtype == np.uint8
     K = (oracle.e4m3_decode(kp) if fp8 else oracle.bf16_to_f32(kp)).astype(np.float64)
@@ -111,7 +112,7 @@ def _numpy_attention(lay, g, q, kp, vp, ks, vs, slots, pos, scale):
         K = K * ks.reshape(lay.num_pages, P, kvh, 1)
         V = V * vs.reshape(lay.num_pages, P, kvh, 1)
     out = np.zeros((len(slots), qh * D))
-    Q = oracle.bf16_to_f32(q).astype(np.float64).reshape(len(slots), qh, D)
+    Q = (oracle.bf16_to_f32(q) if qf is None else qf).astype(np.float64).reshape(len(slots), qh, D)
     for r, (s, p) in enumerate(zip(slots, pos)):
         t = np.arange(p + 1)
         pages = lay.block_tables[s, t // P]
@@ -218,3 +219,48 @@ def test_copy_page_copies_every_layer_and_scales():
         assert np.array_equal(a[:, 4], b[:, 1]) and not a[:, :4].any()
         a = dst[k + "_scale"].reshape(L, NP, -1)
         assert np.array_equal(a[:, 4], src[k + "_scale"].reshape(L, NP, -1)[:, 1])
+
+
+def _q_e4m3_parts(qf, D):
+    """The FP8 tile kernel's Q operands, restated: per (row, head), q * 2^sh
+    with sh = 8 - E (max|q| = m * 2^E, m in [0.5, 1)) as E4M3 hi = RNE(q * 2^sh)
+    and lo = RNE(q * 2^sh - hi). Returns (hi, hi + lo) scaled back by 2^-sh."""
+    rows = qf.shape[0]
+    x = qf.reshape(rows, -1, D)
+    amax = np.abs(x).max(axis=2, keepdims=True)
+    _, E = np.frexp(amax)
+    sh = np.where(amax > 0, 8 - E, 0)
+    y = np.ldexp(x, sh).astype(np.float32)
+    hi = oracle.e4m3_decode(oracle.e4m3_encode(y)).astype(np.float64)
+    lo = oracle.e4m3_decode(oracle.e4m3_encode((y - hi).astype(np.float32))).astype(np.float64)
+    return np.ldexp(hi, -sh).reshape(rows, -1), np.ldexp(hi + lo, -sh).reshape(rows, -1)
+
+
+def test_fp8_tile_bound_catches_dropped_q_lo():
+    """The GPU tests hold FP8 tiles to REL_TILE[True] of each row's largest
+    output. That bound has bite: on inputs shaped like theirs (24/4 heads,
+    hd 256, FP8 KV, scale 1/16), a tile that fed only Q's E4M3 hi part to the
+    score MFMA would miss it by more than 4x, while the hi + lo pair the
+    kernel uses errs by far less than the bound (the rest of the measured
+    tile error, up to 6.6e-4, is P rounded to f16)."""
+    from tests.kvcase import REL_TILE
+    rng = np.random.default_rng(7)
+    lens = [1500, 800, 300, 2000]
+    lay, g, q, kp, vp, ks, vs = _attn_case(rng, lens, 24, 4, 256, 16, True)
+    slots = np.arange(4)
+    pos = np.array(lens) - 1
+    qf = oracle.bf16_to_f32(q).astype(np.float64)
+    hi, hilo = _q_e4m3_parts(qf, 256)
+    # hi + lo keeps q to 2^-8 relative; where lo is an E4M3 subnormal (small q)
+    # to half of lo's spacing, at most 2^-17 of the head's max
+    amax = np.repeat(np.abs(qf.reshape(4, 24, 256)).max(axis=2), 256, axis=1)
+    assert np.all(np.abs(hilo - qf) <= np.abs(qf) * 2.0**-8 + amax * 2.0**-17)
+    full = _numpy_attention(lay, g, q, kp, vp, ks, vs, slots, pos, 1 / 16)
+    row_max = np.abs(full).max(axis=1)
+
+    def rel(Q):
+        got = _numpy_attention(lay, g, q, kp, vp, ks, vs, slots, pos, 1 / 16, qf=Q)
+        return np.abs(got - full).max(axis=1) / row_max
+
+    assert np.all(rel(hi) > 4 * REL_TILE[True])
+    assert np.all(rel(hilo) < REL_TILE[True] / 50)
