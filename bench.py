@@ -186,7 +186,10 @@ def run_decode(torch, ops, st, steps, warmup, dev, splits=None, pps=None):
     return step_ms, t1.ms() / steps, t2.ms() / steps, nbytes_alg, splits, pps
 
 
-def run_append(torch, ops, rows, steps, warmup, dev, seed=7, graph=False):
+def run_append(torch, ops, rows, steps, warmup, dev, seed=7, graph=False, mode="append"):
+    """mode "append": the KV append alone; "meta_append": the row metadata of
+    `rows` one-row decode requests, then the append (two launches); "fused":
+    both in one launch (psk_kv_append_fp8_e4m3_from_requests)."""
     H, D, P = 4, 256, 16
     rng = np.random.default_rng(seed)
     seqs = max(1, rows // P)
@@ -205,7 +208,20 @@ def run_append(torch, ops, rows, steps, warmup, dev, seed=7, graph=False):
     ks = torch.empty(g.scale_elems, dtype=torch.float32, device=dev)
     vs = torch.empty_like(ks)
 
+    if mode != "append":
+        hs, hp = slots.cpu().numpy(), pos.cpu().numpy()
+        descs = [dict(slot=int(hs[r]), row_begin=r, row_count=1, prefix_length=int(hp[r]),
+                      execution_class=0) for r in range(rows)]
+        raw = torch.from_numpy(np.frombuffer(ops.pack_requests(descs), np.uint8).copy()).to(dev)
+        slots = torch.empty_like(slots)
+        pos = torch.empty_like(pos)
+
     def launch():
+        if mode == "fused":
+            ops.kv_append_from_requests(g, 0, k, v, raw, rows, slots, pos, bt, kp, vp, ks, vs)
+            return
+        if mode == "meta_append":
+            ops.prepare_row_metadata(raw, rows, rows, slots, pos)
         ops.kv_append(g, 0, k, v, slots, pos, bt, kp, vp, ks, vs)
 
     warm(torch, launch, warmup)
@@ -725,9 +741,6 @@ def run_mixed_step(torch, ops, steps, warmup, dev):
     part = torch.empty((256 << 20) // 4, dtype=torch.float32, device=dev)
     maxvis = int(ctx.max()) + 512
 
-    def meta():
-        ops.prepare_row_metadata(raw, len(descs), rows, rslots, rpos)
-
     def append():
         ops.kv_append(g, 0, kin, vin, rslots, rpos, bt, T["k"], T["v"], T["k_scale"],
                       T["v_scale"])
@@ -740,9 +753,13 @@ def run_mixed_step(torch, ops, steps, warmup, dev):
     def cow():
         pool.copy_pages_from(cache, dst_pages, cache_pages)
 
+    def meta_append():
+        # the step's row metadata formed inside the append launch
+        ops.kv_append_from_requests(g, 0, kin, vin, raw, len(descs), rslots, rpos, bt, T["k"], T["v"],
+                                    T["k_scale"], T["v_scale"])
+
     def step():
-        meta()
-        append()
+        meta_append()
         attend()
         cow()
 
@@ -754,20 +771,14 @@ def run_mixed_step(torch, ops, steps, warmup, dev):
             step()
     step_ms = t.ms() / steps
     parts = {}
-    for name, fn in (("append", append), ("attention", attend), ("cow_copy", cow)):
+    for name, fn in (("metadata_and_append", meta_append), ("append", append), ("attention", attend),
+                     ("cow_copy", cow)):
         tt = Timer(torch)
         with tt:
             for _ in range(steps):
                 fn()
         parts[name] = round(tt.ms() / steps, 4)
-    # rollback of the 8 verify blocks: keep a seeded accepted prefix of each
-    rb = Timer(torch)
-    with rb:
-        for i in range(n_ver):
-            sq = seqs[n_pre + n_dec + i]
-            keep = math.ceil((sq.position + int(rng.integers(0, 17))) / Pt)
-            sq.rollback(keep)
-    parts["rollback_8_blocks"] = round(rb.ms(), 4)
+    parts["rollback_8_blocks"] = time_rollback(torch, seqs[n_pre + n_dec:], rng, Pt)
     vis = np.asarray(visible, np.float64)
     flops = float((vis * QH * D * 4).sum())
     kinds = [(int(k.kind), int(k.rows), int(k.splits)) for k in plan.kernels[:plan.count]]
@@ -775,6 +786,40 @@ def run_mixed_step(torch, ops, steps, warmup, dev):
                 tokens_per_s=round(rows / (step_ms * 1e-3), 1), parts_ms=parts,
                 attention_tflops=round(flops / (parts["attention"] * 1e-3) / 1e12, 2),
                 attention_flops=flops, plan=kinds)
+
+
+def time_rollback(torch, ver_seqs, rng, page_tokens, warmup=5, reps=40):
+    """Rollback (page truncation) of the verify blocks' rejected tails, each
+    block keeping a seeded accepted prefix; the 16-draft reservation is
+    re-made before every repetition. Host: the time of the rollback calls
+    themselves (free-list updates plus the enqueue of each block-table clear).
+    GPU: HIP events around the clears, with the stream held busy while the
+    host enqueues them, so the events see only the clears' own execution."""
+    keeps = [math.ceil((sq.position + int(rng.integers(0, 17))) / page_tokens) for sq in ver_seqs]
+    host_us, gpu_us = [], []
+    released = 0
+    for r in range(warmup + reps):
+        for sq in ver_seqs:
+            sq.reserve(16)
+        torch.cuda.synchronize()
+        released = sum(len(sq.block_table()) - keep for sq, keep in zip(ver_seqs, keeps))
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1_000_000)
+        e0.record()
+        t0 = time.perf_counter()
+        for sq, keep in zip(ver_seqs, keeps):
+            sq.rollback(keep)
+        t1 = time.perf_counter()
+        e1.record()
+        torch.cuda.synchronize()
+        if r >= warmup:
+            host_us.append((t1 - t0) * 1e6)
+            gpu_us.append(e0.elapsed_time(e1) * 1e3)
+    return dict(blocks=len(ver_seqs), reps=reps,
+                host_us_median=round(float(np.median(host_us)), 2),
+                host_us_p90=round(float(np.percentile(host_us, 90)), 2),
+                gpu_us_median=round(float(np.median(gpu_us)), 2), pages_released_per_rep=released)
 
 
 def cpu_baseline(lens_row, seconds_cap=30.0):
@@ -947,6 +992,13 @@ def main():
         ap["rows_128_graph_replay"] = dict(tokens_per_s=round(128 / (gms * 1e-3), 1),
                                            ms_per_append=round(gms, 5),
                                            GBps=round(nb / (gms * 1e-3) / 1e9, 1))
+        # a planned step's row metadata + append: two launches, or one
+        # (metadata formed inside the append), graph-replayed
+        both = {}
+        for mode in ("meta_append", "fused"):
+            _, _, gm = run_append(torch, ops, 128, args.steps, args.warmup, dev, graph=True, mode=mode)
+            both[mode + "_us"] = round(gm * 1e3, 3)
+        ap["rows_128_metadata_and_append_graph_replay"] = both
         # the row sweep 2^12 .. 2^17: where the append leaves the launch-bound
         # regime for the HBM-bound one
         sweep = {}

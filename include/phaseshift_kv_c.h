@@ -174,6 +174,23 @@ int psk_kv_append_bf16(const psk_kv_append_args* a, void* k_pool, void* v_pool, 
 int psk_kv_append_fp8_e4m3(const psk_kv_append_args* a, void* k_pool, void* v_pool,
                            float* k_scale_pool, float* v_scale_pool, void* stream);
 
+/* KV append of a planned step with its row metadata formed in the same launch
+ * [runtime/batch/device_batch_context.hip:69-90 followed by
+ * kernels/optimized/kv_append.h:78-97]: row r of the append takes slot and
+ * prefix_length + (r - row_begin) of the first request whose rows hold it, and
+ * the launch writes them to a->row_sequence_slots / a->row_positions (which
+ * must be writable device arrays of a->rows entries) for the step's later
+ * launches; rows of no request are skipped and keep their metadata. Same
+ * result as psk_prepare_row_metadata followed by psk_kv_append_*, in one
+ * launch where the append takes its fast path (head_dim % 8 == 0, 16 B
+ * aligned slices), else in those two launches. */
+int psk_kv_append_bf16_from_requests(const psk_kv_append_args* a, const psk_request_descriptor* requests,
+                                     uint32_t num_requests, void* k_pool, void* v_pool, void* stream);
+int psk_kv_append_fp8_e4m3_from_requests(const psk_kv_append_args* a,
+                                         const psk_request_descriptor* requests, uint32_t num_requests,
+                                         void* k_pool, void* v_pool, float* k_scale_pool,
+                                         float* v_scale_pool, void* stream);
+
 /* ---- Paged attention [attention/paged_attention.h:140-201] ---------------- */
 int psk_attention_paged_bf16(const psk_paged_attention_args* a, const void* k_pool,
                              const void* v_pool, void* stream);

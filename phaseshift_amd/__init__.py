@@ -154,6 +154,8 @@ _U32 = C.c_uint32
 SIGNATURES = {
     "psk_kv_append_bf16": [_P, _P, _P, _P],
     "psk_kv_append_fp8_e4m3": [_P, _P, _P, _P, _P, _P],
+    "psk_kv_append_bf16_from_requests": [_P, _P, _U32, _P, _P, _P],
+    "psk_kv_append_fp8_e4m3_from_requests": [_P, _P, _U32, _P, _P, _P, _P, _P],
     "psk_attention_paged_bf16": [_P, _P, _P, _P],
     "psk_attention_paged_fp8_e4m3": [_P, _P, _P, _P, _P, _P],
     "psk_attention_paged_bf16_split": [_P, _P, _P, _P, _U32, _P],

@@ -154,6 +154,24 @@ __device__ __forceinline__ uint32_t row_ror8(uint32_t x) {
 }
 __device__ __forceinline__ float row_ror8(float x) { return __uint_as_float(row_ror8(__float_as_uint(x))); }
 
+// Maximum of x over the 64 lanes without the LDS crossbar: DPP row rotates
+// within each 16-lane row, then the permlane swaps across rows.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+    x = max(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, true));   // row_ror:8
+    x = max(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x124, 0xF, 0xF, true));   // row_ror:4
+    x = max(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x122, 0xF, 0xF, true));   // row_ror:2
+    x = max(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x121, 0xF, 0xF, true));   // row_ror:1
+    const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = max(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return max(b[0], b[1]);
+}
+
+// A wave-uniform float moved to a scalar register.
+__device__ __forceinline__ float uniform_f32(float x) {
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(x)));
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);

@@ -22,6 +22,7 @@
 #include "fastdiv.h"
 
 #include <phaseshift_kv/kv_append.h>
+#include <phaseshift_kv_c.h>
 
 namespace psk {
 namespace {
@@ -36,6 +37,11 @@ struct AppendParams {
     uint32_t log2_lanes;
     uint32_t chunks;           // ceil(head_dim / 8)
     uint32_t vec_ok;           // 16 B loads / vector stores legal
+    // kReq launches: rows take (slot, position) from these request
+    // descriptors and the kernel writes them to a.row_sequence_slots /
+    // a.row_positions for the later launches of the step
+    const psk_request_descriptor* req;
+    uint32_t num_req;
 };
 
 // Loads chunk `c` (elements 8c..8c+7) of a head slice as 8 floats; elements
@@ -88,7 +94,14 @@ __device__ __forceinline__ bool fast_div_ok(float scale) {
 // per wave (the launch-bound small appends of decode steps gain most).
 constexpr int kUnroll = 1;
 
-template <bool kFp8>
+// kReq: the row metadata of a planned step is formed here instead of by a
+// launch of its own (device_batch_context.hip:69-90): the wave loads 64
+// request descriptors at a time, one per lane, and each distinct row of its
+// tasks finds the first request whose [row_begin, row_begin + row_count)
+// holds it by a ballot; lane 0 of the row's first head writes the row's slot
+// and position. A row outside every request keeps its metadata and is not
+// appended.
+template <bool kFp8, bool kReq>
 __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams p) {
     const psk_kv_append_args& a = p.a;
     const uint32_t L = p.lanes_per_head;
@@ -114,8 +127,51 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
         const uint32_t t = live[u] ? task : 0u;
         row[u] = t / a.kv_heads;
         head[u] = t - row[u] * a.kv_heads;
-        slot[u] = a.row_sequence_slots[row[u]];
-        pos[u] = a.row_positions[row[u]];
+        if constexpr (!kReq) {
+            slot[u] = a.row_sequence_slots[row[u]];
+            pos[u] = a.row_positions[row[u]];
+        }
+    }
+    if constexpr (kReq) {
+        static_assert(kUnroll == 1, "request rows: one task group per wave");
+        // the wave's rows are consecutive: [row_lo, row_hi] of its live tasks
+        // (wave-uniform; a wave without live tasks scans nothing)
+        const uint32_t first_task = wave_global * tasks_per_wave;
+        const uint32_t row_lo = first_task / a.kv_heads;
+        const uint32_t row_hi = first_task < total ? (min(first_task + tasks_per_wave, total) - 1u) / a.kv_heads
+                                                   : row_lo - 1u;
+        slot[0] = 0xFFFFFFFFu;
+        pos[0] = 0u;
+        bool found = false;
+        for (uint32_t base = 0; base < p.num_req; base += 64u) {
+            const uint32_t r = base + lane;
+            uint32_t rb = 0u, rc = 0u, rs = 0u, rp = 0u;
+            if (r < p.num_req) {
+                const psk_request_descriptor* d = p.req + r;
+                rb = d->row_begin;
+                rc = d->row_count;
+                rs = d->slot;
+                rp = d->prefix_length;
+            }
+            for (uint32_t R = row_lo; R <= row_hi && first_task < total; ++R) {
+                const uint64_t m = __ballot(r < p.num_req && R >= rb && R - rb < rc);
+                if (m == 0u) continue;
+                const int idx = __builtin_ctzll(m);
+                const uint32_t s_ = __builtin_amdgcn_readlane(rs, idx);
+                const uint32_t p_ = __builtin_amdgcn_readlane(rp, idx) + (R - __builtin_amdgcn_readlane(rb, idx));
+                if (row[0] == R && !found) {
+                    slot[0] = s_;
+                    pos[0] = p_;
+                    found = true;
+                }
+            }
+            if (__all(found || !live[0])) break;
+        }
+        live[0] = live[0] && found;
+        if (live[0] && head[0] == 0u && sub == 0u) {
+            const_cast<uint32_t*>(a.row_sequence_slots)[row[0]] = slot[0];
+            const_cast<uint32_t*>(a.row_positions)[row[0]] = pos[0];
+        }
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -703,10 +759,33 @@ hipError_t launch(const AppendParams& p, hipStream_t stream) {
     const uint64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
     if (fast)
-        hipLaunchKernelGGL(kv_append_fast_kernel<kFp8>, dim3((uint32_t)blocks), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((kv_append_fast_kernel<kFp8, false>), dim3((uint32_t)blocks), dim3(256), 0, stream, p);
     else
         hipLaunchKernelGGL(kv_append_generic_kernel<kFp8>, dim3((uint32_t)blocks), dim3(256), 0, stream,
                            p);
+    return hipGetLastError();
+}
+
+// Row metadata from request descriptors fused into the append (fast path);
+// other shapes run the row-metadata launch and then the plain append.
+template <bool kFp8>
+hipError_t launch_req(AppendParams p, const psk_request_descriptor* req, uint32_t num_req,
+                      hipStream_t stream) {
+    const uint64_t tasks = (uint64_t)p.a.rows * p.a.kv_heads;
+    const uint64_t tasks_per_wave = 64u >> p.log2_lanes;
+    const bool fast = p.vec_ok != 0u && p.chunks <= p.lanes_per_head && tasks < 0xFFFFFFFFull;
+    if (!fast) {
+        const int e = psk_prepare_row_metadata(req, num_req, p.a.rows, const_cast<uint32_t*>(p.a.row_sequence_slots),
+                                               const_cast<uint32_t*>(p.a.row_positions), stream);
+        if (e != hipSuccess) return static_cast<hipError_t>(e);
+        return launch<kFp8>(p, stream);
+    }
+    p.req = req;
+    p.num_req = num_req;
+    const uint64_t waves = (tasks + tasks_per_wave - 1) / tasks_per_wave;
+    const uint64_t blocks = (waves + 3) / 4;
+    if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((kv_append_fast_kernel<kFp8, true>), dim3((uint32_t)blocks), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -781,6 +860,30 @@ extern "C" int psk_kv_append_fp8_e4m3(const psk_kv_append_args* a, void* k_pool,
     return psk::launch<true>(
         psk::make_params(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, 1u),
         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int psk_kv_append_bf16_from_requests(const psk_kv_append_args* a,
+                                                const psk_request_descriptor* requests,
+                                                uint32_t num_requests, void* k_pool, void* v_pool,
+                                                void* stream) {
+    if (a == nullptr || requests == nullptr || num_requests == 0u) return hipErrorInvalidValue;
+    const hipError_t e = psk::validate(*a, k_pool, v_pool);
+    if (e != hipSuccess) return e;
+    return psk::launch_req<false>(psk::make_params(*a, k_pool, v_pool, nullptr, nullptr, 2u), requests,
+                                  num_requests, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int psk_kv_append_fp8_e4m3_from_requests(const psk_kv_append_args* a,
+                                                    const psk_request_descriptor* requests,
+                                                    uint32_t num_requests, void* k_pool, void* v_pool,
+                                                    float* k_scale_pool, float* v_scale_pool,
+                                                    void* stream) {
+    if (a == nullptr || requests == nullptr || num_requests == 0u) return hipErrorInvalidValue;
+    hipError_t e = psk::validate(*a, k_pool, v_pool);
+    if (e != hipSuccess) return e;
+    if (k_scale_pool == nullptr || v_scale_pool == nullptr) return hipErrorInvalidValue;
+    return psk::launch_req<true>(psk::make_params(*a, k_pool, v_pool, k_scale_pool, v_scale_pool, 1u),
+                                 requests, num_requests, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int psk_kv_append_psq4(const psk_kv_append_args* a, uint8_t* k_code_pool,

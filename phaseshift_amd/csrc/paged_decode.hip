@@ -27,8 +27,13 @@
 // PSQ: each K-step of the score product is exactly one 32-value block, so its
 // partial score is multiplied by that block's K scale in fp32; P is multiplied
 // by the V scale of each block before the PV MFMAs of the block's 32 dims.
-// PSQ4 nibbles become E4M3 codes of the same value (v_perm table) and then
-// bf16 exactly, so no product is rounded before the fp32 accumulation.
+// PSQ4 nibbles become E4M3 codes of the same value (v_perm table), exact;
+// the K codes go to the fp8 MFMA as they are, against Q as E4M3 hi + lo parts
+// (about 2^-8 relative per element, one power of two per 32-dim block), and
+// the V codes become bf16 exactly. Two operands are rounded before the fp32
+// accumulation on the PSQ paths: that Q split (PSQ4) and P x V scale, a
+// single bf16 operand (8 significant bits) in the PV product; BF16 and FP8
+// carry P as a bf16 hi + lo pair instead.
 #include "device_common.h"
 
 #include <phaseshift_kv/paged_attention.h>
@@ -308,21 +313,40 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
     // - hi), which keep q to 2^-8 relative (the residual is exact in fp32);
     // the scores take the factor qinv = 2^-sh. Byte j of an operand is
     // element j of the bf16 operand it replaces (same dims, same order).
+    // Each 32-dim block s (one K-step, one K block scale) takes its own power
+    // of two: q * 2^(sh + d_s), d_s = E - E_s for the block's max|q| = m_s *
+    // 2^E_s, and the block's partial scores the factor qfac[s] = 2^-d_s next
+    // to its K scale. A block of small Q elements then keeps 2^-8 relative
+    // even where its K block scale is large (a single power of two per head
+    // would leave it 2^-17 of the head maximum in absolute terms).
     constexpr bool kQ8 = FMT == kFmtPsq4;
     uint64_t q8h[kQ8 ? NS : 1], q8l[kQ8 ? NS : 1];
     float qinv = 1.0f;
+    float qfac[kQ8 ? NS : 1];
     if constexpr (kQ8) {
+        float bmax[NS];
         float amax = 0.0f;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const u32x4 w = __builtin_bit_cast(u32x4, qf[s]);
+            bmax[s] = 0.0f;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                amax = __builtin_fmaxf(amax, __builtin_fmaxf(__builtin_fabsf(__uint_as_float(w[k] << 16)),
-                                                             __builtin_fabsf(__uint_as_float(w[k] & 0xFFFF0000u))));
+                bmax[s] = __builtin_fmaxf(bmax[s],
+                                          __builtin_fmaxf(__builtin_fabsf(__uint_as_float(w[k] << 16)),
+                                                          __builtin_fabsf(__uint_as_float(w[k] & 0xFFFF0000u))));
+            bmax[s] = max_xor32(max_xor16(bmax[s]));   // the head's lanes (n, g = 0..3)
+            amax = __builtin_fmaxf(amax, bmax[s]);
         }
-        amax = max_xor32(max_xor16(amax));   // the head's lanes (n, g = 0..3)
-        const int sh = (amax > 0.0f && amax <= 3.0e38f) ? 8 - __builtin_amdgcn_frexp_expf(amax) : 0;
+        const bool fin = amax > 0.0f && amax <= 3.0e38f;
+        const int eh = __builtin_amdgcn_frexp_expf(amax);
+        const int sh = fin ? 8 - eh : 0;
+        int dsv[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            dsv[s] = (fin && bmax[s] > 0.0f) ? min(eh - __builtin_amdgcn_frexp_expf(bmax[s]), 120) : 0;
+            qfac[s] = __builtin_ldexpf(1.0f, -dsv[s]);
+        }
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const u32x4 w = __builtin_bit_cast(u32x4, qf[s]);
@@ -332,8 +356,8 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                 float y[4], r[4];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    y[2 * t] = __builtin_ldexpf(__uint_as_float(w[2 * h + t] << 16), sh);
-                    y[2 * t + 1] = __builtin_ldexpf(__uint_as_float(w[2 * h + t] & 0xFFFF0000u), sh);
+                    y[2 * t] = __builtin_ldexpf(__uint_as_float(w[2 * h + t] << 16), sh + dsv[s]);
+                    y[2 * t + 1] = __builtin_ldexpf(__uint_as_float(w[2 * h + t] & 0xFFFF0000u), sh + dsv[s]);
                 }
                 hw[h] = e4m3x4_rne(y[0], y[1], y[2], y[3]);
                 r[0] = y[0] - __builtin_amdgcn_cvt_f32_fp8((int)hw[h], 0);
@@ -550,6 +574,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                                 kf, qf[s], (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                         }
                         const u32x4 kw = *reinterpret_cast<const u32x4*>(kscl + 64 * (s >> 1));
+                        if constexpr (kQ8) part *= qfac[s];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const float ksc = __uint_as_float((s & 1) ? (kw[r] & 0xFFFF0000u) : (kw[r] << 16));
@@ -731,6 +756,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                     part = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(ka, (long)q8m[hf][2 * s + 1], part, 0, 0, 0);
                 }
                 const u32x4 kw = *reinterpret_cast<const u32x4*>(kscl + 64 * (s >> 1));
+                part *= qfac[s];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float ksc = __uint_as_float((s & 1) ? (kw[r] & 0xFFFF0000u) : (kw[r] << 16));

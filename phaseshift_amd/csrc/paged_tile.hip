@@ -839,6 +839,9 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     constexpr int DPW = NL + 1;
     constexpr int kWinBytes = (int)kTilePageWindow * 4;
     constexpr int QD = D / 4;                         // dims one lane dequantizes per token row
+    // exponent headroom of the dequantized chunk: largest code x 2 x 2^kB
+    // (PSQ4 10 x 2 x 2^11 = 40960, PSQ8 448 x 2 x 2^6 = 57344) stays below 65504
+    constexpr int kB = FMT == kFmtPsq4 ? 11 : 6;
     static_assert((RT == NW && HPW == 2) || (RT == 1 && HPW == 1), "tile geometry");
     static_assert(NW >= 4 && NS % 2 == 0 && D % 128 == 0, "geometry");
 
@@ -930,23 +933,108 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     for (int i = 0; i < HPW; ++i) hv[i] = hbase + (uint32_t)i < qpk;
     if (tid == 0) bad_lds = 0u;
 
-    // Q fragments as f16, in the BF16 tiles' order: K-step s, dims 32s + 8g .. +8
+    // Q fragments as f16, in the BF16 tiles' order: K-step s, dims 32s + 8g ..
+    // +8, of q * 2^sq with sq = 14 - E for the workgroup's max|q| = m * 2^E (m
+    // in [0.5, 1)): the largest |value| lies in [2^13, 2^14), inside f16's
+    // range whatever the magnitude of q, and values down to 2^-27 of it stay
+    // in f16's normal range. The scores take qinv = 2^-sq (workgroup-uniform).
+    //
+    // K and V values likewise: with Ek (Ev) the largest biased exponent of the
+    // block scales of the workgroup's K (V) tokens [t_begin, t_end), every
+    // value is dequantized as f16(code x scale x 2^(kB + 127 - Ek)), so the
+    // largest stays below 2^(kB + 1) x the largest code, inside f16's range for
+    // any block scale. The scores take 2^(Ek - kB - 127) with the softmax
+    // scale, and O is accumulated in units of 2^(Ev - kB - 127).
+    __shared__ uint32_t wg_max_w[3][NW];
     f16x8 qf[HPW][NS];
+    float qinv;
+    int ek, ev;
+    {
+        u32x4 w_[HPW][NS];
+        float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < HPW; ++i) {
-        const uint32_t head = kv_head * qpk + (hv[i] ? hbase + (uint32_t)i : 0u);
-        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
-                               (uint64_t)(row_ok ? row : r0) * a.q_row_stride + (uint64_t)head * D;
+        for (int i = 0; i < HPW; ++i) {
+            const uint32_t head = kv_head * qpk + (hv[i] ? hbase + (uint32_t)i : 0u);
+            const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
+                                   (uint64_t)(row_ok ? row : r0) * a.q_row_stride + (uint64_t)head * D;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const u32x4 w = __builtin_bit_cast(u32x4, q8(qrow + s * 32 + (int)g * 8, row_ok && hv[i]));
-            u32x4 h;
+            for (int s = 0; s < NS; ++s) {
+                w_[i][s] = __builtin_bit_cast(u32x4, q8(qrow + s * 32 + (int)g * 8, row_ok && hv[i]));
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                h[k] = pack_f16x2(__uint_as_float(w[k] << 16), __uint_as_float(w[k] & 0xFFFF0000u));
-            qf[i][s] = __builtin_bit_cast(f16x8, h);
+                for (int k = 0; k < 4; ++k)
+                    amax = __builtin_fmaxf(amax,
+                                           __builtin_fmaxf(__builtin_fabsf(__uint_as_float(w_[i][s][k] << 16)),
+                                                           __builtin_fabsf(__uint_as_float(w_[i][s][k] & 0xFFFF0000u))));
+            }
         }
+        // block-scale exponents of the tokens [t_begin, t_end): 8 tokens per
+        // thread per pass, their page ids first, then their SW scale dwords of
+        // K and V (bf16 pairs; masks keep the exponent fields, compared as
+        // integers)
+        uint32_t kmax = 0u, vmax = 0u;
+        const uint32_t* ksp = reinterpret_cast<const uint32_t*>(p.k_scale);
+        const uint32_t* vsp = reinterpret_cast<const uint32_t*>(p.v_scale);
+        for (uint32_t t0 = t_begin + tid; t0 < t_end; t0 += 8u * NW * 64u) {
+            uint32_t pg[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t t = t0 + (uint32_t)u * NW * 64u;
+                pg[u] = t < t_end ? bt[t / P] : 0xFFFFFFFFu;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t t = t0 + (uint32_t)u * NW * 64u;
+                if (pg[u] >= a.num_pages) continue;
+                const uint64_t si = (((scale_layer + pg[u]) * P + t % P) * a.kv_heads + kv_head) * (uint64_t)SW;
+#pragma unroll
+                for (int k = 0; k < SW; ++k) {
+                    const uint32_t x = ksp[si + k], y = vsp[si + k];
+                    kmax = max(kmax, max(x & 0x7F800000u, (x & 0x7F80u) << 16));
+                    vmax = max(vmax, max(y & 0x7F800000u, (y & 0x7F80u) << 16));
+                }
+            }
+        }
+        amax = wave_max(amax);
+        kmax = wave_max_u32(kmax);
+        vmax = wave_max_u32(vmax);
+        if (lane == 0u) {
+            wg_max_w[0][w] = __float_as_uint(amax);
+            wg_max_w[1][w] = kmax;
+            wg_max_w[2][w] = vmax;
+        }
+        __syncthreads();
+        uint32_t am = 0u;
+        kmax = 0u;
+        vmax = 0u;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            am = max(am, wg_max_w[0][j]);   // non-negative floats order as integers
+            kmax = max(kmax, wg_max_w[1][j]);
+            vmax = max(vmax, wg_max_w[2][j]);
+        }
+        amax = __uint_as_float(am);
+        ek = (int)__builtin_amdgcn_readfirstlane(kmax >> 23);
+        ev = (int)__builtin_amdgcn_readfirstlane(vmax >> 23);
+        const int sq = __builtin_amdgcn_readfirstlane(
+            (amax > 0.0f && amax <= 3.0e38f) ? 14 - __builtin_amdgcn_frexp_expf(amax) : 0);
+        qinv = uniform_f32(__builtin_ldexpf(1.0f, -sq));
+#pragma unroll
+        for (int i = 0; i < HPW; ++i)
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                u32x4 h;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    h[k] = pack_f16x2(__builtin_ldexpf(__uint_as_float(w_[i][s][k] << 16), sq),
+                                      __builtin_ldexpf(__uint_as_float(w_[i][s][k] & 0xFFFF0000u), sq));
+                qf[i][s] = __builtin_bit_cast(f16x8, h);
+            }
     }
+    // softmax scale x qinv x 2^(Ek - kB - 127); the dequantization's exponent
+    // offsets (value bits - eshift) of K and V
+    const float sl = uniform_f32(p.scale_log2 * qinv * __builtin_ldexpf(1.0f, ek - kB - 127));
+    const int eshift_k = (ek - kB - 127) * (1 << 23);
+    const int eshift_v = (ev - kB - 127) * (1 << 23);
     float m_run[HPW], l_run[HPW];
     f32x4 o[HPW][NDB];
 #pragma unroll
@@ -1013,9 +1101,11 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
             load_lds<4>(sbase + si * (2u * D / 32u) + 4u * min(g, (uint32_t)SW - 1u),
                         st + 2 * KVC + kind * SC_BYTES + hf * 256);
         };
-        // code stage st -> f16 chunk: this lane's token row, QD dims
+        // code stage st -> f16 chunk: this lane's token row, QD dims, each
+        // value scaled by 2^(kB + 127 - Ek) (K) or 2^(kB + 127 - Ev) (V)
         auto dequant = [&](const uint8_t* st, uint8_t* bo) __attribute__((always_inline)) {
             if (NW > 4 && wu >= 4u) return;
+            const int eshift = d_kind == 0u ? eshift_k : eshift_v;   // wave-uniform
             const uint8_t* cb = st + d_kind * KVC + d_half * HSC + 16u * d_tok;
             const uint8_t* sc = st + 2 * KVC + d_kind * SC_BYTES + d_half * 256 + 4u * d_tok;
             uint8_t* ob = bo + d_kind * KVB_BYTES + d_half * HSB + 16u * d_tok;
@@ -1026,7 +1116,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 const uint32_t sb = (s & 1u) ? (sw & 0xFFFF0000u) : (sw << 16);   // the scale, f32 bits
                 // scale = 2^e x m: 2^e rides on the conversion, m in [1, 2)
                 // (exact in f16) multiplies the f16 pairs
-                const float s_pow2 = __uint_as_float(sb & 0x7F800000u);
+                const float s_pow2 = __uint_as_float((uint32_t)max((int)(sb & 0x7F800000u) - eshift, 0));
                 const uint32_t m2 = pack_f16x2(__uint_as_float((sb & 0x807FFFFFu) | 0x3F800000u),
                                                __uint_as_float((sb & 0x807FFFFFu) | 0x3F800000u));
                 // the block's 32 values as E4M3 bytes, dims 32s + 0 .. 31
@@ -1128,7 +1218,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
                 for (int hf = 0; hf < H; ++hf)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        s2[hf][r] = tok_ok[hf][r] ? sc[i][hf][r] * p.scale_log2 : -INFINITY;
+                        s2[hf][r] = tok_ok[hf][r] ? sc[i][hf][r] * sl : -INFINITY;
                         mx = __builtin_fmaxf(mx, s2[hf][r]);
                     }
                 mx = max_xor32(max_xor16(mx));
@@ -1233,23 +1323,32 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         return;
     }
     if (!row_ok || t_begin >= vis) return;
+    // O in true units: x 2^gu, gu = Ev - kB - 127, as two factors 2^(gu / 2)
+    // and 2^(gu - gu / 2), each inside fp32's range
+    const int gu = ev - kB - 127;
+    const float f_lo = __builtin_ldexpf(1.0f, gu >> 1);
+    const float f_hi = __builtin_ldexpf(1.0f, gu - (gu >> 1));
 #pragma unroll
     for (int i = 0; i < HPW; ++i) {
         if (!hv[i]) continue;
         const uint32_t gh = hbase + (uint32_t)i;
         const uint32_t head = kv_head * qpk + gh;
         const float l_all = sum_xor32(sum_xor16(l_run[i]));
+        const float f_out = f_hi / l_all;
         if (part_row == nullptr) {
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
                 const uint64_t oi = (uint64_t)row * a.output_row_stride + (uint64_t)head * D + db * 16 + 4 * g;
                 if (a.output_dtype == PSK_OUT_F32) {
-                    *reinterpret_cast<f32x4*>(static_cast<float*>(a.output) + oi) = o[i][db] / l_all;
+                    f32x4 v;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[r] = (o[i][db][r] * f_lo) * f_out;
+                    *reinterpret_cast<f32x4*>(static_cast<float*>(a.output) + oi) = v;
                 } else {
                     uint16_t* dst = static_cast<uint16_t*>(a.output) + oi;
                     u32x2 pk;
-                    pk[0] = pack_bf16x2(o[i][db][0] / l_all, o[i][db][1] / l_all);
-                    pk[1] = pack_bf16x2(o[i][db][2] / l_all, o[i][db][3] / l_all);
+                    pk[0] = pack_bf16x2((o[i][db][0] * f_lo) * f_out, (o[i][db][1] * f_lo) * f_out);
+                    pk[1] = pack_bf16x2((o[i][db][2] * f_lo) * f_out, (o[i][db][3] * f_lo) * f_out);
                     *reinterpret_cast<u32x2*>(dst) = pk;
                 }
             }
@@ -1260,8 +1359,12 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
             }
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
-                *reinterpret_cast<f32x4*>(part_row + 2u * qpk + gh * kPagedAttentionHeadLimit + db * 16 + 4 * g) =
-                    o[i][db];
+            {
+                f32x4 v;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = (o[i][db][r] * f_lo) * f_hi;
+                *reinterpret_cast<f32x4*>(part_row + 2u * qpk + gh * kPagedAttentionHeadLimit + db * 16 + 4 * g) = v;
+            }
         }
     }
 }

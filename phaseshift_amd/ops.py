@@ -127,6 +127,24 @@ def kv_append(geom: PoolGeometry, layer: int, k_in, v_in, slots, positions, bloc
             C.byref(a), _ptr(k_pool), _ptr(v_pool), s))
 
 
+def kv_append_from_requests(geom: PoolGeometry, layer: int, k_in, v_in, requests_dev,
+                            num_requests: int, slots, positions, block_tables, k_pool, v_pool,
+                            k_scale=None, v_scale=None, stream=None,
+                            max_sequences: int | None = None) -> None:
+    """Row metadata (device_batch_context.hip:69-90) and KV append in one
+    launch: slots / positions are written for the rows of the requests
+    (requests_dev: uint8 device tensor of num_requests RequestDescriptor)."""
+    a = append_args(geom, layer, k_in, v_in, slots, positions, block_tables, max_sequences)
+    s = _stream(stream)
+    if k_pool.dtype == torch.uint8:
+        check("psk_kv_append_fp8_e4m3_from_requests", lib().psk_kv_append_fp8_e4m3_from_requests(
+            C.byref(a), _ptr(requests_dev), num_requests, _ptr(k_pool), _ptr(v_pool), _ptr(k_scale),
+            _ptr(v_scale), s))
+    else:
+        check("psk_kv_append_bf16_from_requests", lib().psk_kv_append_bf16_from_requests(
+            C.byref(a), _ptr(requests_dev), num_requests, _ptr(k_pool), _ptr(v_pool), s))
+
+
 def attention_args(geom: PoolGeometry, layer: int, q, out, slots, positions, block_tables,
                    q_heads: int, scale: float | None = None,
                    max_sequences: int | None = None) -> PagedAttentionArgs:

@@ -188,3 +188,70 @@ def test_append_overwrites_positions(dev, fp8):
     vs1 = None if vs is None else ks1.copy()
     oracle.kv_append(og, k, v, slots, pos, lay.block_tables, kp1, vp1, ks1, vs1)
     assert not np.array_equal(kp1, kp)   # the second launch changed the pool
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("kvh,D", [(4, 256), (2, 128), (3, 100)])
+def test_append_from_requests_equals_metadata_then_append(dev, fp8, kvh, D):
+    """psk_kv_append_*_from_requests (row metadata and append in one launch)
+    against psk_prepare_row_metadata followed by psk_kv_append_*: the same
+    pool bytes, scales, slots and positions, bit for bit, and both against the
+    oracle's append. 150 requests (more than one 64-descriptor pass), given
+    out of row order: decode rows, a 16-row verify block, prefill chunks of
+    40 rows, and two rows (between requests) that no request covers, whose
+    slot/position entries must stay untouched and which are not appended.
+    head_dim 100 takes the two-launch route (no fast path)."""
+    rng = np.random.default_rng(7 + D + kvh + fp8)
+    spec = [(1, 0)] * 140 + [(16, 1)] + [(40, 2)] * 9
+    lens, descs, row = [], [], 0
+    gaps = {60, 145}
+    for i, (cnt, cls) in enumerate(spec):
+        if i in gaps:
+            row += 1
+        prefix = int(rng.integers(0, 300))
+        lens.append(prefix + cnt)
+        descs.append(dict(slot=i, row_begin=row, row_count=cnt, prefix_length=prefix, execution_class=cls))
+        row += cnt
+    rows = row
+    lay = paged_layout(rng, lens, 16, kvh, D, spare_pages=3)
+    order = rng.permutation(len(descs))
+    raw = to_dev(np.frombuffer(ops.pack_requests([descs[i] for i in order]), np.uint8).copy())
+    g = geom_of(lay)
+    k, v = bf16_normal(rng, (rows, kvh * D), 0.01), bf16_normal(rng, (rows, kvh * D), 0.01)
+    dk_in, dv_in, bt = to_dev(k), to_dev(v), to_dev(lay.block_tables)
+
+    def pools():
+        if fp8:
+            return (to_dev(np.full(lay.pool_elems, 0x3F, np.uint8)), to_dev(np.full(lay.pool_elems, 0x3F, np.uint8)),
+                    to_dev(np.full(lay.scale_elems, -1.0, np.float32)),
+                    to_dev(np.full(lay.scale_elems, -1.0, np.float32)))
+        return (to_dev(np.full(lay.pool_elems, 0x3F3F, np.uint16)),
+                to_dev(np.full(lay.pool_elems, 0x3F3F, np.uint16)), None, None)
+
+    sentinel = np.full(rows, 0xABCD1234, np.uint32)
+    s1, p1 = to_dev(sentinel), to_dev(sentinel)
+    a1 = pools()
+    ops.prepare_row_metadata(raw, len(descs), rows, s1, p1)
+    ops.kv_append(g, 0, dk_in, dv_in, s1, p1, bt, *a1)
+    s2, p2 = to_dev(sentinel), to_dev(sentinel)
+    a2 = pools()
+    ops.kv_append_from_requests(g, 0, dk_in, dv_in, raw, len(descs), s2, p2, bt, *a2)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(s1), to_host(s2)) and np.array_equal(to_host(p1), to_host(p2))
+    hs, hp = to_host(s2), to_host(p2)
+    gap_rows = np.nonzero(hs == 0xABCD1234)[0]
+    assert len(gap_rows) == 2 and np.all(hp[gap_rows] == 0xABCD1234)
+    for t1, t2 in zip(a1, a2):
+        if t1 is not None:
+            assert np.array_equal(to_host(t1).view(np.uint8), to_host(t2).view(np.uint8))
+    # and the oracle's append over the covered rows
+    covered = np.nonzero(hs != 0xABCD1234)[0]
+    og = dict(lay.geom, block_table_stride=lay.block_tables.shape[1], max_sequences=lay.block_tables.shape[0])
+    kp = np.full(lay.pool_elems, 0x3F if fp8 else 0x3F3F, np.uint8 if fp8 else np.uint16)
+    vp = kp.copy()
+    ks = np.full(lay.scale_elems, -1.0, np.float32) if fp8 else None
+    vs = None if ks is None else ks.copy()
+    oracle.kv_append(og, k[covered], v[covered], hs[covered], hp[covered], lay.block_tables, kp, vp, ks, vs)
+    assert np.array_equal(to_host(a2[0]), kp) and np.array_equal(to_host(a2[1]), vp)
+    if fp8:
+        assert np.array_equal(to_host(a2[2]).view(np.uint32), ks.view(np.uint32))

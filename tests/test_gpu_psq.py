@@ -25,7 +25,12 @@ from tests.kvcase import (INVALID, Layout, assert_attention_close, bf16_normal,
 pytestmark = pytest.mark.gpu
 
 TOL = 5e-2
-REL = 1e-2   # per row, of the row's largest oracle output
+# Per row, of the row's largest oracle output: 3.3x the largest error measured
+# over this file on MI355X with fp32 output (2.4e-3; single bf16 P x V scale
+# operand in the decode PV product, f16 chunk values in the tiles); bf16
+# output adds its own rounding (2^-9 of a value): 4.6e-3 measured, 1e-2 bound.
+REL = 8e-3
+REL_BF16 = 1e-2
 
 
 def geom_of(lay):
@@ -324,7 +329,7 @@ def test_many_rows_independent_waves_bf16_out(dev, fmt):
     want = oracle_attn(lay, fmt, 24, q, slots, pos, lay.block_tables, pools)
     got = run_attn(dev, lay, fmt, 24, q, slots, pos, lay.block_tables, pools,
                    out_dtype=torch.bfloat16)
-    assert_attention_close(got, want, TOL, REL, "test_gpu_psq 4")
+    assert_attention_close(got, want, TOL, REL_BF16, "test_gpu_psq 4")
 
 
 @pytest.mark.parametrize("fmt", [4, 8])
@@ -675,3 +680,146 @@ def test_invalid_page_leaves_grouped_prefill_rows_unwritten(dev, fmt, split):
         lambda lay, q, s, p, bt, pools: oracle_attn(lay, fmt, 24, q, s, p, bt, pools))
     assert not np.any(got == 7.0)
     assert_attention_close(got, want, TOL, REL, f"test_gpu_psq 15 {(fmt, split)}")
+
+
+# ------------------------------------------------- peaked softmax at 32k
+CB10 = np.array([0, 1, 2, 3, 4, 6, 8, 10, 0, -1, -2, -3, -4, -6, -8, -10], np.float32)
+
+
+def psq_dequant_head(lay, fmt, kc, ks, page, head):
+    """Dequantised [page_tokens, head_dim] values of one (page, kv head) of
+    layer 0, read from host code and scale pools (layout: block
+    ((page * P + off) * kv_heads + head) * D / 32 + d / 32)."""
+    P, H, D = lay.page_tokens, lay.kv_heads, lay.head_dim
+    nb = D // 32
+    blk = ((page * P + np.arange(P))[:, None] * H + head) * nb + np.arange(nb)[None, :]   # [P, nb]
+    s = oracle.bf16_to_f32(ks[blk.ravel()]).reshape(P, nb, 1)
+    if fmt == 4:
+        b = kc.reshape(-1, 16)[blk.ravel()].astype(np.int64)
+        c = np.concatenate([b & 15, b >> 4], axis=1)
+        val = CB10[c].reshape(P, nb, 32)
+    else:
+        val = oracle.e4m3_decode(kc.reshape(-1, 32)[blk.ravel()]).reshape(P, nb, 32)
+    return (val * s).reshape(P, D)
+
+
+def peaked_psq_case(dev, fmt, lens, seed, target_std=4.0):
+    """PSQ pools with Q scaled by a power of two so that the scores of row 0,
+    head 0 over its first 128 pages have standard deviation ~target_std."""
+    rng = np.random.default_rng(seed)
+    lay = paged_layout(rng, lens, 16, 4, 256, spare_pages=1)
+    pools = dev_pools(lay, fmt, dev, seed=seed)
+    kc, ks = to_host(pools[0]), to_host(pools[2])
+    K = np.concatenate([psq_dequant_head(lay, fmt, kc, ks, int(p), 0)
+                        for p in lay.block_tables[0][:128]]).astype(np.float64)
+    q0 = bf16_normal(rng, (len(lens), 24 * 256))
+    s = K @ oracle.bf16_to_f32(q0[0, :256]).astype(np.float64) / 16.0
+    factor = 2.0 ** round(math.log2(target_std / s.std()))
+    q = oracle.f32_to_bf16(oracle.bf16_to_f32(q0) * np.float32(factor))
+    return lay, pools, q
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_peaked_softmax_32k_psq(dev, fmt):
+    """Scores with std ~4 at 32k context over PSQ pools: decode unsplit, the
+    reference split rule and chooser-size splits, and a 16-row verify block at
+    the end of a 32k row on the decode and the tile kernels, every row against
+    the fp32 oracle. The oracle outputs reach O(1) here, so misweighted tokens
+    fail the per-row bound."""
+    lens = [32768, 32768, 30001, 32768]
+    lay, pools, q = peaked_psq_case(dev, fmt, lens, 950 + fmt)
+    bt = lay.block_tables
+    slots = np.arange(3, dtype=np.uint32)
+    pos = np.asarray(lens[:3], np.uint32) - 1
+    want = oracle_attn(lay, fmt, 24, q[:3], slots, pos, bt, pools)
+    print(f"psq{fmt} peaked32k oracle row maxima:", np.abs(want).reshape(3, -1).max(axis=1))
+    assert np.abs(want).reshape(3, -1).max(axis=1).min() > 0.3    # the case is peaked
+    for splits, pps in ((1, 0), (16, 0), (8, 256), (64, 32)):
+        got = run_attn(dev, lay, fmt, 24, q[:3], slots, pos, bt, pools, splits, pps)
+        assert_attention_close(got, want, TOL, REL, f"psq{fmt} peaked32k {splits}/{pps}")
+    rng = np.random.default_rng(78)
+    qv = q[rng.integers(0, 4, 16)].copy()
+    vslots = np.full(16, 3, np.uint32)
+    vpos = np.arange(32752, 32768, dtype=np.uint32)
+    want_v = oracle_attn(lay, fmt, 24, qv, vslots, vpos, bt, pools)
+    for kind in ("decode", "prefill"):
+        got = run_attn(dev, lay, fmt, 24, qv, vslots, vpos, bt, pools, kind=kind)
+        assert_attention_close(got, want_v, TOL, REL, f"psq{fmt} peaked32k verify {kind}")
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_wide_range_q_head(dev, fmt):
+    """One query head per row holds one large element and small rest (a 2^12
+    spread): the PSQ decode (E4M3 hi + lo Q on PSQ4) and tile paths keep the
+    small elements' contribution within the per-row bound."""
+    _, lay, pools, q, slots, pos = attn_case(dev, fmt, [900, 2000, 64], 24, 4, 256, seed=71 + fmt)
+    qf = oracle.bf16_to_f32(q).reshape(3, 24, 256)
+    qf[:, 5, :] *= 2.0 ** -6
+    qf[:, 5, 17] = 40.0
+    qf[:, 11, :] *= 2.0 ** -3
+    qf[:, 11, 200] = -25.0
+    q = oracle.f32_to_bf16(qf.reshape(3, -1))
+    bt = lay.block_tables
+    want = oracle_attn(lay, fmt, 24, q, slots, pos, bt, pools)
+    for splits in (1, 4):
+        got = run_attn(dev, lay, fmt, 24, q, slots, pos, bt, pools, splits)
+        assert_attention_close(got, want, TOL, REL, f"psq{fmt} wide-range q {splits}")
+    vq = np.repeat(q[1:2], 16, axis=0)
+    vs_, vp_ = np.full(16, 1, np.uint32), np.arange(1984, 2000, dtype=np.uint32)
+    want_v = oracle_attn(lay, fmt, 24, vq, vs_, vp_, bt, pools)
+    got = run_attn(dev, lay, fmt, 24, vq, vs_, vp_, bt, pools, kind="prefill")
+    assert_attention_close(got, want_v, TOL, REL, f"psq{fmt} wide-range q tile")
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_large_block_scales_and_q_stay_finite(dev, fmt):
+    """Values past f16's range (65504): K block 3 of every token and 5% of the
+    V blocks carry scales that put |value| near 1e5 (Q's dims of block 3 scaled
+    down by the same factor, so the scores stay O(1)), and every fifth row has
+    query elements up to 1e5 on the dims 0..31, whose K codes are all 0. The decode
+    kernel, the ungrouped tiles and the grouped prefill tiles (a 128-row
+    prefill through the planner) must return finite outputs within the
+    per-row bound of the oracle, as the reference's bf16 / fp32 arithmetic
+    does."""
+    from phaseshift_amd import KV_PSQ4, KV_PSQ8, state
+    rng = np.random.default_rng(515 + fmt)
+    lens = [700, 1300]
+    lay = paged_layout(rng, lens, 16, 4, 256, spare_pages=1)
+    kc, vc, ks, vs = dev_pools(lay, fmt, dev, seed=515 + fmt)
+    nb, cbs = 256 // 32, (16 if fmt == 4 else 32)
+    big = 8192.0 if fmt == 4 else 256.0          # amax 81920 / 114688
+    bigv = torch.tensor([big], device=dev).to(torch.bfloat16).view(torch.int16)
+    ks.view(-1, nb)[:, 3] = bigv
+    sel = torch.from_numpy(rng.random(ks.numel()) < 0.05).to(dev)
+    vs.copy_(torch.where(sel, bigv.expand_as(vs), vs))
+    kc.view(-1, nb, cbs)[:, 0, :] = 0                  # dims 0..31 of every head: K = 0
+    pools = (kc, vc, ks, vs)
+    rows = 128 + 16
+    slots = np.array([0] * 128 + [1] * 16, np.uint32)
+    pos = np.array(list(range(700 - 128, 700)) + list(range(1300 - 16, 1300)), np.uint32)
+    qf = oracle.bf16_to_f32(bf16_normal(rng, (rows, 24 * 256))).reshape(rows, 24, 256)
+    qf[:, :, 96:128] /= big
+    qf[::5, 3, :32] *= 3.0e4                        # past f16's range, on K = 0
+    qf[::5, 3, 7] = 1.0e5
+    q = oracle.f32_to_bf16(qf.reshape(rows, -1))
+    want = oracle_attn(lay, fmt, 24, q, slots, pos, lay.block_tables, pools)
+    assert np.all(np.isfinite(want))
+
+    def check(got, what):
+        got = np.asarray(got, np.float64)
+        assert np.all(np.isfinite(got)), what
+        err = np.abs(got - want).max(axis=1)
+        row_max = np.abs(want).max(axis=1)
+        bad = np.nonzero(err > REL * row_max + 1e-6)[0]
+        assert bad.size == 0, (what, int(bad[0]), float(err[bad[0]]), float(row_max[bad[0]]))
+
+    check(run_attn(dev, lay, fmt, 24, q, slots, pos, lay.block_tables, pools), "decode")
+    check(run_attn(dev, lay, fmt, 24, q, slots, pos, lay.block_tables, pools, kind="prefill"), "tiles")
+    out = torch.full((rows, 24 * 256), 7.0, dtype=torch.float32, device=dev)
+    a = ops.attention_args(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
+                           to_dev(lay.block_tables), 24)
+    plan = state.plan_step(a, KV_PSQ4 if fmt == 4 else KV_PSQ8, [(0, 128, 2, 700), (128, 16, 1, 1300)],
+                           1300, 0, None, *pools, launch=True)
+    torch.cuda.synchronize()
+    assert any(k.kind == 1 and k.rows == 128 for k in plan.kernels[:plan.count])
+    check(out.cpu().numpy(), "grouped prefill")

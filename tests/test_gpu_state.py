@@ -11,7 +11,7 @@ import torch
 import oracle
 import phaseshift_amd as P
 from phaseshift_amd import ops, state
-from tests.kvcase import (INVALID, REL_TILE, assert_attention_close, bf16_normal,
+from tests.kvcase import (INVALID, REL_DECODE, REL_TILE, assert_attention_close, bf16_normal,
                           oracle_attention_parallel, to_dev, to_host)
 
 pytestmark = pytest.mark.gpu
@@ -56,6 +56,10 @@ def test_reserve_rollback_commit(dev):
     dev_row = to_host(bt)[seq.slot]
     assert list(dev_row[:3]) == table[:3] and np.all(dev_row[3:] == INVALID)
     assert pool.info().free_pages == 61 and seq.block_table() == table[:3]
+    seq.rollback(3)                    # repeated rollback: no-op, no double free
+    torch.cuda.synchronize()
+    assert pool.info().free_pages == 61 and seq.block_table() == table[:3]
+    assert list(to_host(bt)[seq.slot][:3]) == table[:3]
     seq.commit(1)
     assert seq.position == 41
     with pytest.raises(P.StateError) as e:
@@ -185,11 +189,13 @@ def test_config5_mixed_step(dev):
         assert np.array_equal(to_host(T[k]), pool_before[k])
     for k in ("k_scale", "v_scale"):
         assert np.array_equal(to_host(T[k]).view(np.uint32), pool_before[k].view(np.uint32))
-    # ---- attention parity on all decode + verify rows and 4 rows per prefill chunk
+    # ---- attention parity: every decode and verify row, every 8th row of each
+    # prefill chunk, and all 512 rows of the chunk with the shortest context
     pick = list(range(48 + 128))
+    shortest = int(np.argmin(ctx[:n_pre]))
     for i in range(n_pre):
         b = 176 + 512 * i
-        pick += [b, b + 1, b + 300, b + 511]
+        pick += list(range(b, b + 512)) if i == shortest else list(range(b, b + 512, 8)) + [b + 511]
     pick = np.array(pick)
     og = dict(geom, q_heads=QH)
     want = oracle_attention_parallel(og, q[pick], h_slots[pick], h_pos[pick], h_bt,
@@ -199,24 +205,71 @@ def test_config5_mixed_step(dev):
     err = np.max(np.abs(got - want), axis=1)
     groups = {"decode": err[:48], "verify": err[48:176], "prefill": err[176:]}
     worst = {k: (float(v.max()), int(np.argmax(v))) for k, v in groups.items()}
-    print("config5 max-abs error per group (value, index):", worst)
+    print("config5 max-abs error per group (value, index):", worst, "prefill rows checked:", len(pick) - 176)
     bad = np.nonzero(err >= 5e-2)[0]
     print("rows over tolerance:", [(int(pick[i]), float(err[i])) for i in bad[:20]])
     assert np.max(err) < 5e-2
     # decode, verify and prefill rows: FP8 KV, so the FP8 tile bound holds all
     assert_attention_close(got, want, 5e-2, REL_TILE[True], "config5 mixed step")
     # ---- verify rollback: accept a random prefix of each 16-draft block
+    # (paged_sequence_state.cpp:189-229; the reference's speculative
+    # transaction test, test_qwen35_spec_transaction.hip:170-203: pages
+    # released exactly, a repeated rollback is a no-op, the rejected tail is
+    # invisible to the next step)
     free_before = pool.info().free_pages
+    released = 0
+    ver = []
     for i in range(n_ver):
         s = seqs[n_pre + n_dec + i]
-        accepted = int(rng.integers(0, 17))
+        accepted = int(rng.integers(0, 16)) if i else 0   # block 0 rejects every draft
         new_pos = s.position + accepted
         keep = math.ceil(new_pos / Pt)
         old = s.block_table()
         s.rollback(keep)
+        released += len(old) - keep
         if accepted:
             s.commit(accepted)
+        s.rollback(keep)                  # repeated: no-op, nothing freed twice
         torch.cuda.synchronize()
         dev_row = to_host(bt)[s.slot]
         assert list(dev_row[:keep]) == old[:keep] and np.all(dev_row[keep:len(old)] == INVALID)
-    assert pool.info().free_pages >= free_before
+        assert s.block_table() == old[:keep] and s.position == new_pos
+        ver.append((s, 16 - accepted))
+    assert pool.info().free_pages == free_before + released
+    assert released > 0
+    # next step: one new token per verify sequence at its accepted position.
+    # The rejected drafts' K/V stay in the kept pages past that position; the
+    # decode must not see them.
+    nv = len(ver)
+    v_slots = np.array([s.slot for s, _ in ver], np.uint32)
+    v_pos = np.array([s.position for s, _ in ver], np.uint32)
+    for s, _ in ver:
+        s.reserve(1)
+    torch.cuda.synchronize()
+    h_bt = to_host(bt)
+    kin2 = bf16_normal(rng, (nv, H * D), 0.01, 20.0)
+    vin2 = bf16_normal(rng, (nv, H * D), 0.01, 20.0)
+    ds2, dp2 = to_dev(v_slots), to_dev(v_pos)
+    before2 = {k: to_host(v).copy() for k, v in T.items()}
+    ops.kv_append(g, 0, to_dev(kin2), to_dev(vin2), ds2, dp2, bt, T["k"], T["v"], T["k_scale"], T["v_scale"])
+    oracle.kv_append(dict(geom, block_table_stride=h_bt.shape[1]), kin2, vin2, v_slots, v_pos, h_bt,
+                     before2["k"], before2["v"], before2["k_scale"], before2["v_scale"])
+    after2 = {k: to_host(v) for k, v in T.items()}
+    for k in ("k", "v"):
+        assert np.array_equal(after2[k], before2[k])
+    q2 = bf16_normal(rng, (nv, QH * D))
+    out2 = torch.full((nv, QH * D), 7.0, dtype=torch.float32, device=dev)
+    ops.paged_attention(g, 0, to_dev(q2), out2, ds2, dp2, bt, T["k"], T["v"], QH, T["k_scale"], T["v_scale"])
+    got2 = out2.cpu().numpy()
+    want2 = oracle_attention_parallel(og, q2, v_slots, v_pos, h_bt, after2["k"], after2["v"],
+                                      after2["k_scale"], after2["v_scale"], 1.0 / 16.0, workers=8)
+    assert_attention_close(got2, want2, 5e-2, REL_DECODE, "config5 decode after rollback")
+    # the check has bite: a decode that read the stale tail (the rejected
+    # drafts still in the kept page past the new token) would break the bound
+    stale = np.array([p_ + min(r - 1, Pt - 1 - p_ % Pt) for p_, (_, r) in zip(v_pos, ver)], np.uint32)
+    many = stale >= v_pos + 4
+    assert np.any(many)
+    seen = oracle_attention_parallel(og, q2[many], v_slots[many], stale[many], h_bt, after2["k"],
+                                     after2["v"], after2["k_scale"], after2["v_scale"], 1.0 / 16.0, workers=8)
+    row_max = np.abs(want2[many]).max(axis=1)
+    assert np.all(np.abs(seen - want2[many]).max(axis=1) > REL_DECODE * row_max + 1e-6)

@@ -200,8 +200,8 @@ def test_args_keep_their_tensors_alive():
 
 def test_split_chooser_against_measured_sweep():
     """psk_choose_decode_split on the bench workloads picks a split whose measured
-    kernel time (one MI355X, tests/measured/decode_split_times_mi355x.json, written by
-    sweep_decode_splits.py beside it) is within 5% of the fastest measured split."""
+    kernel time (one MI355X, tests/measured/decode_split_times_mi355x.json, written on one
+    MI355X box by a working sweep script that is not part of the library) is within 5% of the fastest measured split."""
     import json
     import os
     import numpy as np
