@@ -461,6 +461,29 @@ def run_prefix_cache(torch, steps, warmup, dev):
                restore_GBps_read_plus_write=round(2 * moved / (r_ms * 1e-3) / 1e9, 1),
                launches_per_save=int(st.copy_launches // max(1, 2 * (steps + max(warmup, 3)))),
                reference_copies_per_save=(tokens // P) * L * 4 + 4)
+    # the page copy alone, kernel time: the same per-block copy (page body and
+    # scale rows of K or V per workgroup) over the sequence's 256 pages x 6
+    # layers into the pool's free pages, 20 back-to-back launches
+    from phaseshift_amd import ops
+    T = kv.tensors(torch)
+    src_pages = seq.block_table()
+    used = set(src_pages)
+    dst_pages = [pg for pg in range(kv.geom.num_pages) if pg not in used][:len(src_pages)]
+    pairs = torch.tensor(list(zip(dst_pages, src_pages)), dtype=torch.int32, device=dev)
+    kv_bytes = len(src_pages) * L * 2 * (P * H * D + P * H * 4)
+
+    def cp():
+        ops.copy_pages(kv.geom, T, T, pairs)
+
+    warm(torch, cp, warmup)
+    t = Timer(torch)
+    with t:
+        for _ in range(20):
+            cp()
+    k_ms = t.ms() / 20
+    res["page_copy_kernel"] = dict(pages=len(src_pages), layers=L, bytes_read=kv_bytes, us=round(k_ms * 1e3, 2),
+                                   GBps_read_plus_write=round(2 * kv_bytes / (k_ms * 1e-3) / 1e9, 1),
+                                   frac_of_peak=round(2 * kv_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
     gdn.release(seq.slot)
     seq.release()
     cache.close()

@@ -97,10 +97,10 @@ constexpr int kUnroll = 1;
 // kReq: the row metadata of a planned step is formed here instead of by a
 // launch of its own (device_batch_context.hip:69-90): the wave loads 64
 // request descriptors at a time, one per lane, and each distinct row of its
-// tasks finds the first request whose [row_begin, row_begin + row_count)
-// holds it by a ballot; lane 0 of the row's first head writes the row's slot
-// and position. A row outside every request keeps its metadata and is not
-// appended.
+// tasks finds the request whose [row_begin, row_begin + row_count) holds it
+// by a ballot (requests do not overlap); lane 0 of the row's first head
+// writes the row's slot and position. A row outside every request keeps its
+// metadata and is not appended.
 template <bool kFp8, bool kReq>
 __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams p) {
     const psk_kv_append_args& a = p.a;
@@ -132,6 +132,22 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
             pos[u] = a.row_positions[row[u]];
         }
     }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        // lanes without a chunk read the slice start (always in bounds) and
+        // drop the value, so the loads need no branch
+        const uint32_t e = has_chunk ? e0 : 0u;
+        const uint16_t* ks = static_cast<const uint16_t*>(a.k_input) +
+                             (uint64_t)row[u] * a.k_row_stride + head[u] * D + e;
+        const uint16_t* vs = static_cast<const uint16_t*>(a.v_input) +
+                             (uint64_t)row[u] * a.v_row_stride + head[u] * D + e;
+        // input rows are read once: non-temporal loads (and stores of the
+        // codes below) measured ~3.5% faster at 2^16 rows than the default
+        // policy (the PSQ kernel's 64 B-per-lane blocks measured slower with it)
+        kw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ks));
+        vw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vs));
+    }
+    // (request rows: the descriptor scan runs while the K/V loads are in flight)
     if constexpr (kReq) {
         static_assert(kUnroll == 1, "request rows: one task group per wave");
         // the wave's rows are consecutive: [row_lo, row_hi] of its live tasks
@@ -143,7 +159,15 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
         slot[0] = 0xFFFFFFFFu;
         pos[0] = 0u;
         bool found = false;
-        for (uint32_t base = 0; base < p.num_req; base += 64u) {
+        // first the 64 descriptors ending at index row_lo (the request of
+        // row R has index <= R when requests come in row order, one row or
+        // more each), then every 64-descriptor window in turn
+        const uint32_t b0 = row_lo >= 63u ? row_lo - 63u : 0u;
+        const uint32_t first = p.num_req > 64u ? min(b0, p.num_req - 64u) : 0u;
+        const uint32_t nwin = (p.num_req + 63u) / 64u;
+        for (uint32_t k = 0; k <= nwin; ++k) {
+            const uint32_t base = k == 0u ? first : (k - 1u) * 64u;
+            if (k != 0u && base == first) continue;   // scanned in the first pass
             const uint32_t r = base + lane;
             uint32_t rb = 0u, rc = 0u, rs = 0u, rp = 0u;
             if (r < p.num_req) {
@@ -172,21 +196,6 @@ __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams 
             const_cast<uint32_t*>(a.row_sequence_slots)[row[0]] = slot[0];
             const_cast<uint32_t*>(a.row_positions)[row[0]] = pos[0];
         }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        // lanes without a chunk read the slice start (always in bounds) and
-        // drop the value, so the loads need no branch
-        const uint32_t e = has_chunk ? e0 : 0u;
-        const uint16_t* ks = static_cast<const uint16_t*>(a.k_input) +
-                             (uint64_t)row[u] * a.k_row_stride + head[u] * D + e;
-        const uint16_t* vs = static_cast<const uint16_t*>(a.v_input) +
-                             (uint64_t)row[u] * a.v_row_stride + head[u] * D + e;
-        // input rows are read once: non-temporal loads (and stores of the
-        // codes below) measured ~3.5% faster at 2^16 rows than the default
-        // policy (the PSQ kernel's 64 B-per-lane blocks measured slower with it)
-        kw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ks));
-        vw[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vs));
     }
     uint32_t page[kUnroll], off[kUnroll];
     bool valid[kUnroll];

@@ -65,11 +65,12 @@ __host__ __device__ inline void page_bytes(const psk_page_copy_args& a, uint64_t
     }
 }
 
-// grid.x = page pairs * layers * 4 tensors (K, V, K-scale, V-scale); every
-// block copies one page body (or one page's scale rows) with 16 B accesses.
-// Copies `bytes` (a multiple of 16) with the workgroup's 256 threads: each
-// thread issues the loads of a 16 KB round (4 x 16 B per thread) before
-// its stores, so several loads are in flight per thread.
+// grid.x = page pairs * layers * 2 tensors (K, V); every block copies one
+// page body and then the page's scale rows of that tensor, with 16 B
+// accesses. Copies `bytes` (a multiple of 16) with the workgroup's 256
+// threads: each thread issues the loads of a 16 KB round (4 x 16 B per
+// thread) before its stores, so several loads are in flight per thread. The
+// bytes are moved once: non-temporal loads and stores.
 __device__ __forceinline__ void copy16_block(uint8_t* d, const uint8_t* s, uint64_t bytes) {
     constexpr int U = 4;
     constexpr uint64_t kRound = 256u * 16u * U;
@@ -78,53 +79,54 @@ __device__ __forceinline__ void copy16_block(uint8_t* d, const uint8_t* s, uint6
 #pragma unroll
         for (int j = 0; j < U; ++j) {
             const uint64_t o = o0 + (uint64_t)j * 256u * 16u;
-            if (o < bytes) v[j] = *reinterpret_cast<const u32x4*>(s + o);
+            if (o < bytes) v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(s + o));
         }
 #pragma unroll
         for (int j = 0; j < U; ++j) {
             const uint64_t o = o0 + (uint64_t)j * 256u * 16u;
-            if (o < bytes) *reinterpret_cast<u32x4*>(d + o) = v[j];
+            if (o < bytes) __builtin_nontemporal_store(v[j], reinterpret_cast<u32x4*>(d + o));
         }
     }
 }
 
+// vec16: d and s 16 B aligned: 16 B accesses over the whole 16 B units,
+// bytes for a tail below 16 B; otherwise bytes throughout.
+__device__ __forceinline__ void copy_bytes(uint8_t* d, const uint8_t* s, uint64_t bytes, uint32_t vec16) {
+    const uint64_t m = vec16 ? bytes & ~(uint64_t)15u : 0u;
+    if (m != 0u) copy16_block(d, s, m);
+    for (uint64_t o = m + threadIdx.x; o < bytes; o += 256u) d[o] = s[o];
+}
+
+// blocks per (page pair, layer): K and V, each body + scale rows
+constexpr uint32_t kCopyTensors = 2u;
+
+// tensor 0: K body + K scale rows, 1: V body + V scale rows. Page p of a
+// pool starts at p x (body or scale row bytes): 16 B accesses need those
+// sizes to be multiples of 16 as well as 16 B aligned pools (vec16).
 __device__ __forceinline__ void copy_one(const psk_page_copy_args& a, uint32_t vec16,
                                          uint32_t dst_page, uint32_t src_page, uint32_t layer,
                                          uint32_t tensor) {
     if (dst_page >= a.dst_num_pages || src_page >= a.src_num_pages) return;
     uint64_t body, scales;
     page_bytes(a, body, scales);
-    const uint8_t* s;
-    uint8_t* d;
-    uint64_t bytes;
-    if (tensor < 2u) {
-        bytes = body;
-        const uint64_t so = ((uint64_t)layer * a.src_num_pages + src_page) * bytes;
-        const uint64_t dof = ((uint64_t)layer * a.dst_num_pages + dst_page) * bytes;
-        s = static_cast<const uint8_t*>(tensor == 0u ? a.src_k : a.src_v) + so;
-        d = static_cast<uint8_t*>(tensor == 0u ? a.dst_k : a.dst_v) + dof;
-    } else {
-        if (scales == 0u) return;
-        bytes = scales;
-        const uint64_t so = ((uint64_t)layer * a.src_num_pages + src_page) * bytes;
-        const uint64_t dof = ((uint64_t)layer * a.dst_num_pages + dst_page) * bytes;
-        s = reinterpret_cast<const uint8_t*>(tensor == 2u ? a.src_k_scale : a.src_v_scale) + so;
-        d = reinterpret_cast<uint8_t*>(tensor == 2u ? a.dst_k_scale : a.dst_v_scale) + dof;
-    }
-    if (vec16 && (bytes % 16u) == 0u) {
-        copy16_block(d, s, bytes);
-    } else {
-        for (uint64_t o = threadIdx.x; o < bytes; o += 256u) d[o] = s[o];
-    }
+    const uint64_t sp = (uint64_t)layer * a.src_num_pages + src_page;
+    const uint64_t dp = (uint64_t)layer * a.dst_num_pages + dst_page;
+    copy_bytes(static_cast<uint8_t*>(tensor == 0u ? a.dst_k : a.dst_v) + dp * body,
+               static_cast<const uint8_t*>(tensor == 0u ? a.src_k : a.src_v) + sp * body, body,
+               vec16 && body % 16u == 0u);
+    if (scales == 0u) return;
+    copy_bytes(reinterpret_cast<uint8_t*>(tensor == 0u ? a.dst_k_scale : a.dst_v_scale) + dp * scales,
+               reinterpret_cast<const uint8_t*>(tensor == 0u ? a.src_k_scale : a.src_v_scale) + sp * scales,
+               scales, vec16 && scales % 16u == 0u);
 }
 
 __global__ __launch_bounds__(256) void copy_pages_kernel(const psk_page_copy_args a,
                                                          uint32_t vec16) {
-    const uint32_t rest = blockIdx.x >> 2;
+    const uint32_t rest = blockIdx.x / kCopyTensors;
     const uint32_t pair = rest / a.num_layers;
     if (pair >= a.num_pairs) return;
     copy_one(a, vec16, a.pairs[pair].dst_page, a.pairs[pair].src_page, rest % a.num_layers,
-             blockIdx.x & 3u);
+             blockIdx.x % kCopyTensors);
 }
 
 // Pairs passed by value in the kernel arguments (host-driven copies: no
@@ -134,15 +136,6 @@ struct InlinePairs {
     psk_page_copy_pair p[kInlinePairs];
 };
 
-__global__ __launch_bounds__(256) void copy_pages_inline_kernel(const psk_page_copy_args a,
-                                                                const InlinePairs pairs,
-                                                                uint32_t vec16) {
-    const uint32_t rest = blockIdx.x >> 2;
-    const uint32_t pair = rest / a.num_layers;
-    if (pair >= a.num_pairs) return;
-    copy_one(a, vec16, pairs.p[pair].dst_page, pairs.p[pair].src_page, rest % a.num_layers,
-             blockIdx.x & 3u);
-}
 
 // ------------------------------------------------------------ copy plan
 // One launch for a whole prefix-cache save or restore: the KV page pairs
@@ -161,11 +154,11 @@ __global__ __launch_bounds__(256) void copy_plan_kernel(const psk_page_copy_args
                                                         const InlineSegments segs, uint32_t nseg,
                                                         uint32_t vec16, uint32_t page_blocks) {
     if (blockIdx.x < page_blocks) {
-        const uint32_t rest = blockIdx.x >> 2;
+        const uint32_t rest = blockIdx.x / kCopyTensors;
         const uint32_t pair = rest / a.num_layers;
         if (pair >= a.num_pairs) return;
         const psk_page_copy_pair pp = a.pairs != nullptr ? a.pairs[pair] : pairs.p[pair];
-        copy_one(a, vec16, pp.dst_page, pp.src_page, rest % a.num_layers, blockIdx.x & 3u);
+        copy_one(a, vec16, pp.dst_page, pp.src_page, rest % a.num_layers, blockIdx.x % kCopyTensors);
         return;
     }
     const uint64_t b = blockIdx.x - page_blocks;
@@ -177,12 +170,8 @@ __global__ __launch_bounds__(256) void copy_plan_kernel(const psk_page_copy_args
     const uint64_t n = min(kSegmentBlockBytes, sg.bytes - off);
     const uint8_t* src = static_cast<const uint8_t*>(sg.src) + off;
     uint8_t* dst = static_cast<uint8_t*>(sg.dst) + off;
-    const bool al = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | n) & 15u) == 0u;
-    if (al) {
-        copy16_block(dst, src, n);
-    } else {
-        for (uint64_t o = threadIdx.x; o < n; o += 256u) dst[o] = src[o];
-    }
+    const bool al = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0u;
+    copy_bytes(dst, src, n, al ? 1u : 0u);
 }
 
 // ------------------------------------------------------------------ fill
@@ -522,7 +511,7 @@ hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair
         psk_page_copy_args a = base;
         a.num_pairs = n;
         a.pairs = device_pairs;
-        const uint64_t page_blocks = (uint64_t)n * a.num_layers * 4u;
+        const uint64_t page_blocks = (uint64_t)n * a.num_layers * kCopyTensors;
         const uint64_t blocks = page_blocks + seg_blocks;
         if (page_blocks > 0x7FFFFFFFull || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
         hipLaunchKernelGGL(copy_plan_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a,
@@ -536,7 +525,7 @@ hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair
         a.pairs = nullptr;
         InlinePairs ip{};
         for (uint32_t i = 0; i < a.num_pairs; ++i) ip.p[i] = pairs[b + i];
-        const uint64_t page_blocks = (uint64_t)a.num_pairs * a.num_layers * 4u;
+        const uint64_t page_blocks = (uint64_t)a.num_pairs * a.num_layers * kCopyTensors;
         const uint32_t ns = b == 0 ? nseg : 0u;
         const uint64_t blocks = page_blocks + (b == 0 ? seg_blocks : 0u);
         if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
@@ -566,7 +555,7 @@ extern "C" int psk_kv_copy_pages(const psk_page_copy_args* a, void* stream) {
     uint32_t vec16 = 0;
     const hipError_t e = psk::copy_validate(a, vec16);
     if (e != hipSuccess) return e;
-    const uint64_t blocks = (uint64_t)a->num_pairs * a->num_layers * 4u;
+    const uint64_t blocks = (uint64_t)a->num_pairs * a->num_layers * psk::kCopyTensors;
     if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
     hipLaunchKernelGGL(psk::copy_pages_kernel, dim3((uint32_t)blocks), dim3(256), 0,
                        static_cast<hipStream_t>(stream), *a, vec16);

@@ -60,11 +60,14 @@ def test_fp8_gather_codes_and_scales(dev):
 
 
 @pytest.mark.parametrize("fp8", [False, True])
-def test_batched_page_copy(dev, fp8):
+@pytest.mark.parametrize("P,H,D", [(16, 4, 256), (7, 3, 100)])
+def test_batched_page_copy(dev, fp8, P, H, D):
     """32 prefix pages copied between two pools (prefix-cache save), every layer,
-    K, V and the FP8 scale rows (paged_kv_pool.cpp:338-542)."""
-    rng = np.random.default_rng(3 + fp8)
-    L, NS, ND, P, H, D = 3, 80, 64, 16, 4, 256
+    K, V and the FP8 scale rows (paged_kv_pool.cpp:338-542). Page 7 x 3 heads
+    x 100: page bodies (2100 / 4200 B) and scale rows (84 B) that are not
+    multiples of 16 B, so pages after the first start unaligned."""
+    rng = np.random.default_rng(3 + fp8 + P)
+    L, NS, ND = 3, 80, 64
     eb = 1 if fp8 else 2
     src = {k: random_fp8_codes(rng, L * NS * P * H * D * eb) for k in "kv"}
     dst = {k: random_fp8_codes(rng, L * ND * P * H * D * eb) for k in "kv"}
