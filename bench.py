@@ -416,7 +416,7 @@ def run_prefix_cache(torch, steps, warmup, dev):
     """Prefix-cache save and restore of a 4096-token prefix: FP8 KV, 6
     attention layers x 4 kv heads x hd 256, page 16 (256 pages), plus the GDN
     slot of the reference's qwen35-0.8B layout (18 states, conv 6144 x 3,
-    16 x 128 x 128 recurrent). Each is one batched copy launch per 32 pages."""
+    16 x 128 x 128 recurrent). Each is one batched copy launch (up to 256 pages)."""
     from phaseshift_amd import state
     L, P, H, D, tokens = 6, 16, 4, 256, 4096
     kv = state.KVPool(2 * tokens // P + 8, P, L, H, D, fp8=True)
@@ -431,6 +431,21 @@ def run_prefix_cache(torch, steps, warmup, dev):
     gi = gdn.info()
     moved = (tokens // P) * L * 2 * (P * H * D + P * H * 4) + gi.conv_slot_bytes + gi.recurrent_slot_bytes
     save_ms, restore_ms = [], []
+
+    save_gpu, restore_gpu = [], []
+
+    def gpu_us(fn):
+        # the stream held busy while the host enqueues: the events then time
+        # the GPU work of the call alone (pair-list upload + copy launch)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1_000_000)
+        e0.record()
+        fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3
 
     def once(record):
         cache.clear()
@@ -448,6 +463,15 @@ def run_prefix_cache(torch, steps, warmup, dev):
             restore_ms.append(t2.ms())
         gdn.release(r.slot)
         r.release()
+        if record:
+            cache.clear()
+            save_gpu.append(gpu_us(lambda: cache.save(seq, gdn, kv, toks)))
+            r = state.Sequence(slots, kv, tokens)
+            gdn.initialize(r.slot)
+            cid = cache.find_longest(toks).id
+            restore_gpu.append(gpu_us(lambda: cache.restore(r, gdn, kv, cid)))
+            gdn.release(r.slot)
+            r.release()
 
     for _ in range(max(warmup, 3)):
         once(False)
@@ -459,7 +483,10 @@ def run_prefix_cache(torch, steps, warmup, dev):
                save_ms=round(s_ms, 4), restore_ms=round(r_ms, 4),
                save_GBps_read_plus_write=round(2 * moved / (s_ms * 1e-3) / 1e9, 1),
                restore_GBps_read_plus_write=round(2 * moved / (r_ms * 1e-3) / 1e9, 1),
-               launches_per_save=int(st.copy_launches // max(1, 2 * (steps + max(warmup, 3)))),
+               save_gpu_us=round(float(np.median(save_gpu)), 2),
+               restore_gpu_us=round(float(np.median(restore_gpu)), 2),
+               save_gpu_GBps_read_plus_write=round(2 * moved / (float(np.median(save_gpu)) * 1e-6) / 1e9, 1),
+               launches_per_save=int(st.copy_launches // max(1, 2 * (steps + max(warmup, 3)) + 2 * steps)),
                reference_copies_per_save=(tokens // P) * L * 4 + 4)
     # the page copy alone, kernel time: the same per-block copy (page body and
     # scale rows of K or V per workgroup) over the sequence's 256 pages x 6

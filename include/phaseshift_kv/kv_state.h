@@ -83,7 +83,7 @@ public:
     // K and V bodies plus the FP8 scale rows (paged_kv_pool.cpp:338-542).
     Status copy_page_from(PageId dst_page, const PagedKVPool& src, PageId src_page,
                           hipStream_t stream);
-    // Any number of (dst, src) page pairs in one launch per 32 pairs.
+    // Any number of (dst, src) page pairs in one launch per 256 pairs.
     Status copy_pages_from(const std::vector<PageId>& dst_pages, const PagedKVPool& src,
                            const std::vector<PageId>& src_pages, hipStream_t stream);
     // The checked copy arguments and pairs of such a copy, for callers that

@@ -15,15 +15,17 @@ struct CopySegment {
     uint64_t bytes;
 };
 constexpr uint32_t kMaxCopySegments = 8;
+// Page pairs a copy launch carries in its kernel arguments (2 KB).
+constexpr uint32_t kInlinePairs = 256;
 
 // Page pairs of `args` (all layers, K, V and scale rows), in launches of up to
-// 32 pairs.
+// kInlinePairs pairs.
 hipError_t copy_pages_host_pairs(const psk_page_copy_args& args, const psk_page_copy_pair* pairs,
                                  uint32_t n, hipStream_t stream);
 // Page pairs (kv may be null when n == 0) and up to kMaxCopySegments segments;
-// one launch when n <= 32 or when device_pairs (room for n pairs, owned by
-// the caller, reused only after this launch in stream order) is given, else
-// one launch per 32 pairs.
+// one launch when n <= kInlinePairs or when device_pairs (room for n pairs,
+// owned by the caller, reused only after this launch in stream order) is
+// given, else one launch per kInlinePairs pairs.
 hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair* pairs, uint32_t n,
                           const CopySegment* segs, uint32_t nseg, hipStream_t stream,
                           psk_page_copy_pair* device_pairs = nullptr);

@@ -131,18 +131,18 @@ __global__ __launch_bounds__(256) void copy_pages_kernel(const psk_page_copy_arg
 
 // Pairs passed by value in the kernel arguments (host-driven copies: no
 // device staging buffer and no ordering hazard on a reused host buffer).
-constexpr uint32_t kInlinePairs = 32;
 struct InlinePairs {
     psk_page_copy_pair p[kInlinePairs];
 };
 
 
 // ------------------------------------------------------------ copy plan
-// One launch for a whole prefix-cache save or restore: the KV page pairs
-// above (blocks [0, page_blocks)) and up to kMaxCopySegments contiguous
-// segments (GDN state slots, DFlash rings), each cut into kSegmentBlockBytes
-// per workgroup.
-constexpr uint64_t kSegmentBlockBytes = 64u * 1024u;
+// One launch for a whole prefix-cache save or restore: up to
+// kMaxCopySegments contiguous segments (GDN state slots, DFlash rings), each
+// cut into kSegmentBlockBytes per workgroup (blocks [0, seg_blocks)), then
+// the KV page pairs above. The segment blocks go first: a launch's tail is
+// then the short page blocks.
+constexpr uint64_t kSegmentBlockBytes = 16u * 1024u;
 struct InlineSegments {
     CopySegment s[kMaxCopySegments];
     uint64_t first_block[kMaxCopySegments + 1];
@@ -152,16 +152,17 @@ struct InlineSegments {
 __global__ __launch_bounds__(256) void copy_plan_kernel(const psk_page_copy_args a,
                                                         const InlinePairs pairs,
                                                         const InlineSegments segs, uint32_t nseg,
-                                                        uint32_t vec16, uint32_t page_blocks) {
-    if (blockIdx.x < page_blocks) {
-        const uint32_t rest = blockIdx.x / kCopyTensors;
+                                                        uint32_t vec16, uint32_t seg_blocks) {
+    if (blockIdx.x >= seg_blocks) {
+        const uint32_t rest = (blockIdx.x - seg_blocks) / kCopyTensors;
         const uint32_t pair = rest / a.num_layers;
         if (pair >= a.num_pairs) return;
         const psk_page_copy_pair pp = a.pairs != nullptr ? a.pairs[pair] : pairs.p[pair];
-        copy_one(a, vec16, pp.dst_page, pp.src_page, rest % a.num_layers, blockIdx.x % kCopyTensors);
+        copy_one(a, vec16, pp.dst_page, pp.src_page, rest % a.num_layers,
+                 (blockIdx.x - seg_blocks) % kCopyTensors);
         return;
     }
-    const uint64_t b = blockIdx.x - page_blocks;
+    const uint64_t b = blockIdx.x;
     uint32_t i = 0;
     while (i + 1u < nseg && segs.first_block[i + 1] <= b) ++i;
     if (i >= nseg || b >= segs.first_block[nseg]) return;
@@ -513,9 +514,9 @@ hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair
         a.pairs = device_pairs;
         const uint64_t page_blocks = (uint64_t)n * a.num_layers * kCopyTensors;
         const uint64_t blocks = page_blocks + seg_blocks;
-        if (page_blocks > 0x7FFFFFFFull || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+        if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
         hipLaunchKernelGGL(copy_plan_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a,
-                           InlinePairs{}, is, nseg, vec16, (uint32_t)page_blocks);
+                           InlinePairs{}, is, nseg, vec16, (uint32_t)seg_blocks);
         return hipGetLastError();
     }
     uint32_t b = 0;
@@ -531,7 +532,7 @@ hipError_t copy_plan_host(const psk_page_copy_args* kv, const psk_page_copy_pair
         if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
         if (blocks > 0) {
             hipLaunchKernelGGL(copy_plan_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a, ip,
-                               is, ns, vec16, (uint32_t)page_blocks);
+                               is, ns, vec16, (uint32_t)(b == 0 ? seg_blocks : 0u));
             const hipError_t le = hipGetLastError();
             if (le != hipSuccess) return le;
         }

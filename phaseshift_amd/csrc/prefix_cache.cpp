@@ -149,10 +149,10 @@ Status PrefixCache::launch_copy(const psk_page_copy_args& kv,
     const auto* sg = static_cast<const psk::CopySegment*>(segs);
     const uint32_t n = static_cast<uint32_t>(pairs.size());
     psk::CopySegment none{};
-    if (n <= 32u || pairs_cap_ < n) {
+    if (n <= psk::kInlinePairs || pairs_cap_ < n) {
         const hipError_t e = psk::copy_plan_host(&kv, pairs.data(), n, nseg ? sg : &none, nseg, stream);
         if (e != hipSuccess) return Status::hip_error("prefix cache copy", e);
-        stats_.copy_launches += std::max<uint64_t>(1, (n + 31) / 32);
+        stats_.copy_launches += std::max<uint64_t>(1, (n + psk::kInlinePairs - 1) / psk::kInlinePairs);
         return Status::make_ok();
     }
     if (pairs_ev_pending_) {

@@ -188,18 +188,19 @@ def test_dflash_ring_roundtrip(dev):
     assert fx.cache.stats().copy_launches == 2
 
 
-def test_many_pages_one_launch(dev):
-    """40 pages (more than the 32 pairs a launch carries in its arguments):
-    the pair list goes to the device first, and the save is still one copy
-    launch; bytes exact."""
-    fx = Fixture(dev, pages=96, capacity=16 * 48, entries=2, max_blocks=48)
-    seq = fx.sequence(16 * 40)
+@pytest.mark.parametrize("npages", [40, 300])
+def test_many_pages_one_launch(dev, npages):
+    """40 pages (their pairs inline in the launch's arguments) and 300 pages
+    (more than the 256 pairs a launch carries: the pair list goes to the
+    device first): each save is one copy launch; bytes exact."""
+    fx = Fixture(dev, pages=2 * npages + 16, capacity=16 * (npages + 8), entries=2, max_blocks=npages + 8)
+    seq = fx.sequence(16 * npages)
     want = fx.page_bytes(seq.block_table())
     want_gdn = fx.gdn_slot(seq.slot)
-    fx.cache.save(seq, fx.gdn, fx.kv, tokens_of(640))
+    fx.cache.save(seq, fx.gdn, fx.kv, tokens_of(16 * npages))
     assert fx.cache.stats().copy_launches == 1
     restored = fx.sequence(0)
-    fx.cache.restore(restored, fx.gdn, fx.kv, fx.cache.find_longest(tokens_of(640)).id)
+    fx.cache.restore(restored, fx.gdn, fx.kv, fx.cache.find_longest(tokens_of(16 * npages)).id)
     torch.cuda.synchronize()
     got = fx.page_bytes(restored.block_table())
     for k in want:
