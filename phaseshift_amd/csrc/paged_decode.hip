@@ -627,9 +627,15 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                 }
             }
             mx = max_xor32(max_xor16(mx));   // lane permutes, no LDS round trip
-            const float m_new = __builtin_fmaxf(m_run, mx);
+            // m_run is the head's softmax reference. BF16 / FP8 (P as a bf16 hi +
+            // lo pair): it moves only when a score exceeds it by more than
+            // kLazyMaxSlack (then P <= 2^slack). PSQ (P x V scale as one bf16
+            // operand): it is the running maximum, so the largest weight of a
+            // row is 1, exact in bf16.
+            const bool moved = mx > m_run + (kPsq ? 0.0f : kLazyMaxSlack);
+            const float m_new = moved ? mx : m_run;
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+            const float alpha = moved ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
             float pv[H][4];
             float psum = 0.0f;
 #pragma unroll
@@ -642,8 +648,8 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
                 }
             l_run = l_run * alpha + psum;
             m_run = m_new;
-            // O is rescaled only when some head's running max moved.
-            if (__any(alpha != 1.0f)) {
+            // O is rescaled only when some head's reference moved.
+            if (__any(moved)) {
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) o[db] *= alpha;
             }
@@ -774,9 +780,10 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
             }
             mx = max_xor32(max_xor16(mx));
             mx = __builtin_fmaxf(mx, row_ror8(mx));   // the other half
-            const float m_new = __builtin_fmaxf(m_run, mx);
+            const bool moved = mx > m_run;   // the running maximum (PSQ, see consume)
+            const float m_new = moved ? mx : m_run;
             const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+            const float alpha = moved ? __builtin_amdgcn_exp2f(m_run - m_use) : 1.0f;
             float pv[4], psum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -785,7 +792,7 @@ __global__ __launch_bounds__(NW * 64, waves_per_simd<FMT>()) void paged_decode_k
             }
             l_run = l_run * alpha + psum;
             m_run = m_new;
-            if (__any(alpha != 1.0f)) {
+            if (__any(moved)) {
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) o[db] *= alpha;
             }
