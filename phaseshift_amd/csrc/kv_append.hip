@@ -85,14 +85,15 @@ __device__ __forceinline__ bool fast_div_ok(float scale) {
 }
 
 // Fast path: head_dim % 8 == 0, head_dim <= 8 * L, every access aligned. A
-// wave runs kUnroll groups of 64/L tasks. The slot/position loads go out
-// first, then the input loads, then the block-table loads (which wait only
-// for slot/position), so the HBM reads overlap the lookup chain (reference
-// skip rules: kv_append.hip:31-55). One group per wave measured fastest at
-// every size, by GPU time per launch from a replayed graph: 128 rows 7.38 ->
-// 3.07 us, 1024 rows 7.65 -> 3.49, 2^16 rows 77.4 -> 76.8 against four groups
-// per wave (the launch-bound small appends of decode steps gain most).
-constexpr int kUnroll = 1;
+// wave runs U groups of 64/L tasks. The slot/position loads go out first,
+// then the input loads, then the block-table loads (which wait only for
+// slot/position), so the HBM reads overlap the lookup chain (reference skip
+// rules: kv_append.hip:31-55). GPU time per launch (replayed graph for the
+// small sizes): one group per wave is fastest up to 2^15 rows (128 rows
+// 3.06 us against 4.41 with two groups and 7.38 with four), two groups from
+// 2^16 rows (2^16 rows 75.5-76.4 us against 78.6-79.3 with one; 2^17 rows
+// 149.8-150.5 against 155.7-156.4); kTwoGroupTasks picks.
+constexpr uint64_t kTwoGroupTasks = 1u << 18;
 
 // kReq: the row metadata of a planned step is formed here instead of by a
 // launch of its own (device_batch_context.hip:69-90): the wave loads 64
@@ -101,7 +102,7 @@ constexpr int kUnroll = 1;
 // by a ballot (requests do not overlap); lane 0 of the row's first head
 // writes the row's slot and position. A row outside every request keeps its
 // metadata and is not appended.
-template <bool kFp8, bool kReq>
+template <bool kFp8, bool kReq, int kUnroll>
 __global__ __launch_bounds__(256) void kv_append_fast_kernel(const AppendParams p) {
     const psk_kv_append_args& a = p.a;
     const uint32_t L = p.lanes_per_head;
@@ -764,11 +765,14 @@ hipError_t launch(const AppendParams& p, hipStream_t stream) {
     const uint64_t tasks_per_wave = 64u >> p.log2_lanes;
     const uint64_t groups = (tasks + tasks_per_wave - 1) / tasks_per_wave;
     const bool fast = p.vec_ok != 0u && p.chunks <= p.lanes_per_head && tasks < 0xFFFFFFFFull;
-    const uint64_t waves = fast ? (groups + kUnroll - 1) / kUnroll : groups;
+    const int U = fast && tasks >= kTwoGroupTasks ? 2 : 1;
+    const uint64_t waves = (groups + U - 1) / U;
     const uint64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    if (fast)
-        hipLaunchKernelGGL((kv_append_fast_kernel<kFp8, false>), dim3((uint32_t)blocks), dim3(256), 0, stream, p);
+    if (fast && U == 2)
+        hipLaunchKernelGGL((kv_append_fast_kernel<kFp8, false, 2>), dim3((uint32_t)blocks), dim3(256), 0, stream, p);
+    else if (fast)
+        hipLaunchKernelGGL((kv_append_fast_kernel<kFp8, false, 1>), dim3((uint32_t)blocks), dim3(256), 0, stream, p);
     else
         hipLaunchKernelGGL(kv_append_generic_kernel<kFp8>, dim3((uint32_t)blocks), dim3(256), 0, stream,
                            p);
@@ -794,7 +798,7 @@ hipError_t launch_req(AppendParams p, const psk_request_descriptor* req, uint32_
     const uint64_t waves = (tasks + tasks_per_wave - 1) / tasks_per_wave;
     const uint64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((kv_append_fast_kernel<kFp8, true>), dim3((uint32_t)blocks), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((kv_append_fast_kernel<kFp8, true, 1>), dim3((uint32_t)blocks), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
