@@ -271,6 +271,87 @@ __device__ __forceinline__ uint32_t psq4_e4m3x4(uint32_t x, bool hi) {
     return mag | ((hi ? x : (x << 4)) & 0x80808080u);
 }
 
+// Exclusive scan of two counters over the NW waves of the workgroup; tx, ty
+// receive the workgroup totals. All NW*64 threads must call it.
+template <int NW>
+__device__ __forceinline__ void block_scan2(uint32_t& x, uint32_t& y, uint32_t& tx, uint32_t& ty,
+                                            uint32_t* tmp /* 2*NW */) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t ix = x, iy = y;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t ux = __shfl_up(ix, o, 64), uy = __shfl_up(iy, o, 64);
+        if (lane >= (uint32_t)o) { ix += ux; iy += uy; }
+    }
+    if (lane == 63u) { tmp[wave] = ix; tmp[NW + wave] = iy; }
+    __syncthreads();
+    uint32_t bx = 0, by = 0;
+    tx = 0; ty = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        if ((uint32_t)w < wave) { bx += tmp[w]; by += tmp[NW + w]; }
+        tx += tmp[w];
+        ty += tmp[NW + w];
+    }
+    x = bx + ix - x;
+    y = by + iy - y;
+}
+
+// Maps a dense unit index to (item, split) over `count` items, item i holding
+// units(i) splits (0: the item is skipped). Units are ordered so that the
+// workgroups of one launch spread evenly over the XCDs (block b runs on XCD
+// b mod 8) and the longest go first: every item's splits but the last
+// (item-major), then the last split of every item. Returns false past the
+// last unit. All NW*64 threads of the workgroup must call it.
+template <int NW, typename UnitsFn>
+__device__ bool find_dense_unit(uint32_t count, UnitsFn units, uint32_t unit, uint32_t& item,
+                                uint32_t& split) {
+    __shared__ uint32_t tmp[2 * NW];
+    __shared__ uint32_t found[2];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t each = (count + NW * 64u - 1u) / (NW * 64u);
+    const uint32_t i0 = min(count, tid * each), i1 = min(count, i0 + each);
+    uint32_t nf = 0, nl = 0;   // this thread's non-last and last units
+    uint32_t u0 = 0;           // units of item i0, kept for the search below
+    for (uint32_t i = i0; i < i1; ++i) {
+        const uint32_t u = units(i);
+        if (i == i0) u0 = u;
+        if (u != 0u) { nf += u - 1u; nl += 1u; }
+    }
+    if (tid == 0) found[0] = 0xFFFFFFFFu;
+    uint32_t pf = nf, pl = nl, F, L;
+    block_scan2<NW>(pf, pl, F, L, tmp);
+    if (unit < F) {
+        if (unit >= pf && unit < pf + nf) {
+            uint32_t k = unit - pf;
+            for (uint32_t i = i0; i < i1; ++i) {
+                const uint32_t u = i == i0 ? u0 : units(i);
+                if (u > 1u) {
+                    if (k < u - 1u) { found[0] = i; found[1] = k; break; }
+                    k -= u - 1u;
+                }
+            }
+        }
+    } else if (unit - F < L) {
+        const uint32_t k0 = unit - F;
+        if (k0 >= pl && k0 < pl + nl) {
+            uint32_t k = k0 - pl;
+            for (uint32_t i = i0; i < i1; ++i) {
+                const uint32_t u = i == i0 ? u0 : units(i);
+                if (u != 0u) {
+                    if (k == 0u) { found[0] = i; found[1] = u - 1u; break; }
+                    --k;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // uniform over the workgroup: scalar registers
+    item = __builtin_amdgcn_readfirstlane(found[0]);
+    split = __builtin_amdgcn_readfirstlane(found[1]);
+    return item != 0xFFFFFFFFu;
+}
+
 // Raises kernel fn's dynamic LDS limit to the CU's 160 KB (less 1 KB of
 // static LDS) on the current device, once per device: `done` holds one bit per
 // device index that is already set up (devices past 63 are set up on every call).

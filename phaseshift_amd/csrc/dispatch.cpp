@@ -273,10 +273,60 @@ namespace {
 DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t tiles_per_group, uint32_t region_rows,
                               uint32_t kv_heads, uint32_t q_heads, uint32_t head_dim,
                               uint32_t kv_dtype, uint32_t page_tokens,
-                              uint32_t max_visible_tokens, uint64_t partial_bytes) {
+                              uint32_t max_visible_tokens, uint64_t partial_bytes,
+                              const std::vector<uint32_t>& tile_visible) {
     DecodeSplit s;
     if (max_visible_tokens < kSplitMinVisible || n_tiles == 0 || kv_heads == 0) return s;
     const uint32_t q_per_kv = q_heads / kv_heads;
+    auto fits = [&](uint64_t splits) {
+        return (uint64_t)region_rows * kv_heads * splits * q_per_kv *
+                   (2u + ::ps::kernel::kPagedAttentionHeadLimit) * sizeof(float) <=
+               partial_bytes;
+    };
+    if (tiles_per_group == 1u && tile_visible.size() == n_tiles) {
+        // Ungrouped tiles split into dense (tile, split) units, dealt
+        // longest first over the XCDs. Cost model, in pages: rounds of units
+        // over the CUs x (pages per split + kTileSplitFixedPages of start-up:
+        // Q split, block-table window, partial write). One workgroup per CU:
+        // a 6-wave workgroup (5-6 heads) puts two waves on SIMDs 0 and 1, and
+        // a second one doubles those (measured on 8 verify blocks of config
+        // 5: 236 units of 80 pages 66 us, 280 units of 66 pages 102 us).
+        constexpr uint64_t kTileSplitFixedPages = 16;
+        const uint32_t nw6 = q_per_kv > 4u && q_per_kv <= 6u;
+        const uint64_t slots =
+            (uint64_t)device_cus() * (nw6 ? 1u : psk::tile_workgroups_per_cu(kv_dtype, head_dim, q_per_kv));
+        const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
+        std::vector<uint64_t> pages(n_tiles);
+        uint64_t longest = 0;
+        for (uint32_t t = 0; t < n_tiles; ++t) {
+            pages[t] = std::min<uint64_t>(max_pages, (tile_visible[t] + page_tokens - 1) / page_tokens);
+            longest = std::max(longest, pages[t]);
+        }
+        auto cost = [&](uint64_t per) {
+            uint64_t units = 0;
+            for (uint64_t pg : pages) units += (pg + per - 1) / per;
+            units *= kv_heads;
+            return ((units + slots - 1) / slots) * (std::min(per, longest) + kTileSplitFixedPages);
+        };
+        uint64_t best_cost = cost(max_pages), best_splits = 1, best_per = 0;
+        const uint64_t top = std::min<uint64_t>(kMaxSplits, std::min<uint64_t>(64, max_pages / kMinPagesPerSplit));
+        for (uint64_t splits = 2; splits <= top; ++splits) {
+            const uint64_t per = (max_pages + splits - 1) / splits;
+            if ((max_pages + per - 1) / per != splits) continue;   // same as a smaller count
+            if (!fits(splits)) break;
+            const uint64_t cst = cost(per);
+            if (cst < best_cost) {
+                best_cost = cst;
+                best_splits = splits;
+                best_per = per;
+            }
+        }
+        if (best_splits > 1) {
+            s.splits = static_cast<uint32_t>(best_splits);
+            s.pages_per_split = static_cast<uint32_t>(best_per);
+        }
+        return s;
+    }
     const uint64_t slots = (uint64_t)device_cus() *
                            psk::tile_workgroups_per_cu(kv_dtype, head_dim, q_per_kv);
     const uint64_t wgs = psk::tile_launch_workgroups(n_tiles, tiles_per_group, q_per_kv, kv_heads);
@@ -425,10 +475,13 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         if (k.tile_count == 0) continue;
         k.row_begin = lo;
         k.rows = hi - lo;
+        std::vector<uint32_t> tile_vis;
+        if (group == 1u)
+            for (const auto& gr : groups) tile_vis.push_back(gr.first);
         const DecodeSplit s = choose_tile_split(
             k.tile_count, k.tiles_per_group, k.rows, c.kv_heads, c.q_heads, c.head_dim,
             static_cast<uint32_t>(step.kv_dtype), c.page_tokens,
-            step.max_visible_tokens, pbytes);
+            step.max_visible_tokens, pbytes, tile_vis);
         k.splits = s.splits;
         k.pages_per_split = s.pages_per_split;
         Status st = push(k);

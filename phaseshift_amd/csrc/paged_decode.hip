@@ -107,81 +107,15 @@ __device__ __forceinline__ uint32_t row_units(const psk_paged_attention_args& a,
     return min(splits, (pc + per - 1u) / per);
 }
 
-// Exclusive scan of two counters over the NW waves of the workgroup.
-template <int NW>
-__device__ __forceinline__ void block_scan2(uint32_t& x, uint32_t& y, uint32_t& tx, uint32_t& ty,
-                                            uint32_t* tmp /* 2*NW */) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    uint32_t ix = x, iy = y;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t ux = __shfl_up(ix, o, 64), uy = __shfl_up(iy, o, 64);
-        if (lane >= (uint32_t)o) { ix += ux; iy += uy; }
-    }
-    if (lane == 63u) { tmp[wave] = ix; tmp[NW + wave] = iy; }
-    __syncthreads();
-    uint32_t bx = 0, by = 0;
-    tx = 0; ty = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        if ((uint32_t)w < wave) { bx += tmp[w]; by += tmp[NW + w]; }
-        tx += tmp[w];
-        ty += tmp[NW + w];
-    }
-    x = bx + ix - x;
-    y = by + iy - y;
-}
-
-// Maps a dense unit index to (row, split). Units are ordered so that the
-// workgroups of one launch spread evenly over the XCDs (block b runs on XCD
-// b mod 8) and the longest go first: every row's splits but the last
-// (row-major), then the last split of every row. Returns false past the last
-// unit. All NW*64 threads of the workgroup must call it.
+// Maps a dense unit index to (row, split) (find_dense_unit over the rows:
+// every row's splits but the last, row-major, then the last split of every
+// row). Returns false past the last unit. All NW*64 threads of the workgroup
+// must call it.
 template <int NW>
 __device__ bool find_unit(const psk_paged_attention_args& a, uint32_t splits, uint32_t pps,
                           uint32_t unit, uint32_t& row, uint32_t& split) {
-    __shared__ uint32_t tmp[2 * NW];
-    __shared__ uint32_t found[2];
-    const uint32_t tid = threadIdx.x;
-    const uint32_t R = a.rows;
-    const uint32_t each = (R + NW * 64u - 1u) / (NW * 64u);
-    const uint32_t r0 = min(R, tid * each), r1 = min(R, r0 + each);
-    uint32_t nf = 0, nl = 0;   // this thread's non-last and last units
-    for (uint32_t r = r0; r < r1; ++r) {
-        const uint32_t u = row_units(a, splits, pps, r);
-        if (u != 0u) { nf += u - 1u; nl += 1u; }
-    }
-    if (tid == 0) found[0] = 0xFFFFFFFFu;
-    uint32_t pf = nf, pl = nl, F, L;
-    block_scan2<NW>(pf, pl, F, L, tmp);
-    if (unit < F) {
-        if (unit >= pf && unit < pf + nf) {
-            uint32_t k = unit - pf;
-            for (uint32_t r = r0; r < r1; ++r) {
-                const uint32_t u = row_units(a, splits, pps, r);
-                if (u > 1u) {
-                    if (k < u - 1u) { found[0] = r; found[1] = k; break; }
-                    k -= u - 1u;
-                }
-            }
-        }
-    } else if (unit - F < L) {
-        const uint32_t k0 = unit - F;
-        if (k0 >= pl && k0 < pl + nl) {
-            uint32_t k = k0 - pl;
-            for (uint32_t r = r0; r < r1; ++r) {
-                const uint32_t u = row_units(a, splits, pps, r);
-                if (u != 0u) {
-                    if (k == 0u) { found[0] = r; found[1] = u - 1u; break; }
-                    --k;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    row = found[0];
-    split = found[1];
-    return row != 0xFFFFFFFFu;
+    return find_dense_unit<NW>(
+        a.rows, [&](uint32_t r) { return row_units(a, splits, pps, r); }, unit, row, split);
 }
 
 constexpr uint32_t kPageWindow = 1024;   // block-table entries staged in LDS per pass

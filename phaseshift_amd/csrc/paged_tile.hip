@@ -158,6 +158,78 @@ constexpr int tile_waves_per_simd(int hpw) { return hpw == 1 ? 3 : 2; }
 // heads (HPW each) of one tile. RT > 1 (NW == RT): wave w owns tile w of a
 // group of RT consecutive tiles of one sequence and HPW heads of the group's
 // head part (blockIdx); the tiles share every staged K/V chunk.
+// Split units of ungrouped tile t: the splits of its visible range that hold
+// pages (0 for a tile the kernels skip). Follows the kernels' own rules: the
+// tile's first row names the sequence, rows of another sequence or past the
+// block table see nothing, and the tile streams the largest visible range of
+// its rows.
+__device__ uint32_t tile_units(const TileParams& p, uint32_t t) {
+    const psk_paged_attention_args& a = p.a;
+    uint32_t r0, nrows;
+    if (p.n_tiles != 0u) {
+        if (t >= p.n_tiles) return 0u;
+        r0 = p.tile_begin[t];
+        nrows = p.tile_rows[t];
+    } else {
+        r0 = t * kTileRows;
+        nrows = kTileRows;
+    }
+    if (r0 >= a.rows) return 0u;
+    nrows = min(nrows, a.rows - r0);
+    if (nrows == 0u) return 0u;
+    const uint32_t slot = a.row_sequence_slots[r0];
+    if (slot >= a.max_sequences) return 0u;
+    const uint64_t cap = (uint64_t)a.block_table_stride * a.page_tokens;
+    // all rows' loads first (rows past the tile repeat its last row)
+    uint32_t sl[kTileRows], ps[kTileRows];
+#pragma unroll
+    for (int j = 0; j < kTileRows; ++j) {
+        const uint32_t r = r0 + min((uint32_t)j, nrows - 1u);
+        sl[j] = a.row_sequence_slots[r];
+        ps[j] = a.row_positions[r];
+    }
+    uint32_t vis_max = 0u;
+#pragma unroll
+    for (int j = 0; j < kTileRows; ++j) {
+        const uint64_t v64 = (uint64_t)ps[j] + 1u;
+        if (sl[j] == slot && v64 <= cap) vis_max = max(vis_max, (uint32_t)v64);
+    }
+    if (vis_max == 0u) return 0u;
+    const uint32_t pc = (vis_max + a.page_tokens - 1u) / a.page_tokens;
+    const uint32_t per = p.pages_per_split != 0u ? p.pages_per_split : (pc + p.splits - 1u) / p.splits;
+    return min(p.splits, (pc + per - 1u) / per);
+}
+
+// Workgroup -> (split, head part, kv head, tile group). Split ungrouped
+// launches (RT == 1, splits > 1) number only the (tile, split) units that hold
+// pages, densely and longest first (find_dense_unit), as blockIdx = unit *
+// kv_heads + kv_head: a verify launch over blocks of different context
+// lengths otherwise leaves most of its grid empty and the active workgroups
+// unevenly spread over the XCDs. Returns false for a workgroup without work.
+template <int NW, int HPW, int RT>
+__device__ __forceinline__ bool tile_workgroup(const TileParams& p, uint32_t qpk, uint32_t& split,
+                                               uint32_t& hpart, uint32_t& kv_head, uint32_t& group) {
+    hpart = 0u;
+    if constexpr (RT == 1) {
+        if (p.splits > 1u) {
+            kv_head = blockIdx.x % p.a.kv_heads;
+            const uint32_t count = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1u) / kTileRows;
+            return find_dense_unit<NW>(
+                count, [&](uint32_t t) { return tile_units(p, t); }, blockIdx.x / p.a.kv_heads, group, split);
+        }
+    }
+    split = blockIdx.x % p.splits;
+    uint32_t rest = blockIdx.x / p.splits;
+    if constexpr (RT > 1) {
+        const uint32_t hparts = (qpk + HPW - 1u) / HPW;
+        hpart = rest % hparts;
+        rest /= hparts;
+    }
+    kv_head = rest % p.a.kv_heads;
+    group = rest / p.a.kv_heads;
+    return true;
+}
+
 template <int FMT, int D, int NW, int HPW, int RT, bool kAl16>
 __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_kernel(const TileParams p) {
     static_assert(RT == 1 || RT == NW, "grouped tiles: one wave per tile");
@@ -200,16 +272,8 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t qpk = a.q_heads / a.kv_heads;
 
-    const uint32_t split = blockIdx.x % p.splits;
-    uint32_t rest = blockIdx.x / p.splits;
-    uint32_t hpart = 0;
-    if constexpr (RT > 1) {
-        const uint32_t hparts = (qpk + HPW - 1u) / HPW;
-        hpart = rest % hparts;
-        rest /= hparts;
-    }
-    const uint32_t kv_head = rest % a.kv_heads;
-    const uint32_t group = rest / a.kv_heads;
+    uint32_t split, hpart, kv_head, group;
+    if (!tile_workgroup<NW, HPW, RT>(p, qpk, split, hpart, kv_head, group)) return;
     const uint32_t rt = RT > 1 ? w : 0u;
     const uint32_t tile = group * RT + rt;
     // the group's first tile names the sequence (workgroup-uniform)
@@ -855,16 +919,8 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t qpk = a.q_heads / a.kv_heads;
 
-    const uint32_t split = blockIdx.x % p.splits;
-    uint32_t rest = blockIdx.x / p.splits;
-    uint32_t hpart = 0;
-    if constexpr (RT > 1) {
-        const uint32_t hparts = (qpk + HPW - 1u) / HPW;
-        hpart = rest % hparts;
-        rest /= hparts;
-    }
-    const uint32_t kv_head = rest % a.kv_heads;
-    const uint32_t group = rest / a.kv_heads;
+    uint32_t split, hpart, kv_head, group;
+    if (!tile_workgroup<NW, HPW, RT>(p, qpk, split, hpart, kv_head, group)) return;
     // the group's first tile names the sequence (workgroup-uniform)
     uint32_t g0;
     if (p.n_tiles != 0u) {

@@ -92,3 +92,35 @@ def test_tile_rows_of_other_sequence_left_unwritten(dev):
     assert np.all(got[10:] == 7.0)
     want = oracle_out(lay, 24, q[:10], slots[:10], pos[:10], lay.block_tables, kp, vp, ks, vs)
     assert_attention_close(got[:10], want, 5e-2, REL_TILE[True], "test_gpu_tiles 4")
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("splits,pps", [(64, 16), (5, 120), (13, 79)])
+def test_split_tiles_of_uneven_lengths(dev, fp8, splits, pps):
+    """Split ungrouped tiles run as dense (tile, split) units, longest first:
+    16-row blocks over contexts from 40 to 9000 tokens leave most of the
+    (tile, split) grid empty. Also covered: a tile whose rows name no valid
+    sequence (skipped, rows untouched) and a tile whose last rows belong to
+    another sequence: the tile kernel leaves their partials alone and the
+    combine then writes those rows from partials nobody produced, so they are
+    not compared (the unsplit contract is
+    test_tile_rows_of_other_sequence_left_unwritten)."""
+    qh, kvh, D = 24, 4, 256
+    rng = np.random.default_rng(41 + splits)
+    prefixes = [9000, 40, 3000, 900, 6000]
+    lens = [p_ + 16 for p_ in prefixes]
+    lay = paged_layout(rng, lens, 16, kvh, D, spare_pages=2)
+    kp, vp, ks, vs = make_pools(lay, fp8, 77, dev)
+    slots = np.concatenate([np.full(16, i, np.uint32) for i in range(len(lens))])
+    pos = np.concatenate([np.arange(p_, p_ + 16, dtype=np.uint32) for p_ in prefixes])
+    slots[16:32] = 1000           # tile 1: no valid sequence
+    slots[16 * 3 + 12:16 * 4] = 2  # tile 3: last 4 rows of another sequence
+    pos[16 * 3 + 12:16 * 4] = np.arange(10, 14)
+    q = bf16_normal(rng, (len(slots), qh * D))
+    got = run_tile(lay, qh, q, slots, pos, kp, vp, ks, vs, splits=splits, pps=pps)
+    assert np.all(got[16:32] == 7.0)
+    cmp = np.ones(len(slots), bool)
+    cmp[16:32] = False
+    cmp[16 * 3 + 12:16 * 4] = False
+    want = oracle_out(lay, qh, q[cmp], slots[cmp], pos[cmp], lay.block_tables, kp, vp, ks, vs)
+    assert_attention_close(got[cmp], want, TOL[fp8], REL_TILE[fp8], f"uneven tiles {splits}/{pps}")
