@@ -18,7 +18,7 @@
 
 namespace psk {
 size_t decode_workgroup_lds_bytes(uint32_t kv_dtype, uint32_t head_dim);
-uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q_per_kv);
+uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q_per_kv, bool grouped);
 hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
                               const void* v, const void* ks, const void* vs,
                               const uint32_t* tile_begin, const uint32_t* tile_rows,
@@ -294,7 +294,7 @@ DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t tiles_per_group, uint32
         constexpr uint64_t kTileSplitFixedPages = 16;
         const uint32_t nw6 = q_per_kv > 4u && q_per_kv <= 6u;
         const uint64_t slots =
-            (uint64_t)device_cus() * (nw6 ? 1u : psk::tile_workgroups_per_cu(kv_dtype, head_dim, q_per_kv));
+            (uint64_t)device_cus() * (nw6 ? 1u : psk::tile_workgroups_per_cu(kv_dtype, head_dim, q_per_kv, false));
         const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;
         std::vector<uint64_t> pages(n_tiles);
         uint64_t longest = 0;
@@ -328,7 +328,7 @@ DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t tiles_per_group, uint32
         return s;
     }
     const uint64_t slots = (uint64_t)device_cus() *
-                           psk::tile_workgroups_per_cu(kv_dtype, head_dim, q_per_kv);
+                           psk::tile_workgroups_per_cu(kv_dtype, head_dim, q_per_kv, tiles_per_group > 1u);
     const uint64_t wgs = psk::tile_launch_workgroups(n_tiles, tiles_per_group, q_per_kv, kv_heads);
     if (wgs >= slots) return s;
     const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;

@@ -154,6 +154,14 @@ constexpr int kTileStages = 4;   // two pairs of chunks (see the main loop)
 // with two (the accumulators of 2 heads take 128 registers at D=256).
 constexpr int tile_waves_per_simd(int hpw) { return hpw == 1 ? 3 : 2; }
 
+// GQA groups that grouped launches take: 1-8 heads per kv head, as head
+// pairs (a 1-head group or the last pair of an odd group computes one head
+// of the pair on zero Q). Measured on 8 prefill chunks of 512 rows (FP8,
+// 4 kv heads, hd 256, contexts 5.3k-14.3k) against one tile per workgroup:
+// 1 head per group 826 -> 484 us, 2 heads 862 -> 511, 4 heads 956 -> 705,
+// 8 heads 1294 -> 1100.
+constexpr bool grouped_heads(uint32_t q_per_kv) { return q_per_kv >= 1u && q_per_kv <= 8u; }
+
 // RT: row tiles per workgroup. RT == 1: the NW waves split the GQA group's
 // heads (HPW each) of one tile. RT > 1 (NW == RT): wave w owns tile w of a
 // group of RT consecutive tiles of one sequence and HPW heads of the group's
@@ -1489,7 +1497,11 @@ hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream
 
 // Waves and heads per wave by group size: up to 4 heads one per wave (4
 // waves, so every SIMD issues part of the DMAs); 5-6 heads one per wave (6
-// waves: two workgroups put 3 waves on every SIMD); 7-8 heads two per wave.
+// waves: two workgroups put 3 waves on every SIMD); 7-8 heads one per wave
+// (8 waves, two on every SIMD). Two heads per wave on 4 waves, the earlier
+// layout for 7-8 heads, spilled over 100 registers at head_dim 256 and ran
+// 2.3-2.7x slower (32/4 heads: 8 verify blocks 156 -> 67 us, a 512-row
+// prefill chunk 839 -> 314 us).
 // 5-6 heads in grouped launches (tiles_per_group == kTileGroup): four waves,
 // one per tile, each on two heads of the group's head part, so each converted
 // K/V fragment feeds two MFMAs and two workgroups put 2 waves on every SIMD.
@@ -1501,7 +1513,7 @@ template <int FMT, int D>
 hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
     const uint32_t qpk = p.a.q_heads / p.a.kv_heads;
     const uint64_t tiles = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1) / kTileRows;
-    const bool grouped = p.tiles_per_group == (uint32_t)kTileGroup && qpk > 4u && qpk <= 6u;
+    const bool grouped = p.tiles_per_group == (uint32_t)kTileGroup && grouped_heads(qpk);
     const uint64_t grid = grouped ? (tiles + kTileGroup - 1) / kTileGroup * ((qpk + 1u) / 2u) * p.a.kv_heads * p.splits
                                   : tiles * p.a.kv_heads * p.splits;
     if (grid == 0u || grid > 0x7FFFFFFFull) return hipErrorInvalidValue;
@@ -1516,7 +1528,7 @@ hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
         if (grouped) return launch_tile_t2<FMT, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
         if (qpk <= 4u) return launch_tile_t2<FMT, D, 4, 1>(p, grid, stream);
         if (qpk <= 6u) return launch_tile_t2<FMT, D, 6, 1>(p, grid, stream);
-        return launch_tile_t2<FMT, D, 4, 2>(p, grid, stream);
+        return launch_tile_t2<FMT, D, 8, 1>(p, grid, stream);
     }
 }
 
@@ -1629,8 +1641,9 @@ hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dty
 
 // Tile workgroups that fit one CU: LDS (block-table window + pipeline
 // stages) and waves (3 per SIMD with one head per wave, 2 with two).
-// kv_dtype: PSK_KV_*.
-uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q_per_kv) {
+// kv_dtype: PSK_KV_*; grouped: a grouped launch (tiles_per_group ==
+// kTileGroup) rather than one tile per workgroup.
+uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q_per_kv, bool grouped) {
     const size_t D = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
     const bool psq = kv_dtype == PSK_KV_PSQ4_W32 || kv_dtype == PSK_KV_PSQ8_W32;
     size_t lds;
@@ -1645,21 +1658,21 @@ uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q
         lds = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * stage;
     }
     const uint32_t by_lds = (uint32_t)((160u * 1024u) / (lds + 64u));
-    // waves: groups of 5-6 heads run grouped (4 two-head waves); otherwise up
-    // to 4 heads one per wave (4 waves), 5-6 one per wave (6), 7-8 two per
-    // wave (4; PSQ one per wave, 8)
-    const bool grouped = q_per_kv > 4u && q_per_kv <= 6u;
-    const uint32_t hpw = grouped || (q_per_kv > 6u && !psq) ? 2u : 1u;
-    const uint32_t nw = grouped || q_per_kv <= 4u ? 4u : q_per_kv <= 6u ? 6u : psq ? 8u : 4u;
+    // waves: grouped launches 4 two-head waves; otherwise up to 4 heads one
+    // per wave (4 waves), 5-6 one per wave (6), 7-8 one per wave (8)
+    grouped = grouped && grouped_heads(q_per_kv);
+    const uint32_t hpw = grouped ? 2u : 1u;
+    const uint32_t nw = grouped || q_per_kv <= 4u ? 4u : q_per_kv <= 6u ? 6u : 8u;
     const uint32_t by_waves = 4u * (uint32_t)tile_waves_per_simd((int)hpw) / nw;
     const uint32_t n = by_lds < by_waves ? by_lds : by_waves;
     return n == 0u ? 1u : n;
 }
 
 // Tiles per workgroup the step planner should group a prefill launch into:
-// kTileGroup for GQA groups of 5-6 heads, every KV format.
+// kTileGroup for every GQA group the tile kernels take (1-8 heads), every KV
+// format.
 uint32_t tile_group_size(uint32_t q_per_kv, uint32_t /*kv_dtype*/) {
-    return q_per_kv > 4u && q_per_kv <= 6u ? (uint32_t)kTileGroup : 1u;
+    return grouped_heads(q_per_kv) ? (uint32_t)kTileGroup : 1u;
 }
 
 // Workgroups of a tile launch of n_tiles (a multiple of tiles_per_group when grouped).

@@ -505,7 +505,8 @@ def test_tile_split_over_psq_pools(dev, fmt):
 
 
 @pytest.mark.parametrize("fmt", [4, 8])
-def test_mixed_step_with_prefill_over_psq_pools(dev, fmt):
+@pytest.mark.parametrize("qh", [24, 8, 32])
+def test_mixed_step_with_prefill_over_psq_pools(dev, fmt, qh):
     """A config-5-shaped step over PSQ pools through the planner: decode rows,
     a 16-row verify block and a 160-row prefill chunk (tile launches), against
     the oracle."""
@@ -517,10 +518,10 @@ def test_mixed_step_with_prefill_over_psq_pools(dev, fmt):
     slots = np.array([0, 1] + [2] * 16 + [3] * 160, np.uint32)
     pos = np.array([2499, 899] + list(range(600, 616)) + list(range(1000, 1160)), np.uint32)
     rows = len(slots)
-    q = bf16_normal(rng, (rows, 24 * 256))
-    out = torch.full((rows, 24 * 256), 7.0, dtype=torch.float32, device=dev)
+    q = bf16_normal(rng, (rows, qh * 256))
+    out = torch.full((rows, qh * 256), 7.0, dtype=torch.float32, device=dev)
     a = ops.attention_args(geom_of(lay), 0, to_dev(q), out, to_dev(slots), to_dev(pos),
-                           to_dev(lay.block_tables), 24)
+                           to_dev(lay.block_tables), qh)
     nbytes = 256 << 20
     part = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
     reqs = [(0, 1, 0, 2500), (1, 1, 0, 900), (2, 16, 1, 616), (18, 160, 2, 1160)]
@@ -529,8 +530,8 @@ def test_mixed_step_with_prefill_over_psq_pools(dev, fmt):
     torch.cuda.synchronize()
     kinds = sorted((k.kind, k.rows) for k in plan.kernels[:plan.count])
     assert kinds == [(0, 2), (1, 16), (1, 160)], kinds
-    want = oracle_attn(lay, fmt, 24, q, slots, pos, lay.block_tables, pools)
-    assert_attention_close(out.cpu().numpy(), want, TOL, REL, "test_gpu_psq 12")
+    want = oracle_attn(lay, fmt, qh, q, slots, pos, lay.block_tables, pools)
+    assert_attention_close(out.cpu().numpy(), want, TOL, REL, f"test_gpu_psq 12 qh={qh}")
 
 
 @pytest.mark.parametrize("fmt", [4, 8])

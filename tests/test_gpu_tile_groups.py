@@ -1,4 +1,4 @@
-"""Grouped prefill tiles (GQA groups of 5-6 heads): the step planner puts
+"""Grouped prefill tiles (GQA groups of 1-8 heads): the step planner puts
 consecutive 16-row tiles of one prefill request into groups of four (one
 workgroup, one wave per tile, the group's K/V chunks staged once) and pads a
 short last group with empty tiles. Ragged requests (partial groups, a partial
@@ -68,6 +68,19 @@ def test_grouped_prefill_vs_oracle(dev, fp8, qh, kvh, split):
                                     [(k.kind, k.row_begin, k.rows, k.splits, k.pages_per_split, k.side)
                                      for k in plan.kernels[:plan.count]])
     assert_attention_close(got, want, TOL[fp8], REL_TILE[fp8], f"grouped prefill fp8={fp8} {qh}/{kvh} split={split}")
+
+
+@pytest.mark.parametrize("qh,fp8,split", [(4, True, False), (8, False, True), (12, True, True),
+                                           (16, True, False), (28, False, False), (32, True, True)])
+def test_grouped_prefill_other_group_sizes(dev, qh, fp8, split):
+    """Grouped launches for GQA groups of 1-8 heads (4 kv heads): head pairs,
+    the second head of an odd group's last pair computed on zero Q and never
+    written."""
+    plan, got, want = grouped_step(dev, fp8, qh, 4, 256, split)
+    tile = [k for k in plan.kernels[:plan.count] if k.kind == 1]
+    assert len(tile) == 1 and (tile[0].splits > 1) == split
+    assert not np.any(got == 7.0)
+    assert_attention_close(got, want, TOL[fp8], REL_TILE[fp8], f"grouped prefill {qh}/4 fp8={fp8} split={split}")
 
 
 def test_grouped_prefill_d128(dev):

@@ -60,6 +60,7 @@ def run_tile(lay, qh, q, slots, pos, kp, vp, ks, vs, splits=1, pps=0, out_dtype=
     (24, 4, 256, 0, 37),       # first chunk of a sequence, ragged last tile
     (8, 4, 128, 130, 50),      # GQA 2
     (16, 2, 64, 64, 33),       # GQA 8 (largest tile group)
+    (32, 4, 256, 600, 40),     # GQA 8 at head_dim 256 (8 one-head waves)
     (4, 4, 128, 90, 20),       # MHA
 ])
 def test_tile_vs_oracle(dev, fp8, qh, kvh, D, prefix, chunk):
