@@ -36,8 +36,11 @@ constexpr uint32_t kMaxTileSplits = 1024;
 constexpr uint32_t kInlineTiles = 256;
 
 // Tiles per workgroup of a grouped launch (consecutive list entries of one
-// sequence; rows == 0 pads a group).
-constexpr int kTileGroup = 4;
+// sequence; rows == 0 pads a group): 8 waves, one per tile, two per SIMD, so
+// one workgroup fills a CU. Against 4 tiles (two workgroups per CU) each
+// staged K/V chunk serves twice the rows: config 5's step 1.140 -> 1.08-1.09
+// ms, its prefill chunks alone 902-923 -> 884 us (alternated builds, one box).
+constexpr int kTileGroup = 8;
 
 struct TileParams {
     psk_paged_attention_args a;
@@ -862,14 +865,14 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     }
 }
 
-// Grouped PSQ prefill tiles. Workgroup = (4 consecutive tiles of one
-// sequence, head pair, kv_head, split), 4 waves, wave w on tile w and both
+// Grouped PSQ prefill tiles. Workgroup = (kTileGroup consecutive tiles of
+// one sequence, head pair, kv_head, split), one wave per tile, wave w on tile w and both
 // heads of the pair (as the FP8 grouped tiles). Each 32-token chunk's PSQ
 // codes and block scales reach LDS by DMA; the workgroup then dequantizes
 // the chunk once, every K and V value to f16(code value x block scale), into
 // an f16 chunk in the BF16 tile layout (16-bit values), and the waves run the
 // f16 MFMA score and PV products on it (Q and P as f16). The dequantization
-// is shared by the 8 (tile, head) products of the workgroup instead of being
+// is shared by the 2 x kTileGroup (tile, head) products of the workgroup instead of being
 // repeated per head, and no per-block scaling of scores or P remains.
 // The scale's power of two rides on the E4M3 -> f16 conversion and its
 // mantissa (exact in f16) multiplies the f16 pairs, so each value is
@@ -1502,9 +1505,9 @@ hipError_t launch_tile_t2(const TileParams& p, uint64_t grid, hipStream_t stream
 // layout for 7-8 heads, spilled over 100 registers at head_dim 256 and ran
 // 2.3-2.7x slower (32/4 heads: 8 verify blocks 156 -> 67 us, a 512-row
 // prefill chunk 839 -> 314 us).
-// 5-6 heads in grouped launches (tiles_per_group == kTileGroup): four waves,
-// one per tile, each on two heads of the group's head part, so each converted
-// K/V fragment feeds two MFMAs and two workgroups put 2 waves on every SIMD.
+// Grouped launches (tiles_per_group == kTileGroup, 1-8 heads): kTileGroup
+// waves, one per tile, each on two heads of the group's head part, so each
+// converted K/V fragment feeds two MFMAs; 2 waves on every SIMD.
 // Wave counts that load the SIMDs unevenly (3 waves per workgroup) lose: the
 // chunk barrier waits on the doubly loaded SIMDs. PSQ grouped launches go to
 // paged_tile_psq_group_kernel (the same workgroup shape on a shared f16
@@ -1662,7 +1665,7 @@ uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q
     // per wave (4 waves), 5-6 one per wave (6), 7-8 one per wave (8)
     grouped = grouped && grouped_heads(q_per_kv);
     const uint32_t hpw = grouped ? 2u : 1u;
-    const uint32_t nw = grouped || q_per_kv <= 4u ? 4u : q_per_kv <= 6u ? 6u : 8u;
+    const uint32_t nw = grouped ? (uint32_t)kTileGroup : q_per_kv <= 4u ? 4u : q_per_kv <= 6u ? 6u : 8u;
     const uint32_t by_waves = 4u * (uint32_t)tile_waves_per_simd((int)hpw) / nw;
     const uint32_t n = by_lds < by_waves ? by_lds : by_waves;
     return n == 0u ? 1u : n;

@@ -1,5 +1,5 @@
 """Grouped prefill tiles (GQA groups of 1-8 heads): the step planner puts
-consecutive 16-row tiles of one prefill request into groups of four (one
+consecutive 16-row tiles of one prefill request into groups of eight (one
 workgroup, one wave per tile, the group's K/V chunks staged once) and pads a
 short last group with empty tiles. Ragged requests (partial groups, a partial
 last tile, a chunk at position 0) and split and unsplit launches, every row
@@ -19,9 +19,9 @@ pytestmark = pytest.mark.gpu
 
 def grouped_step(dev, fp8, qh, kvh, D, split):
     rng = np.random.default_rng(qh * 7 + fp8 + 2 * split)
-    # (prefix, rows, class): 328 rows = 20 full tiles + 8 (6 groups, the last
-    # padded), 136 rows from position 0 (3 groups), 128 rows (2 full groups),
-    # decode rows between them
+    # (prefix, rows, class): 328 rows = 20 full tiles + 8 (3 groups of 8 tiles,
+    # the last padded), 136 rows from position 0 (2 groups, the second one
+    # tile and 7 empty), 128 rows (1 full group), decode rows between them
     reqs_spec = [(1500, 328, 2), (900, 1, 0), (0, 136, 2), (2100, 1, 0), (700, 128, 2),
                  (333, 1, 0)]
     lens = [p + n for p, n, _ in reqs_spec]
