@@ -894,7 +894,8 @@ constexpr size_t tile_pg_lds_bytes() {
 // RT == kTileGroup (grouped prefill): wave w owns tile w of the group and
 // the HPW = 2 heads of the workgroup's head pair. RT == 1 (verify blocks,
 // implicit tiles, other group sizes): the NW waves own HPW = 1 head each of
-// one tile. The first 4 waves issue the DMAs and dequantize.
+// one tile. The first 4 waves issue the DMAs; the first 4 (8 at head_dim
+// 256 with 8 waves) dequantize.
 template <int FMT, int D, int NW, int HPW, int RT, bool kAl16>
 __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_psq_group_kernel(const TileParams p) {
     constexpr int H = 2;
@@ -913,7 +914,10 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     constexpr int KVB_BYTES = H * HSB;
     constexpr int DPW = NL + 1;
     constexpr int kWinBytes = (int)kTilePageWindow * 4;
-    constexpr int QD = D / 4;                         // dims one lane dequantizes per token row
+    // waves that dequantize each chunk: 8 at head_dim 256 with 8 or more
+    // waves (one 32-value block per lane), else 4 (D / 128 blocks per lane)
+    constexpr int NDQ = NW >= 8 && D == 256 ? 8 : 4;
+    constexpr int QD = D / NDQ;                       // dims one lane dequantizes per token row
     // exponent headroom of the dequantized chunk: largest code x 2 x 2^kB
     // (PSQ4 10 x 2 x 2^11 = 40960, PSQ8 448 x 2 x 2^6 = 57344) stays below 65504
     constexpr int kB = FMT == kFmtPsq4 ? 11 : 6;
@@ -1118,12 +1122,13 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
     uint8_t* const cstages = lds + kWinBytes;
     uint8_t* const bst = cstages + CS * CSTAGE;       // the f16 chunk
     const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
-    // dequantization: wave w takes (kind, half) = (w / 2, w % 2), lane (t, q)
-    // token t, dims [QD q, QD (q + 1)). The LDS serves 8 lanes of a 16 B
-    // access per clock; they are 8 tokens of one 16 B column, whose rows sit
-    // 16 B apart, so the 8 accesses hit distinct banks.
-    const uint32_t dq = g;
-    const uint32_t d_kind = w >> 1, d_half = w & 1u, d_tok = n;
+    // dequantization: wave w < NDQ takes (kind, half, dim part) = ((w / 2) % 2,
+    // w % 2, w / 4), lane (t, q) token t, dims [QD j, QD (j + 1)) with j =
+    // (NDQ / 4) q + w / 4. The LDS serves 8 lanes of a 16 B access per clock;
+    // they are 8 tokens of one 16 B column, whose rows sit 16 B apart, so the
+    // 8 accesses hit distinct banks.
+    const uint32_t dq = (uint32_t)(NDQ / 4) * g + (w >> 2);
+    const uint32_t d_kind = (w >> 1) & 1u, d_half = w & 1u, d_tok = n;
 
     for (uint32_t wp = pb; wp < pe; wp += kTilePageWindow) {
         const uint32_t wp_end = min(pe, wp + kTilePageWindow);
@@ -1171,7 +1176,7 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         // code stage st -> f16 chunk: this lane's token row, QD dims, each
         // value scaled by 2^(kB + 127 - Ek) (K) or 2^(kB + 127 - Ev) (V)
         auto dequant = [&](const uint8_t* st, uint8_t* bo) __attribute__((always_inline)) {
-            if (NW > 4 && wu >= 4u) return;
+            if (NW > NDQ && wu >= (uint32_t)NDQ) return;
             const int eshift = d_kind == 0u ? eshift_k : eshift_v;   // wave-uniform
             const uint8_t* cb = st + d_kind * KVC + d_half * HSC + 16u * d_tok;
             const uint8_t* sc = st + 2 * KVC + d_kind * SC_BYTES + d_half * 256 + 4u * d_tok;
