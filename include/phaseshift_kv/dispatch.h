@@ -69,7 +69,7 @@ struct PlannedKernel {
     uint32_t tiles_per_group = 1; // Tile: consecutive tiles per workgroup (rows == 0 pads)
     uint32_t req_first = 0;       // Tile with splits > 1: combine ranges
     uint32_t req_count = 0;
-    uint32_t side = 0;            // 1: runs on the side stream, beside the step's largest tile launch
+    uint32_t side = 0;            // 1 / 2: runs on side lane 1 (decode) / 2 (other tile launches), beside the step's largest tile launch
     uint64_t partial_offset = 0;  // floats into the split-K workspace this launch uses
 };
 

@@ -510,9 +510,11 @@ typedef struct psk_planned_kernel {
     uint32_t rows;
     uint32_t splits;
     uint32_t pages_per_split;
-    uint32_t side;                     /* 1: decode launch on a side stream, concurrent with
-                                          the step's tile launches (forked and joined by
-                                          events on the caller's stream) */
+    uint32_t side;                     /* 0: on the caller's stream; 1 / 2: on side lane 1
+                                          (decode launches) / 2 (the other tile launches),
+                                          concurrent with the step's largest tile launch and
+                                          with each other (forked and joined by events on the
+                                          caller's stream) */
 } psk_planned_kernel;
 
 typedef struct psk_step_plan_t {

@@ -488,12 +488,15 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
         if (!st.ok()) return st;
     }
     // In a step with a large tile launch (>= kForkMinTileRows rows), every
-    // other launch (decode, smaller tile launches) runs on a side stream,
-    // in order there and concurrently with the large one: their workgroups
-    // take the CUs the compute-bound tile launch leaves idle in its tail.
-    // The large launch keeps the start of the split-K workspace, the side
-    // launches share the part after it (they run one after another); when
-    // both parts do not fit, the step stays in order on one stream.
+    // other launch runs beside it on a side lane: the decode launches on lane
+    // 1, the other tile launches (verify blocks) on lane 2, in order within a
+    // lane. Their workgroups take the CUs the compute-bound tile launch leaves
+    // idle (its second round of workgroups, its tail), and the two lanes run
+    // concurrently with each other too. The large launch keeps the start of
+    // the split-K workspace; lane 1 uses the region after it and lane 2 the
+    // region after lane 1's. When those do not fit, every side launch goes to
+    // lane 1 and shares its region (one after another); when even that does
+    // not fit, the step stays in order on one stream.
     const uint32_t qpk = c.kv_heads ? c.q_heads / c.kv_heads : 0u;
     auto need_of = [&](const PlannedKernel& k) -> uint64_t {
         return k.splits > 1 ? (uint64_t)k.rows * c.kv_heads * k.splits * qpk *
@@ -507,15 +510,30 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
             main_k = (int)i;
     if (step.concurrent_decode && main_k >= 0 && plan.count > 1 &&
         plan.kernels[main_k].rows >= kForkMinTileRows) {
-        uint64_t need_side = 0;
-        for (uint32_t i = 0; i < plan.count; ++i)
-            if ((int)i != main_k) need_side = std::max(need_side, need_of(plan.kernels[i]));
+        uint64_t need_side = 0, need1 = 0, need2 = 0;
+        bool any1 = false, any2 = false;
+        for (uint32_t i = 0; i < plan.count; ++i) {
+            if ((int)i == main_k) continue;
+            const uint64_t n = need_of(plan.kernels[i]);
+            need_side = std::max(need_side, n);
+            if (plan.kernels[i].kind == PlannedKernel::Kind::Decode) {
+                need1 = std::max(need1, n);
+                any1 = true;
+            } else {
+                need2 = std::max(need2, n);
+                any2 = true;
+            }
+        }
         const uint64_t side_at = (need_of(plan.kernels[main_k]) + 255u) & ~uint64_t{255};
-        if (need_side == 0 || side_at + need_side <= pbytes) {
+        const uint64_t lane2_at = side_at + ((need1 + 255u) & ~uint64_t{255});
+        const bool two_lanes = any1 && any2 && (need2 == 0 || lane2_at + need2 <= pbytes) &&
+                               (need1 == 0 || side_at + need1 <= pbytes);
+        if (two_lanes || need_side == 0 || side_at + need_side <= pbytes) {
             for (uint32_t i = 0; i < plan.count; ++i) {
                 if ((int)i == main_k) continue;
-                plan.kernels[i].side = 1;
-                plan.kernels[i].partial_offset = side_at / 4u;
+                const bool lane2 = two_lanes && plan.kernels[i].kind != PlannedKernel::Kind::Decode;
+                plan.kernels[i].side = lane2 ? 2u : 1u;
+                plan.kernels[i].partial_offset = (lane2 ? lane2_at : side_at) / 4u;
             }
         }
     }
@@ -524,13 +542,15 @@ Status plan_paged_attention_step(const PagedAttentionStep& step, PagedAttentionP
 
 namespace {
 
-// Side stream and fork/join events per (device, caller stream), created on
-// first use and kept for the life of the process. Default priority, no
-// blocking with the null stream.
+// Side lanes (two streams) and fork/join events per (device, caller
+// stream), created on first use and kept for the life of the process.
+// Default priority, no blocking with the null stream.
 struct SideStream {
-    hipStream_t stream = nullptr;
+    hipStream_t stream = nullptr;    // lane 1
+    hipStream_t stream2 = nullptr;   // lane 2
     hipEvent_t fork = nullptr;
     hipEvent_t join = nullptr;
+    hipEvent_t join2 = nullptr;
 };
 
 SideStream* side_stream_for(hipStream_t main) {
@@ -546,11 +566,15 @@ SideStream* side_stream_for(hipStream_t main) {
     if (it != table.end()) return &it->second;
     SideStream s;
     if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&s.stream2, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join2, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
+        if (s.join2) (void)hipEventDestroy(s.join2);
         if (s.join) (void)hipEventDestroy(s.join);
         if (s.fork) (void)hipEventDestroy(s.fork);
+        if (s.stream2) (void)hipStreamDestroy(s.stream2);
         if (s.stream) (void)hipStreamDestroy(s.stream);
         return nullptr;   // the step then runs in order on `main`
     }
@@ -658,22 +682,32 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
         }
         return hipSuccess;
     }
-    // fork: the side stream starts after the work before this step on
+    bool lane2 = false;
+    for (uint32_t i = 0; i < plan.count; ++i) lane2 = lane2 || plan.kernels[i].side == 2u;
+    // fork: the side lanes start after the work before this step on
     // `stream`; `stream` continues only after the side launches (join)
     hipError_t e = hipEventRecord(side->fork, stream);
     if (e != hipSuccess) return e;
     e = hipStreamWaitEvent(side->stream, side->fork, 0);
+    if (e == hipSuccess && lane2) e = hipStreamWaitEvent(side->stream2, side->fork, 0);
     if (e != hipSuccess) return e;
     // the large launch is enqueued first, so its workgroups take the CUs
-    // first and the side launches fill its tail
+    // first and the side launches fill what it leaves
     for (uint32_t i = 0; e == hipSuccess && i < plan.count; ++i)
         if (!plan.kernels[i].side) e = run(plan.kernels[i], stream);
     for (uint32_t i = 0; e == hipSuccess && i < plan.count; ++i)
-        if (plan.kernels[i].side) e = run(plan.kernels[i], side->stream);
-    // join even after an error, so a capture never ends with the side stream forked
-    const hipError_t j1 = hipEventRecord(side->join, side->stream);
-    const hipError_t j2 = j1 == hipSuccess ? hipStreamWaitEvent(stream, side->join, 0) : j1;
-    return e != hipSuccess ? e : j2;
+        if (plan.kernels[i].side == 1u) e = run(plan.kernels[i], side->stream);
+    for (uint32_t i = 0; e == hipSuccess && i < plan.count; ++i)
+        if (plan.kernels[i].side == 2u) e = run(plan.kernels[i], side->stream2);
+    // join even after an error, so a capture never ends with a side lane forked
+    hipError_t j = hipEventRecord(side->join, side->stream);
+    if (j == hipSuccess) j = hipStreamWaitEvent(stream, side->join, 0);
+    if (lane2) {
+        hipError_t j2 = hipEventRecord(side->join2, side->stream2);
+        if (j2 == hipSuccess) j2 = hipStreamWaitEvent(stream, side->join2, 0);
+        if (j == hipSuccess) j = j2;
+    }
+    return e != hipSuccess ? e : j;
 }
 
 }  // namespace ps::qwen35::runtime

@@ -143,7 +143,8 @@ def test_other_launches_beside_the_largest_tile_launch():
             [(176 + 512 * i, 512, 2) for i in range(8)])
     plan = state.plan_step(args(4272), P.KV_FP8, reqs, 16384, 256 << 20)
     ks = plan.kernels[:plan.count]
-    assert [(k.kind, k.side) for k in ks] == [(0, 1), (1, 1), (1, 0)]
+    # decode on side lane 1, the verify tile launch on lane 2 (each its own workspace region)
+    assert [(k.kind, k.side) for k in ks] == [(0, 1), (1, 2), (1, 0)]
     # small tile steps (largest tile launch under 1024 rows) and decode-only steps never fork
     small = [(i, 1, 0) for i in range(8)] + [(8, 16, 1), (24, 128, 2)]
     plan = state.plan_step(args(152), P.KV_FP8, small, 16384, 256 << 20)
