@@ -613,15 +613,19 @@ hipError_t launch_paged_attention_plan(const PagedAttentionStep& step, const Pag
                                             step.v_scale_pool, tb.data(), tr.data(), k.tile_count,
                                             k.tiles_per_group, parts, k.splits,
                                             k.pages_per_split, stream);
-                for (uint32_t q = 0; e == hipSuccess && k.splits > 1 && q < k.req_count; ++q) {
-                    const StepRequest& r = plan.combine[k.req_first + q];
-                    const PagedAttentionCommonArgs ra =
-                        region_args(a, r.row_begin - k.row_begin, r.row_count);
+                // one combine per run of adjacent requests of the launch (rows of
+                // other requests inside the launch's region hold no partials)
+                for (uint32_t q = 0; e == hipSuccess && k.splits > 1 && q < k.req_count;) {
+                    const uint32_t begin = plan.combine[k.req_first + q].row_begin;
+                    uint32_t end = begin + plan.combine[k.req_first + q].row_count;
+                    for (++q; q < k.req_count && plan.combine[k.req_first + q].row_begin == end; ++q)
+                        end += plan.combine[k.req_first + q].row_count;
+                    const PagedAttentionCommonArgs ra = region_args(a, begin - k.row_begin, end - begin);
                     // the combine reads partials of the region's rows; shift them with it
                     const uint64_t row_floats = (uint64_t)a.kv_heads * k.splits *
                                                 (a.q_heads / a.kv_heads) * (2u + kPagedAttentionHeadLimit);
                     e = launch_attention_paged_split_reduce_ex(
-                        ra, parts + (uint64_t)(r.row_begin - k.row_begin) * row_floats,
+                        ra, parts + (uint64_t)(begin - k.row_begin) * row_floats,
                         k.splits, k.pages_per_split, stream);
                 }
             } else {
