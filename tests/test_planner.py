@@ -174,6 +174,28 @@ def test_other_launches_beside_the_largest_tile_launch():
     assert forked and ordered
 
 
+def test_side_lanes_fall_back_to_one_lane():
+    """Config-5 shape: the decode launch on side lane 1 and the verify launch
+    on lane 2 when the workspace holds both partial regions; both on lane 1,
+    sharing one region, when it holds only the larger of them."""
+    reqs = ([(i, 1, 0) for i in range(48)] + [(48 + 16 * i, 16, 1) for i in range(8)] +
+            [(176 + 512 * i, 512, 2) for i in range(8)])
+
+    def plan_at(cap):
+        ks = state.plan_step(args(4272), P.KV_FP8, reqs, 16384, cap).kernels
+        ks = [ks[i] for i in range(3)]
+        need = [k.rows * 4 * k.splits * 6 * 258 * 4 if k.splits > 1 else 0 for k in ks]
+        return [(k.kind, k.side, k.splits) for k in ks], need
+
+    both, need = plan_at(256 << 20)
+    assert [(k, s) for k, s, _ in both] == [(0, 1), (1, 2), (1, 0)], both
+    assert need[0] > 0 and need[1] > 0 and need[2] == 0
+    # room for the larger region only (the regions start 256-byte aligned)
+    one, need1 = plan_at(max(need[0], need[1]) + 1024)
+    assert need1 == need and [s for _, _, s in one] == [s for _, _, s in both]
+    assert [(k, s) for k, s, _ in one] == [(0, 1), (1, 1), (1, 0)], one
+
+
 def test_args_keep_their_tensors_alive():
     """The argument structs hold raw device pointers; they keep the tensors
     they point into alive (a temporary passed in must not be freed and its
