@@ -837,18 +837,20 @@ __global__ __launch_bounds__(NW * 64, tile_waves_per_simd(HPW)) void paged_tile_
         const uint32_t head = kv_head * qpk + gh;
         const float l_all = sum_xor32(sum_xor16(l_run[i]));
         if (part_row == nullptr) {
+            // one division per (row, head), then a multiply per value
+            const float inv_l = 1.0f / l_all;
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
                 const uint64_t oi =
                     (uint64_t)row * a.output_row_stride + (uint64_t)head * D + db * 16 + 4 * g;
                 if (a.output_dtype == PSK_OUT_F32) {
-                    f32x4 v = o[i][db] / l_all;
+                    f32x4 v = o[i][db] * inv_l;
                     *reinterpret_cast<f32x4*>(static_cast<float*>(a.output) + oi) = v;
                 } else {
                     uint16_t* dst = static_cast<uint16_t*>(a.output) + oi;
                     u32x2 pk;
-                    pk[0] = pack_bf16x2(o[i][db][0] / l_all, o[i][db][1] / l_all);
-                    pk[1] = pack_bf16x2(o[i][db][2] / l_all, o[i][db][3] / l_all);
+                    pk[0] = pack_bf16x2(o[i][db][0] * inv_l, o[i][db][1] * inv_l);
+                    pk[1] = pack_bf16x2(o[i][db][2] * inv_l, o[i][db][3] * inv_l);
                     *reinterpret_cast<u32x2*>(dst) = pk;
                 }
             }
