@@ -292,7 +292,9 @@ DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t tiles_per_group, uint32
         // a second one doubles those (measured on 8 verify blocks of config
         // 5: 236 units of 80 pages 66 us, 280 units of 66 pages 102 us).
         constexpr uint64_t kTileSplitFixedPages = 16;
-        const bool nw6 = q_per_kv > 4u && q_per_kv <= 6u;   // the 6-wave kernel
+        // 5-6 heads: the 6-wave kernel (PSQ: 8 waves, 2 per SIMD, which fill the
+        // registers of a CU's SIMDs at 168 each)
+        const bool nw6 = q_per_kv > 4u && q_per_kv <= 6u;
         const uint64_t slots =
             (uint64_t)device_cus() * (nw6 ? 1u : psk::tile_workgroups_per_cu(kv_dtype, head_dim, q_per_kv, false));
         const uint64_t max_pages = (max_visible_tokens + page_tokens - 1) / page_tokens;

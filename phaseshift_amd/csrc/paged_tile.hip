@@ -1531,8 +1531,11 @@ hipError_t launch_tile_t(const TileParams& p, hipStream_t stream) {
         // PSQ: one shared f16 dequantization per chunk, then f16 MFMAs
         // (paged_tile_psq_group_kernel); ungrouped one head per wave
         if (grouped) return launch_tile_pg<FMT, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
+        // 5-8 heads on 8 waves: at head_dim 256 all 8 share the chunk's
+        // dequantization (5-6 heads: the reference's prefill launcher over
+        // config 5's chunks 2.13 -> 1.87 ms PSQ4, 2.17 -> 1.95 ms PSQ8
+        // against 6 waves with 4 dequantizing)
         if (qpk <= 4u) return launch_tile_pg<FMT, D, 4, 1, 1>(p, grid, stream);
-        if (qpk <= 6u) return launch_tile_pg<FMT, D, 6, 1, 1>(p, grid, stream);
         return launch_tile_pg<FMT, D, 8, 1, 1>(p, grid, stream);
     } else {
         if (grouped) return launch_tile_t2<FMT, D, kTileGroup, 2, kTileGroup>(p, grid, stream);
@@ -1668,11 +1671,12 @@ uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q
         lds = (size_t)kTilePageWindow * 4 + (size_t)kTileStages * stage;
     }
     const uint32_t by_lds = (uint32_t)((160u * 1024u) / (lds + 64u));
-    // waves: grouped launches 4 two-head waves; otherwise up to 4 heads one
-    // per wave (4 waves), 5-6 one per wave (6), 7-8 one per wave (8)
+    // waves: grouped launches kTileGroup two-head waves; otherwise up to 4
+    // heads one per wave (4 waves), 5-6 one per wave (6; PSQ 8), 7-8 one per
+    // wave (8)
     grouped = grouped && grouped_heads(q_per_kv);
     const uint32_t hpw = grouped ? 2u : 1u;
-    const uint32_t nw = grouped ? (uint32_t)kTileGroup : q_per_kv <= 4u ? 4u : q_per_kv <= 6u ? 6u : 8u;
+    const uint32_t nw = grouped ? (uint32_t)kTileGroup : q_per_kv <= 4u ? 4u : q_per_kv <= 6u && !psq ? 6u : 8u;
     const uint32_t by_waves = 4u * (uint32_t)tile_waves_per_simd((int)hpw) / nw;
     const uint32_t n = by_lds < by_waves ? by_lds : by_waves;
     return n == 0u ? 1u : n;
