@@ -104,19 +104,20 @@ def oracle_attention_parallel(geom, q, slots, positions, block_tables, kp, vp, k
         out = np.zeros((rows, H * D), np.float32 if output_dtype == "f32" else np.uint16)
     slots = np.asarray(slots, np.uint32)
     positions = np.asarray(positions, np.uint32)
-    bounds = np.linspace(0, rows, min(workers, rows) + 1).astype(int)
+    n = min(workers, rows)
 
     def job(i):
-        a, b = bounds[i], bounds[i + 1]
-        if a == b:
+        # rows dealt round-robin, so workers share long and short contexts alike
+        idx = np.arange(i, rows, n)
+        if idx.size == 0:
             return
-        o = np.ascontiguousarray(out[a:b])
-        oracle.paged_attention(geom, q[a:b], slots[a:b], positions[a:b], block_tables, kp, vp,
-                               ks, vs, scale, output_dtype, out=o)
-        out[a:b] = o
+        o = np.ascontiguousarray(out[idx])
+        oracle.paged_attention(geom, np.ascontiguousarray(q[idx]), slots[idx], positions[idx],
+                               block_tables, kp, vp, ks, vs, scale, output_dtype, out=o)
+        out[idx] = o
 
-    with ThreadPoolExecutor(len(bounds) - 1) as ex:
-        list(ex.map(job, range(len(bounds) - 1)))
+    with ThreadPoolExecutor(max(n, 1)) as ex:
+        list(ex.map(job, range(n)))
     return out
 
 
