@@ -25,6 +25,7 @@ hipError_t launch_paged_tiles(const psk_paged_attention_args& a, uint32_t kv_dty
                               uint32_t n_tiles, uint32_t tiles_per_group, float* partials,
                               uint32_t splits, uint32_t pages_per_split, hipStream_t stream);
 uint32_t tile_group_size(uint32_t q_per_kv, uint32_t kv_dtype);
+uint32_t tile_dense_units_limit();
 uint64_t tile_launch_workgroups(uint64_t n_tiles, uint32_t tiles_per_group, uint32_t q_per_kv,
                                 uint32_t kv_heads);
 bool paged_tiles_supported(const psk_paged_attention_args& a, uint32_t kv_dtype, const void* k,
@@ -316,6 +317,8 @@ DecodeSplit choose_tile_split(uint32_t n_tiles, uint32_t tiles_per_group, uint32
             const uint64_t per = (max_pages + splits - 1) / splits;
             if ((max_pages + per - 1) / per != splits) continue;   // same as a smaller count
             if (!fits(splits)) break;
+            // the model holds for launches that run as dense units
+            if ((uint64_t)n_tiles * splits > psk::tile_dense_units_limit()) break;
             const uint64_t cst = cost(per);
             if (cst < best_cost) {
                 best_cost = cst;

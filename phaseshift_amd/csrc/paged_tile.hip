@@ -211,20 +211,27 @@ __device__ uint32_t tile_units(const TileParams& p, uint32_t t) {
     return min(p.splits, (pc + per - 1u) / per);
 }
 
+// Largest tiles x splits of a launch whose workgroups take dense units: each
+// workgroup scans every tile's rows to find its unit, which stays cheap (one
+// tile per thread, at most a few thousand workgroups) up to this size; larger
+// launches have enough workgroups to balance without it.
+constexpr uint32_t kDenseTileUnits = 1024;
+
 // Workgroup -> (split, head part, kv head, tile group). Split ungrouped
-// launches (RT == 1, splits > 1) number only the (tile, split) units that hold
-// pages, densely and longest first (find_dense_unit), as blockIdx = unit *
-// kv_heads + kv_head: a verify launch over blocks of different context
-// lengths otherwise leaves most of its grid empty and the active workgroups
-// unevenly spread over the XCDs. Returns false for a workgroup without work.
+// launches (RT == 1, splits > 1, tiles x splits <= kDenseTileUnits) number
+// only the (tile, split) units that hold pages, densely and longest first
+// (find_dense_unit), as blockIdx = unit * kv_heads + kv_head: a verify launch
+// over blocks of different context lengths otherwise leaves most of its grid
+// empty and the active workgroups unevenly spread over the XCDs. Returns
+// false for a workgroup without work.
 template <int NW, int HPW, int RT>
 __device__ __forceinline__ bool tile_workgroup(const TileParams& p, uint32_t qpk, uint32_t& split,
                                                uint32_t& hpart, uint32_t& kv_head, uint32_t& group) {
     hpart = 0u;
     if constexpr (RT == 1) {
-        if (p.splits > 1u) {
+        const uint32_t count = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1u) / kTileRows;
+        if (p.splits > 1u && (uint64_t)count * p.splits <= kDenseTileUnits) {
             kv_head = blockIdx.x % p.a.kv_heads;
-            const uint32_t count = p.n_tiles != 0u ? p.n_tiles : (p.a.rows + kTileRows - 1u) / kTileRows;
             return find_dense_unit<NW>(
                 count, [&](uint32_t t) { return tile_units(p, t); }, blockIdx.x / p.a.kv_heads, group, split);
         }
@@ -1685,6 +1692,10 @@ uint32_t tile_workgroups_per_cu(uint32_t kv_dtype, uint32_t head_dim, uint32_t q
 // Tiles per workgroup the step planner should group a prefill launch into:
 // kTileGroup for every GQA group the tile kernels take (1-8 heads), every KV
 // format.
+// Largest tiles x splits whose split launch runs as dense units (the planner
+// models those launches).
+uint32_t tile_dense_units_limit() { return kDenseTileUnits; }
+
 uint32_t tile_group_size(uint32_t q_per_kv, uint32_t /*kv_dtype*/) {
     return grouped_heads(q_per_kv) ? (uint32_t)kTileGroup : 1u;
 }

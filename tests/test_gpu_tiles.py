@@ -125,3 +125,15 @@ def test_split_tiles_of_uneven_lengths(dev, fp8, splits, pps):
     cmp[16 * 3 + 12:16 * 4] = False
     want = oracle_out(lay, qh, q[cmp], slots[cmp], pos[cmp], lay.block_tables, kp, vp, ks, vs)
     assert_attention_close(got[cmp], want, TOL[fp8], REL_TILE[fp8], f"uneven tiles {splits}/{pps}")
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_split_tiles_beyond_the_dense_limit(dev, fp8):
+    """A split tile launch with more tiles x splits than the dense numbering
+    takes (70 implicit tiles x 16 splits = 1120 > 1024) runs on the plain
+    (tile, kv head, split) grid: a 1120-row chunk after a 200-token prefix,
+    8 pages per split, every row against the oracle."""
+    lay, kp, vp, ks, vs, q, slots, pos = tile_case(91, 200, 1120, 24, 4, 256, fp8, dev)
+    want = oracle_out(lay, 24, q, slots, pos, lay.block_tables, kp, vp, ks, vs)
+    got = run_tile(lay, 24, q, slots, pos, kp, vp, ks, vs, splits=16, pps=8)
+    assert_attention_close(got, want, TOL[fp8], REL_TILE[fp8], "tiles beyond the dense limit")
