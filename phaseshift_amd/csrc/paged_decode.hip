@@ -107,13 +107,30 @@ __device__ __forceinline__ uint32_t row_units(const psk_paged_attention_args& a,
     return min(splits, (pc + per - 1u) / per);
 }
 
-// Maps a dense unit index to (row, split) (find_dense_unit over the rows:
-// every row's splits but the last, row-major, then the last split of every
-// row). Returns false past the last unit. All NW*64 threads of the workgroup
-// must call it.
+// Largest rows x splits of a split launch whose workgroups take dense units:
+// each workgroup scans every row to find its unit, which stays cheap up to
+// this size; larger launches have enough workgroups to balance without it.
+constexpr uint64_t kDenseDecodeUnits = 4096;
+
+// Maps a unit index to (row, split). Split launches up to kDenseDecodeUnits:
+// dense units (find_dense_unit over the rows: every row's splits but the
+// last, row-major, then the last split of every row). Unsplit launches: unit
+// u is row u. Larger split launches: unit u is (u / splits, u % splits).
+// Returns false for a unit without work. All NW*64 threads of the workgroup
+// must call it (the branch taken is uniform).
 template <int NW>
 __device__ bool find_unit(const psk_paged_attention_args& a, uint32_t splits, uint32_t pps,
                           uint32_t unit, uint32_t& row, uint32_t& split) {
+    if (splits == 1u) {
+        row = unit;
+        split = 0u;
+        return unit < a.rows && row_units(a, 1u, pps, unit) != 0u;
+    }
+    if ((uint64_t)a.rows * splits > kDenseDecodeUnits) {
+        row = unit / splits;
+        split = unit % splits;
+        return row < a.rows && split < row_units(a, splits, pps, row);
+    }
     return find_dense_unit<NW>(
         a.rows, [&](uint32_t r) { return row_units(a, splits, pps, r); }, unit, row, split);
 }
