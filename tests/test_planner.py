@@ -174,6 +174,23 @@ def test_other_launches_beside_the_largest_tile_launch():
     assert forked and ordered
 
 
+def test_verify_split_fills_one_round_of_units():
+    """Split verify tiles run as dense (tile, split) units; the planner sizes
+    the split from each block's own context so that the units of config 5's
+    8 verify blocks (contexts 3.7k-15.4k, 4 kv heads) fit one round of one
+    6-wave workgroup per CU (256 CUs) while still splitting."""
+    import math
+    rng = np.random.default_rng(5005)
+    ctx = rng.integers(2048, 16385, 64)
+    vis = [int(c) + 16 for c in ctx[56:]]
+    reqs = [(16 * i, 16, 1, v) for i, v in enumerate(vis)]
+    plan = state.plan_step(args(128), P.KV_FP8, reqs, int(ctx.max()) + 512, 256 << 20)
+    k = plan.kernels[0]
+    assert plan.count == 1 and k.kind == 1 and k.splits > 1
+    units = sum(math.ceil(math.ceil(v / 16) / k.pages_per_split) for v in vis) * 4
+    assert 128 < units <= 256, (k.splits, k.pages_per_split, units)
+
+
 def test_side_lanes_fall_back_to_one_lane():
     """Config-5 shape: the decode launch on side lane 1 and the verify launch
     on lane 2 when the workspace holds both partial regions; both on lane 1,
