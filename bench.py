@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,psq,prefix,graph,loop,dropin")
+    ap.add_argument("--only", default="", help="comma list: main,cfg4,cfg3,append,cfg5,prefill,psq,prefix,graph,loop,dropin")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times), the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -252,6 +252,61 @@ def run_append(torch, ops, rows, steps, warmup, dev, seed=7, graph=False, mode="
         for _ in range(steps):
             cg.replay()
     return ms, rows * APPEND_BYTES_PER_ROW_FP8, t.ms() / (steps * n)
+
+
+def run_fp8_prefill(torch, ops, steps, warmup, dev):
+    """Config 5's 8 prefill chunks of 512 causal rows (contexts U[2k, 16k]
+    before each chunk, seed 5005, FP8 KV, 24/4 heads, hd 256, page 16) alone:
+    through the step planner (grouped tiles, one launch) and through the
+    reference's prefill launcher (implicit 16-row tiles, one launch)."""
+    from phaseshift_amd import KV_FP8, state
+    QH, H, D, P = 24, 4, 256, 16
+    rng = np.random.default_rng(5005)
+    pre = rng.integers(2048, 16385, 8)
+    lens = pre + 512
+    need = (lens + P - 1) // P
+    g = ops.PoolGeometry(1, int(need.sum()), P, H, D)
+    perm = rng.permutation(int(need.sum())).astype(np.int32)
+    bt = np.full((8, int(need.max())), -1, np.int32)
+    o_ = 0
+    for r, n in enumerate(need):
+        bt[r, :n] = perm[o_:o_ + n]
+        o_ += n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    kp = torch.randint(0, 126, (g.pool_elems,), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
+    vp = torch.randint(0, 126, (g.pool_elems,), generator=gen, device=dev, dtype=torch.int32).to(torch.uint8)
+    ks = torch.rand(g.scale_elems, generator=gen, device=dev) * 0.02 + 1e-3
+    vs = torch.rand(g.scale_elems, generator=gen, device=dev) * 0.02 + 1e-3
+    rows = 8 * 512
+    q = torch.randn((rows, QH * D), generator=gen, device=dev).to(torch.bfloat16).view(torch.int16)
+    out = torch.empty((rows, QH * D), dtype=torch.bfloat16, device=dev)
+    slots = torch.from_numpy(np.repeat(np.arange(8), 512).astype(np.int32)).to(dev)
+    pos = torch.from_numpy(np.concatenate([np.arange(p0, p0 + 512) for p0 in pre]).astype(np.int32)).to(dev)
+    btd = torch.from_numpy(bt).to(dev)
+    flops = float(sum(int(p0) * 512 + 512 * 513 // 2 for p0 in pre)) * QH * D * 4
+    a = ops.attention_args(g, 0, q, out, slots, pos, btd, QH)
+    reqs = [(512 * i, 512, 2, int(lens[i])) for i in range(8)]
+    part = torch.empty((64 << 20) // 4, dtype=torch.float32, device=dev)
+    t_ms = {}
+    for kind, reps in (("planner", steps), ("prefill", max(2, steps // 2))):
+        def launch():
+            if kind == "planner":
+                state.plan_step(a, KV_FP8, reqs, int(lens.max()), part.numel() * 4, part, kp, vp, ks, vs,
+                                launch=True)
+            else:
+                ops.paged_attention(g, 0, q, out, slots, pos, btd, kp, vp, QH, ks, vs, kind="prefill")
+
+        warm(torch, launch, warmup)
+        t = Timer(torch)
+        with t:
+            for _ in range(reps):
+                launch()
+        t_ms[kind] = t.ms() / reps
+    tflops = flops / (t_ms["planner"] * 1e-3) / 1e12
+    return dict(rows=rows, tile_ms=round(t_ms["planner"], 4), tile_tflops=round(tflops, 1),
+                frac_of_mfma_peak=round(tflops / 2500.0, 4),
+                reference_launcher_ms=round(t_ms["prefill"], 4), flops=flops)
 
 
 def run_psq(torch, ops, steps, warmup, dev):
@@ -992,8 +1047,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "launches": 5}))
         return
-    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5", "psq",
-                                                     "prefix", "graph", "loop", "dropin"}
+    only = set(args.only.split(",")) if args.only else {"main", "cfg4", "cfg3", "append", "cfg5", "prefill",
+                                                     "psq", "prefix", "graph", "loop", "dropin"}
     extra = {}
 
     # ---- main: north-star point, FP8 batch 64 @ 32k
@@ -1075,6 +1130,9 @@ def main():
     if "loop" in only:
         extra["cfg4_decode_loop_planned"] = run_decode_loop(torch, ops, dev)
 
+    if "prefill" in only:
+        extra["cfg5_prefill_chunks_fp8"] = run_fp8_prefill(torch, ops, max(5, args.steps // 2),
+                                                           args.warmup, dev)
     if "cfg5" in only:
         extra["cfg5_mixed_step"] = run_mixed_step(torch, ops, max(5, args.steps // 2),
                                                   args.warmup, dev)
